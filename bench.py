@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Verify-step benchmark on one MI355X: paged attention (one layer) + acceptance sampling.
+
+Workload: the Llama-3-8B verify step — batch 64, k = 7 drafts (8 query rows per sequence), every
+context 4096 tokens, GQA 32 query / 8 kv heads, head_dim 128, bf16 KV in 16-token blocks through
+a shuffled block table, then acceptance over a 128256-entry vocabulary at temperature 0.8 with
+target logits ~ N(0, 3) and draft logits = target + N(0, 1). Synthetic data from torch's seeded
+generator, resident in HBM before timing starts.
+
+One step = kyro_paged_attention_mq + kyro_spec_verify on the same stream. W warm-up steps, then
+K timed steps between two synchronisations. ``value`` is verified tokens per second,
+sum_b (accepted_b + 1) / seconds per step. HIP events on the launch stream time the attention
+kernel for the roofline entry; the CPU oracle (f32 build) is timed on a bounded sample of the same
+workload for the cpu_baseline entry.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "verified tok/s at bs64 k=7; paged-attn + sampling HBM GB/s (% of peak)"
+
+B, HQ, HKV, D, BS, CTX, K_DRAFT, VOCAB, TEMP = 64, 32, 8, 128, 16, 4096, 7, 128256, 0.8
+
+
+def make_inputs(dev, seed=0):
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q_len = K_DRAFT + 1
+    nb_seq = CTX // BS
+    num_blocks = B * nb_seq
+    kc = torch.randn((num_blocks, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((num_blocks, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
+    table = torch.randperm(num_blocks, generator=g, device=dev).view(B, nb_seq).contiguous()
+    ctx = torch.full((B,), CTX, dtype=torch.int64, device=dev)
+    q_start = (torch.arange(B + 1, device=dev) * q_len).to(torch.int32)
+    q = torch.randn((B * q_len, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+
+    target = torch.randn((B, K_DRAFT + 1, VOCAB), generator=g, device=dev) * 3.0
+    draft = (target[:, :K_DRAFT] + torch.randn((B, K_DRAFT, VOCAB), generator=g, device=dev)).contiguous()
+    eps = 2.0 ** -24
+    probs = torch.softmax(draft.double() / TEMP, dim=-1)
+    cdf = probs.cumsum(-1)
+    u_draw = torch.rand((B, K_DRAFT, 1), generator=g, device=dev, dtype=torch.float64)
+    tokens = torch.searchsorted(cdf, u_draw * cdf[..., -1:]).clamp_(max=VOCAB - 1)
+    tokens = tokens.squeeze(-1).to(torch.int32).contiguous()
+    del probs, cdf
+    u_acc = torch.rand((B, K_DRAFT), generator=g, device=dev).clamp_(eps, 1 - eps)
+    u_res = torch.rand((B,), generator=g, device=dev).clamp_(eps, 1 - eps)
+    nd = torch.full((B,), K_DRAFT, dtype=torch.int32, device=dev)
+    temp = torch.full((B,), TEMP, dtype=torch.float32, device=dev)
+    return dict(q=q, kc=kc, vc=vc, table=table, ctx=ctx, q_start=q_start, target=target,
+                draft=draft, tokens=tokens, u_acc=u_acc, u_res=u_res, nd=nd, temp=temp)
+
+
+def attention_bytes():
+    kv = B * CTX * HKV * D * 2 * 2
+    q = B * (K_DRAFT + 1) * HQ * D * 2
+    return kv + q + q  # bf16 out has the query's size
+
+
+def sampler_bytes():
+    return B * (2 * K_DRAFT + 1) * VOCAB * 4
+
+
+def cpu_baseline(sample: int, threads: int):
+    """Times the f32 build of the CPU oracle on `sample` sequences of the same workload."""
+    import numpy as np
+
+    import oracle
+    from kyro_amd import workloads as wl
+
+    acase = wl.gqa_llama3_8b(batch=sample, ctx=CTX)
+    vcase = wl.verify_llama3_8b(batch=sample, vocab=VOCAB)
+    t0 = time.perf_counter()
+    oracle.paged_attention_mq(acase.query, acase.key_cache, acase.value_cache, acase.block_table,
+                              acase.context_lens, num_heads=HQ, num_kv_heads=HKV, head_dim=D,
+                              block_size=BS, q_start_loc=acase.q_start_loc, threads=threads,
+                              precision="f32")
+    t1 = time.perf_counter()
+    r = oracle.spec_verify(vcase.target, vcase.draft, vcase.draft_tokens, vcase.num_draft,
+                           vcase.temperature, vcase.u_accept, vcase.u_resample, precision="f32")
+    t2 = time.perf_counter()
+    tokens = int(np.sum(r["accepted"] + 1))
+    return {
+        "value": tokens / (t2 - t0),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{sample} of {B} sequences of the same step (attention over ctx {CTX}, "
+                   f"GQA {HQ}/{HKV}, then acceptance over V {VOCAB}); f32 CPU oracle, attention on "
+                   f"{threads} threads ({t1 - t0:.2f} s), acceptance on 1 thread ({t2 - t1:.2f} s)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--path", default="auto", choices=["auto", "vector", "mfma"])
+    ap.add_argument("--splits", type=int, default=0, help="context splits (0 = automatic)")
+    ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} (WORLD_SIZE {world}) is not supported; "
+              "the verify step shards by sequence or kv head with no exchange, so the one-GPU "
+              "figure is the per-GPU rate.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    dev = torch.device("cuda", 0)
+    kyro_amd.lib()
+    x = make_inputs(dev)
+    attn = kyro_amd.PagedAttention(BS, HQ, D, HKV)
+    out = torch.empty((B * (K_DRAFT + 1), HQ, D), dtype=torch.bfloat16, device=dev)
+    acc = torch.empty((B,), dtype=torch.int32, device=dev)
+    toks = torch.empty((B, K_DRAFT + 1), dtype=torch.int32, device=dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        attn.forward_async(x["q"], x["kc"], x["vc"], x["table"], x["ctx"], q_start_loc=x["q_start"],
+                           max_q_len=K_DRAFT + 1, out_dtype=torch.bfloat16, out=out, path=args.path,
+                           num_splits=args.splits)
+        if ev is not None:
+            ev[1].record()
+        kyro_amd.verify_drafts_async(x["target"], x["draft"], x["tokens"], x["nd"], x["temp"],
+                                     x["u_acc"], x["u_res"], out=(acc, toks))
+        if ev is not None:
+            ev[2].record()
+
+    for _ in range(args.warmup):
+        step()
+    kyro_amd.sync(0)
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kyro_amd.sync(0)
+
+    sec_per_step = (t1 - t0) / args.steps
+    attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
+    samp_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
+    emitted = int((acc.cpu() + 1).sum().item())
+    a_bytes, s_bytes = attention_bytes(), sampler_bytes()
+    achieved = a_bytes / (attn_ms * 1e-3) / 1e9
+    step_gbs = (a_bytes + s_bytes) / sec_per_step / 1e9
+
+    traffic = None
+    pmc_path = os.path.join(ROOT, "profiles", "attention_llama3_8b_pmc.json")
+    if os.path.exists(pmc_path):
+        with open(pmc_path) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        baseline = cpu_baseline(args.cpu_sample, threads)
+
+    line = {
+        "metric": METRIC,
+        "value": emitted / sec_per_step,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec_per_step * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: torch generator seed 0 on the GPU (KV, Q ~ N(0,1); target logits ~ N(0,3); "
+                "draft = target + N(0,1); draft tokens drawn from softmax(draft/T))",
+        "config": {
+            "workload": "Llama-3-8B verify step: paged attention (1 layer) + acceptance sampling",
+            "batch": B, "draft_k": K_DRAFT, "context": CTX, "q_heads": HQ, "kv_heads": HKV,
+            "head_dim": D, "block_size": BS, "kv_dtype": "bf16", "vocab": VOCAB,
+            "temperature": TEMP, "logits_dtype": "f32", "attention_path": args.path,
+            "splits": args.splits,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "attn_mfma_kernel" if args.path != "vector" else "attn_vector_kernel",
+            "achieved": achieved,
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBS,
+            "traffic": traffic,
+            "algorithmic_bytes": a_bytes,
+            "avg_launch_us": attn_ms * 1e3,
+        },
+        "cpu_baseline": baseline,
+        "step": {
+            "algorithmic_bytes": a_bytes + s_bytes,
+            "GB_s": step_gbs,
+            "frac_of_peak": step_gbs / PEAK_HBM_GBS,
+            "attention_us": attn_ms * 1e3,
+            "sampler_us": samp_ms * 1e3,
+            "sampler_GB_s": s_bytes / (samp_ms * 1e-3) / 1e9,
+            "tokens_per_step": emitted,
+            "mean_accepted": emitted / B - 1,
+        },
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,188 @@
+/*
+ * kyro_verify.h — C ABI of the MI355X (gfx950) speculative-decoding verify step.
+ *
+ * Two device operations replace the two hot functions of Kyro's verify path:
+ *
+ *   kyro_paged_attention_mq  replaces  PagedAttention::forward
+ *                                       (src/model/attention_kernel.rs:22-31, body :59-136)
+ *   kyro_spec_verify         replaces  SpeculativeDecoder::verify_drafts
+ *                                       (src/speculative.rs:286-339), extended from greedy
+ *                                       argmax-match to p/q rejection sampling with the
+ *                                       sampling conventions of sample_token
+ *                                       (src/worker.rs:267-362)
+ *
+ * Everything else here is plumbing a Rust `extern "C"` block (or ctypes, or C++) binds to:
+ * a per-device context that owns a HIP stream and a scratch arena, opaque device buffers,
+ * and status codes with a thread-local message.
+ *
+ * Conventions
+ *  - Every data pointer passed to a compute entry point is a DEVICE pointer on the context's
+ *    device (from kyro_buf_ptr, hipMalloc, or a torch tensor's data_ptr()).
+ *  - Compute calls are asynchronous on the context's stream. Errors that only the device can
+ *    see (an out-of-range block id, a context length beyond the block table) are latched in a
+ *    device word; the offending blocks are skipped, never dereferenced, and the next
+ *    kyro_sync()/kyro_check() on the context returns KYRO_EINVAL with a message.
+ *  - No C++ exception crosses this boundary. Every function returns a kyro_status; the text of
+ *    the last failure on the calling thread is kyro_last_error().
+ *  - A kyro_ctx may be moved between threads but must not be used by two threads at once
+ *    (the reference model object is Send but not Sync: src/worker.rs:14, src/model/loader.rs:13).
+ */
+#ifndef KYRO_VERIFY_H
+#define KYRO_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KYRO_ABI_VERSION 1
+
+typedef enum kyro_status {
+    KYRO_OK = 0,
+    KYRO_EINVAL = 1,       /* bad argument, shape, or (latched) bad block id / context length */
+    KYRO_EOOM = 2,         /* device allocation failed */
+    KYRO_EHIP = 3,         /* a HIP runtime call failed */
+    KYRO_EUNSUPPORTED = 4  /* valid request this build has no kernel for (e.g. head_dim 96) */
+} kyro_status;
+
+typedef enum kyro_dtype {
+    KYRO_F32 = 0,
+    KYRO_BF16 = 1
+} kyro_dtype;
+
+typedef struct kyro_ctx_s* kyro_ctx;
+typedef struct kyro_buf_s* kyro_buf;
+
+/* ---------------------------------------------------------------- context and errors */
+
+/* Text of the last error raised on the calling thread ("" if none). Never NULL. */
+const char* kyro_last_error(void);
+
+/* ABI version of the loaded library (KYRO_ABI_VERSION at build time). */
+int kyro_abi_version(void);
+
+/* Creates a context on HIP device `device` with its own non-blocking stream. */
+int kyro_ctx_create(int device, kyro_ctx* out);
+int kyro_ctx_destroy(kyro_ctx ctx);
+
+/* Makes subsequent calls on `ctx` run on `hip_stream` (a hipStream_t; NULL = HIP's null stream,
+ * which is what torch's default stream handle 0 denotes). A new context uses a stream of its own
+ * until this is called. The caller keeps ownership of the stream. */
+int kyro_ctx_set_stream(kyro_ctx ctx, void* hip_stream);
+
+/* Grows the context's scratch arena to at least `bytes` now, so later calls do not allocate. */
+int kyro_ctx_reserve(kyro_ctx ctx, size_t bytes);
+
+/* Waits for all work queued on the context's stream, then reports latched device errors. */
+int kyro_sync(kyro_ctx ctx);
+
+/* Reports (and clears) latched device errors after waiting for the stream. Same as kyro_sync. */
+int kyro_check(kyro_ctx ctx);
+
+/* ---------------------------------------------------------------- device buffers */
+
+int kyro_buf_alloc(kyro_ctx ctx, size_t bytes, kyro_buf* out);
+int kyro_buf_free(kyro_buf buf);
+void* kyro_buf_ptr(kyro_buf buf);
+size_t kyro_buf_size(kyro_buf buf);
+/* Synchronous host->device / device->host copies on the context's stream. */
+int kyro_buf_upload(kyro_ctx ctx, kyro_buf dst, size_t dst_offset, const void* src, size_t bytes);
+int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, size_t bytes);
+
+/* ---------------------------------------------------------------- paged attention */
+
+/* Attention-kernel choice. AUTO picks MFMA when the GQA group x queries fill >= 1 16-row tile
+ * with enough rows to pay for it, the vector kernel otherwise (bf16), and always the vector
+ * kernel for f32. */
+typedef enum kyro_attn_path {
+    KYRO_ATTN_AUTO = 0,
+    KYRO_ATTN_VECTOR = 1,
+    KYRO_ATTN_MFMA = 2
+} kyro_attn_path;
+
+/* Mirrors PagedAttention { block_size, num_heads, head_dim, num_kv_heads }
+ * (src/model/attention_kernel.rs:4-9) plus the shapes the Rust side reads off its tensors. */
+typedef struct kyro_paged_attention_params {
+    int32_t block_size;          /* tokens per KV block (Kyro uses 16: src/model/llama.rs:46) */
+    int32_t num_heads;           /* query heads H */
+    int32_t head_dim;            /* D: 64 or 128 */
+    int32_t num_kv_heads;        /* Hkv; H % Hkv == 0; query head h reads kv head h / (H/Hkv) */
+    int32_t batch_size;          /* B */
+    int32_t total_q;             /* rows of `query`: B when q_start_loc is NULL */
+    int32_t max_blocks_per_seq;  /* width of block_table */
+    int32_t num_blocks;          /* leading dim of the caches; ids outside [0,num_blocks) latch EINVAL */
+    int32_t dtype;               /* kyro_dtype of query and caches */
+    int32_t out_dtype;           /* kyro_dtype of out (the reference returns F32) */
+    int32_t causal;              /* 1: query j of a sequence with q_len rows sees keys
+                                    [0, ctx - q_len + j]; 0: every query sees [0, ctx) */
+    float scale;                 /* 0 => 1/sqrt(head_dim) (attention_kernel.rs:69) */
+    int32_t path;                /* kyro_attn_path */
+    int32_t num_splits;          /* context splits per (sequence, kv head); 0 => automatic */
+    int32_t max_q_len;           /* upper bound on query rows per sequence; 0 => 1 without
+                                    q_start_loc, total_q with it (sizes the split workspace;
+                                    a sequence above it latches KYRO_EINVAL) */
+} kyro_paged_attention_params;
+
+/*
+ * Multi-query paged attention over a block-table KV cache.
+ *   query        [total_q, H, D]                    dtype
+ *   q_start_loc  [B+1] int32, rows of sequence b are [q_start_loc[b], q_start_loc[b+1]);
+ *                NULL => one row per sequence (the reference's [B, H, D] query)
+ *   key_cache    [num_blocks, Hkv, block_size, D]   dtype   (attention_kernel.rs:54)
+ *   value_cache  [num_blocks, Hkv, block_size, D]   dtype   (attention_kernel.rs:55)
+ *   block_table  [B, max_blocks_per_seq] int64               (attention_kernel.rs:56)
+ *   context_lens [B] int64; includes the sequence's own query positions (llama.rs:83-84)
+ *   out          [total_q, H, D]                    out_dtype
+ * A sequence with context length 0 gets zeros (attention_kernel.rs:77-84); a partial last
+ * block is truncated (:91-93); block ids may repeat (aliasing, the test at :214).
+ */
+int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* params,
+                            const void* query, const int32_t* q_start_loc,
+                            const void* key_cache, const void* value_cache,
+                            const int64_t* block_table, const int64_t* context_lens,
+                            void* out);
+
+/* ---------------------------------------------------------------- speculative verify */
+
+typedef struct kyro_spec_verify_params {
+    int32_t batch_size;   /* B */
+    int32_t max_draft;    /* kmax: target_logits has kmax+1 rows per sequence, draft kmax */
+    int32_t vocab_size;   /* V */
+    int32_t logits_dtype; /* kyro_dtype of both logits tensors (KYRO_F32) */
+} kyro_spec_verify_params;
+
+/*
+ * Fused acceptance for one verify step, per sequence b with k = num_draft[b] <= kmax and
+ * T = temperature[b]:
+ *   T > 0:  p_i = softmax(target_logits[b,i,:] / T) for i <= k, q_i = softmax(draft_logits[b,i,:] / T)
+ *           for i < k. Draft x_i = draft_tokens[b,i] is accepted while u_accept[b,i] < min(1, p_i(x_i)
+ *           / q_i(x_i)) (q_i(x_i) == 0 accepts). At the first rejection j one token is drawn from
+ *           max(p_j - q_j, 0) / sum with u_resample[b]; after k acceptances the bonus token is drawn
+ *           from p_k. Draws are the inverse-CDF walk in index order of sample_token
+ *           (src/worker.rs:352-360): the first v with cumsum(v) >= u * total; if rounding leaves
+ *           none, the last index with positive mass. A residual that sums to zero falls back to p_j.
+ *   T <= 0: greedy, as verify_drafts (src/speculative.rs:315-323): accept while argmax(target row i)
+ *           == x_i (ties -> lowest index), emit argmax(target row j) at the first mismatch, and
+ *           argmax(target row k) as the bonus after k acceptances.
+ * Outputs: out_accepted[b] = accepted drafts in [0, k]; out_tokens[b, 0..out_accepted[b]] = the
+ * accepted drafts, out_tokens[b, out_accepted[b]] = the correction or bonus token, the rest
+ * 0xFFFFFFFF. Optional (NULL to skip): out_p_draft[b,i] = p_i(x_i), out_q_draft[b,i] = q_i(x_i)
+ * for i < k of sampled sequences (NaN elsewhere and for greedy sequences).
+ * Shapes: target_logits [B, kmax+1, V], draft_logits [B, kmax, V] (may be NULL when every
+ * sequence is greedy or kmax == 0), draft_tokens [B, kmax] uint32, num_draft [B] int32,
+ * temperature [B] f32, u_accept [B, kmax] f32, u_resample [B] f32; uniforms in (0, 1).
+ */
+int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* params,
+                     const void* target_logits, const void* draft_logits,
+                     const uint32_t* draft_tokens, const int32_t* num_draft,
+                     const float* temperature, const float* u_accept, const float* u_resample,
+                     int32_t* out_accepted, uint32_t* out_tokens,
+                     float* out_p_draft, float* out_q_draft);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KYRO_VERIFY_H */

@@ -1,0 +1,79 @@
+// Kernel argument blocks and launchers shared by the host runtime and the .hip kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kyro {
+
+// Bits latched into the context's device error word. The host turns them into KYRO_EINVAL.
+enum ErrorBits : int {
+    ERR_BLOCK_ID = 1,   // block_table entry outside [0, num_blocks)
+    ERR_CTX_LEN = 2,    // context length < 0 or > max_blocks_per_seq * block_size
+    ERR_Q_LAYOUT = 4,   // q_start_loc not monotone, out of [0, total_q], or a q_len > max_q_len
+    ERR_TOKEN = 8,      // draft token id >= vocab_size
+    ERR_NUM_DRAFT = 16, // num_draft outside [0, max_draft]
+    ERR_NO_DRAFT = 32   // a sampled sequence with drafts but no draft_logits
+};
+
+
+enum AttnKernel : int { ATTN_KERNEL_VECTOR = 1, ATTN_KERNEL_MFMA = 2 };
+
+struct AttnArgs {
+    const void* q;
+    const int32_t* q_start;  // [B+1] or nullptr (row b belongs to sequence b)
+    const void* k;
+    const void* v;
+    const int64_t* table;
+    const int64_t* ctx_lens;
+    void* out;
+    float* ws_m;     // [units, splits, rows_cap]
+    float* ws_l;     // [units, splits, rows_cap]
+    float* ws_acc;   // [units, splits, rows_cap, D]
+    int* counters;   // [units], zero between calls
+    int* err;        // device error word
+    int B, H, Hkv, group, D, bs;
+    int max_blocks, num_blocks, total_q, max_q_len, rows_cap;
+    int causal, out_bf16, dtype_bf16;
+    float scale_log2;  // softmax scale * log2(e)
+    int splits, chunk_blocks, units, units_padded;
+};
+
+hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
+
+// Per-sequence decision taken after the acceptance scan.
+struct SpecPlan {
+    int mode;   // SPEC_DONE, SPEC_RESIDUAL (row j of target and draft), SPEC_PLAIN (row j of target)
+    int row;    // j
+    float mt, inv_zt;  // target row max logit, 1 / sum exp
+    float md, inv_zd;  // draft row max logit, 1 / sum exp
+    float c2;          // log2(e) / T
+    float u;           // u_resample
+};
+
+enum SpecMode : int { SPEC_DONE = 0, SPEC_RESIDUAL = 1, SPEC_PLAIN = 2 };
+
+struct SpecArgs {
+    const float* target;  // [B, kmax+1, V]
+    const float* draft;   // [B, kmax, V] or nullptr
+    const uint32_t* draft_tokens;
+    const int32_t* num_draft;
+    const float* temperature;
+    const float* u_accept;
+    const float* u_res;
+    int32_t* out_accepted;
+    uint32_t* out_tokens;
+    float* out_p;
+    float* out_q;
+    float2* stats;   // [B, 2 kmax + 1, C]: {max, sum exp} (sampled) or {max, index bits} (greedy)
+    SpecPlan* plan;  // [B]
+    float2* csum;    // [B, C]: {residual mass, p mass} of the resampled row, per chunk
+    int* err;
+    int B, kmax, V, C, chunk, vec4;
+};
+
+hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
+
+constexpr int kSpecChunk = 8192;  // vocabulary entries per workgroup in the streaming passes
+
+}  // namespace kyro

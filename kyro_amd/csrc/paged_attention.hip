@@ -1,0 +1,612 @@
+// Multi-query paged attention for the verify step on gfx950.
+//
+// Replaces PagedAttention::forward / paged_attention_kernel (src/model/attention_kernel.rs:22-136)
+// for q_len >= 1 query rows per sequence, in the reference's layouts:
+//   query [total_q, H, D], caches [num_blocks, Hkv, block_size, D], block_table [B, max_blocks]
+//   int64, context_lens [B] int64, out [total_q, H, D].
+//
+// Work decomposition. One workgroup (4 waves) owns one (sequence, kv head, context split).
+// Every query row that reads that kv head — the GQA group x the sequence's q_len rows — is
+// processed together, so each K/V byte is read from HBM exactly once. The 4 waves stream disjoint
+// blocks of the split with private online-softmax state and merge through LDS at the end; splits
+// of one (sequence, kv head) merge through a small workspace, in the last workgroup to finish.
+// Workgroups are numbered so that all splits of one (sequence, kv head) land on one XCD (the
+// dispatcher deals workgroups round-robin over the 8 XCDs), keeping that merge in one L2.
+//
+// Two kernels share that frame:
+//  * attn_mfma_kernel (bf16, D = 128, block_size 16): scores S^T = K Q^T and O^T = V^T P^T on
+//    v_mfma_f32_16x16x32_bf16. K and V are loaded straight from HBM into the MFMA operand
+//    layouts with 128-bit loads — K as 16 token rows x 64 contiguous bytes per instruction, V as
+//    4 full 256-byte token rows per instruction — so no LDS staging is needed; V is transposed in
+//    registers with v_perm_b32. The softmax'd S^T fragment is already the P^T operand of the PV
+//    product, and the output column of O^T is the query row, so the per-row rescale stays in the
+//    lane that owns the row's softmax state.
+//  * attn_vector_kernel (f32 or bf16, D = 64 or 128, any block size): 16 lanes per token row,
+//    4 token rows per wave per step, dot products reduced with DPP inside each 16-lane row.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace kyro {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+struct SeqInfo {
+    int b, kvh, q0, q_len, rows, nblk;
+    int ctx;
+    bool ok;
+};
+
+// Workgroup -> (unit = sequence * Hkv + kv head, split). Consecutive workgroups go to different
+// XCDs; the splits of one unit share (blockIdx % 8) and therefore one XCD.
+__device__ __forceinline__ bool map_workgroup(const AttnArgs& a, int& unit, int& split) {
+    const int wg = blockIdx.x;
+    const int xcd = wg & 7;
+    const int local = wg >> 3;
+    unit = (local / a.splits) * 8 + xcd;
+    split = local % a.splits;
+    return unit < a.units;
+}
+
+__device__ SeqInfo seq_info(const AttnArgs& a, int unit) {
+    SeqInfo s;
+    s.b = unit / a.Hkv;
+    s.kvh = unit % a.Hkv;
+    const int64_t ctx = a.ctx_lens[s.b];
+    s.ok = true;
+    if (ctx < 0 || ctx > (int64_t)a.max_blocks * a.bs) {
+        if (threadIdx.x == 0) latch_error(a.err, ERR_CTX_LEN);
+        s.ok = false;
+    }
+    int q0 = s.b, q1 = s.b + 1;
+    if (a.q_start) {
+        q0 = a.q_start[s.b];
+        q1 = a.q_start[s.b + 1];
+    }
+    if (q0 < 0 || q1 < q0 || q1 > a.total_q || q1 - q0 > a.max_q_len) {
+        if (threadIdx.x == 0) latch_error(a.err, ERR_Q_LAYOUT);
+        s.ok = false;
+    }
+    s.ctx = s.ok ? (int)ctx : 0;
+    s.q0 = q0;
+    s.q_len = s.ok ? q1 - q0 : 0;
+    s.rows = s.q_len * a.group;
+    s.nblk = (s.ctx + a.bs - 1) / a.bs;
+    return s;
+}
+
+__device__ __forceinline__ int num_splits_for(const AttnArgs& a, int nblk) {
+    const int n = (nblk + a.chunk_blocks - 1) / a.chunk_blocks;
+    return n < 1 ? 1 : n;
+}
+
+// Output row of local row n (n = j * group + head-in-group) of a sequence.
+__device__ __forceinline__ size_t out_row(const AttnArgs& a, const SeqInfo& si, int n) {
+    const int j = n / a.group;
+    const int hg = n - j * a.group;
+    return (size_t)(si.q0 + j) * a.H + (size_t)si.kvh * a.group + hg;
+}
+
+__device__ __forceinline__ int64_t checked_block(const AttnArgs& a, int b, int i) {
+    const int64_t blk = a.table[(size_t)b * a.max_blocks + i];
+    if (blk < 0 || blk >= a.num_blocks) {
+        latch_error(a.err, ERR_BLOCK_ID);
+        return -1;
+    }
+    return blk;
+}
+
+template <int D>
+__device__ __forceinline__ void store_row4(const AttnArgs& a, size_t row, int d, float x0, float x1,
+                                           float x2, float x3) {
+    if (a.out_bf16) {
+        uint2 w;
+        w.x = pack_bf16x2(x0, x1);
+        w.y = pack_bf16x2(x2, x3);
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + row * D + d) = w;
+    } else {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + row * D + d) =
+            make_float4(x0, x1, x2, x3);
+    }
+}
+
+// Shared LDS frame of one workgroup: the merged (unnormalised) accumulator of up to R rows,
+// each wave's running max, each wave's rescaled row sums.
+template <int R, int D>
+struct Frame {
+    static constexpr int kStride = D + 4;  // pad rows to spread LDS banks
+    float acc[R * kStride];
+    float m[kWaves][R];
+    float l[kWaves][R];
+    float mx[R];
+    int last;
+};
+
+template <int R, int D>
+__device__ __forceinline__ void frame_zero(Frame<R, D>& f) {
+    for (int i = threadIdx.x; i < R * Frame<R, D>::kStride; i += kThreads) f.acc[i] = 0.f;
+}
+
+// After every wave has added its rescaled accumulator: either normalise and store the rows
+// (single split) or park the split's partial state in the workspace.
+template <int R, int D>
+__device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int split, int nsplit,
+                            int row0, int nrows, Frame<R, D>& f) {
+    constexpr int Q = D / 4;
+    if (nsplit == 1) {
+        for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
+            const int n = idx / Q, d = (idx - n * Q) * 4;
+            float L = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) L += f.l[w][n];
+            const float inv = L > 0.f ? 1.f / L : 0.f;
+            const float* src = &f.acc[n * Frame<R, D>::kStride + d];
+            store_row4<D>(a, out_row(a, si, row0 + n), d, src[0] * inv, src[1] * inv, src[2] * inv,
+                          src[3] * inv);
+        }
+        return;
+    }
+    const size_t base = ((size_t)unit * a.splits + split) * a.rows_cap;
+    for (int n = threadIdx.x; n < nrows; n += kThreads) {
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) L += f.l[w][n];
+        a.ws_m[base + row0 + n] = f.mx[n];
+        a.ws_l[base + row0 + n] = L;
+    }
+    for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
+        const int n = idx / Q, d = (idx - n * Q) * 4;
+        const float* src = &f.acc[n * Frame<R, D>::kStride + d];
+        *reinterpret_cast<float4*>(a.ws_acc + (base + row0 + n) * D + d) =
+            make_float4(src[0], src[1], src[2], src[3]);
+    }
+}
+
+// Called by every workgroup of a multi-split unit once all its rows are parked. The last
+// workgroup to arrive merges the splits and writes the output, then re-arms the counter.
+template <int R, int D>
+__device__ void merge_splits(const AttnArgs& a, const SeqInfo& si, int unit, int nsplit,
+                             Frame<R, D>& f) {
+    __threadfence();  // release this workgroup's partials (agent scope)
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int prev = atomicAdd(&a.counters[unit], 1);
+        f.last = (prev == nsplit - 1);
+    }
+    __syncthreads();
+    if (!f.last) return;
+    __threadfence();  // acquire the other workgroups' partials
+    constexpr int Q = D / 4;
+    const size_t base = (size_t)unit * a.splits * a.rows_cap;
+    for (int idx = threadIdx.x; idx < si.rows * Q; idx += kThreads) {
+        const int n = idx / Q, d = (idx - n * Q) * 4;
+        float M = kNegInf;
+        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_m[base + (size_t)s * a.rows_cap + n]);
+        float L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (M != kNegInf) {
+            for (int s = 0; s < nsplit; ++s) {
+                const size_t r = base + (size_t)s * a.rows_cap + n;
+                const float w = fast_exp2(a.ws_m[r] - M);
+                L += w * a.ws_l[r];
+                const float4 v = *reinterpret_cast<const float4*>(a.ws_acc + r * D + d);
+                acc.x += w * v.x;
+                acc.y += w * v.y;
+                acc.z += w * v.z;
+                acc.w += w * v.w;
+            }
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    }
+    if (threadIdx.x == 0) a.counters[unit] = 0;
+}
+
+// ------------------------------------------------------------------------------ MFMA kernel
+
+constexpr int kMfmaD = 128;
+constexpr int kMfmaBS = 16;
+
+template <int NT>
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+    constexpr int D = kMfmaD;
+    constexpr int R = NT * 16;
+    __shared__ Frame<R, D> frame;
+
+    int unit, split;
+    if (!map_workgroup(a, unit, split)) return;
+    const SeqInfo si = seq_info(a, unit);
+    if (!si.ok) return;
+    const int nsplit = num_splits_for(a, si.nblk);
+    if (split >= nsplit) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;  // MFMA row/column within a 16-tile
+    const int g = lane >> 4;  // 16-lane group
+    const int blk_begin = split * a.chunk_blocks;
+    const int blk_end = min(si.nblk, blk_begin + a.chunk_blocks);
+    const uint16_t* __restrict__ qp = reinterpret_cast<const uint16_t*>(a.q);
+    const uint16_t* __restrict__ kp = reinterpret_cast<const uint16_t*>(a.k);
+    const uint16_t* __restrict__ vp = reinterpret_cast<const uint16_t*>(a.v);
+    const size_t head_stride = (size_t)kMfmaBS * D;               // one (block, kv head) slab
+    const size_t block_stride = (size_t)a.Hkv * head_stride;      // one block, all kv heads
+    const size_t kv_off = (size_t)si.kvh * head_stride;
+
+    const int nrows_total = si.rows > 0 ? si.rows : 1;
+    for (int row0 = 0; row0 < nrows_total; row0 += R) {
+        const int nrows = min(R, si.rows - row0);
+        frame_zero(frame);
+
+        // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
+        bf16x8 qB[NT][4];
+        int vis[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = row0 + nt * 16 + r;
+            if (n < si.rows) {
+                const int j = n / a.group;
+                const size_t qrow = out_row(a, si, n);
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                    qB[nt][s] = __builtin_bit_cast(bf16x8, load16(qp + qrow * D + 32 * s + 8 * g));
+                vis[nt] = a.causal ? si.ctx - si.q_len + j + 1 : si.ctx;
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+                vis[nt] = 0;
+            }
+        }
+
+        float m[NT], lsum[NT];
+        f32x4 O[8][NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            m[nt] = kNegInf;
+            lsum[nt] = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+        // Each wave takes pairs of blocks (32 tokens = one K-step of the PV MFMA).
+        for (int pb = blk_begin + 2 * wave; pb < blk_end; pb += 2 * kWaves) {
+            int64_t blk[2];
+            blk[0] = checked_block(a, si.b, pb);
+            blk[1] = (pb + 1 < blk_end) ? checked_block(a, si.b, pb + 1) : -1;
+
+            bf16x8 kA[2][4];
+            uint4 vin[2][4];
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi) {
+                if (blk[bi] >= 0) {
+                    const uint16_t* kb = kp + (size_t)blk[bi] * block_stride + kv_off + (size_t)r * D + 8 * g;
+                    const uint16_t* vb = vp + (size_t)blk[bi] * block_stride + kv_off + (size_t)(4 * g) * D + 8 * r;
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) kA[bi][s] = __builtin_bit_cast(bf16x8, load16(kb + 32 * s));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vin[bi][e] = load16(vb + (size_t)e * D);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) kA[bi][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vin[bi][e] = make_uint4(0, 0, 0, 0);
+                }
+            }
+
+            // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
+            f32x4 S[2][NT];
+#pragma unroll
+            for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kA[bi][s], qB[nt][s], c, 0, 0, 0);
+                    S[bi][nt] = c;
+                }
+
+            bf16x8 pB[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float sv[8];
+                float mx = kNegInf;
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = (pb + bi) * kMfmaBS + 4 * g + e;
+                        const bool ok = blk[bi] >= 0 && t < vis[nt];
+                        const float x = ok ? S[bi][nt][e] * a.scale_log2 : kNegInf;
+                        sv[bi * 4 + e] = x;
+                        mx = fmaxf(mx, x);
+                    }
+                mx = fmaxf(mx, shfl_xor_f(mx, 16));
+                mx = fmaxf(mx, shfl_xor_f(mx, 32));
+                const float m_new = fmaxf(m[nt], mx);
+                const float mref = (m_new == kNegInf) ? 0.f : m_new;
+                const float alpha = fast_exp2(m[nt] - mref);
+                float ps = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    sv[i] = fast_exp2(sv[i] - mref);
+                    ps += sv[i];
+                }
+                lsum[nt] = lsum[nt] * alpha + ps;
+                if (__any(m_new > m[nt] && m[nt] != kNegInf)) {
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) O[dt][nt] *= alpha;
+                }
+                m[nt] = m_new;
+                uint4 pw;
+                pw.x = pack_bf16x2(sv[0], sv[1]);
+                pw.y = pack_bf16x2(sv[2], sv[3]);
+                pw.z = pack_bf16x2(sv[4], sv[5]);
+                pw.w = pack_bf16x2(sv[6], sv[7]);
+                pB[nt] = __builtin_bit_cast(bf16x8, pw);
+            }
+
+            // O^T += V^T P^T. A operand of d-tile dt: lane row r <-> head dim 8 r + dt, k-slots
+            // 8 g .. 8 g + 7 <-> tokens 4 g .. 4 g + 3 of block 0 then of block 1.
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+                const int w = dt >> 1;
+                uint4 av;
+                av.x = __builtin_amdgcn_perm(((const uint32_t*)&vin[0][1])[w], ((const uint32_t*)&vin[0][0])[w], sel);
+                av.y = __builtin_amdgcn_perm(((const uint32_t*)&vin[0][3])[w], ((const uint32_t*)&vin[0][2])[w], sel);
+                av.z = __builtin_amdgcn_perm(((const uint32_t*)&vin[1][1])[w], ((const uint32_t*)&vin[1][0])[w], sel);
+                av.w = __builtin_amdgcn_perm(((const uint32_t*)&vin[1][3])[w], ((const uint32_t*)&vin[1][2])[w], sel);
+                const bf16x8 A = __builtin_bit_cast(bf16x8, av);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, pB[nt], O[dt][nt], 0, 0, 0);
+            }
+        }
+
+        // Row sums: each lane summed its own 8 tokens per pair; fold the four 16-lane groups.
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            lsum[nt] += shfl_xor_f(lsum[nt], 16);
+            lsum[nt] += shfl_xor_f(lsum[nt], 32);
+        }
+
+        // Merge the four waves: common max, rescale, add into LDS.
+        if (g == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) frame.m[wave][nt * 16 + r] = m[nt];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = nt * 16 + r;
+            float M = frame.m[0][n];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, frame.m[w][n]);
+            const float f = (m[nt] == kNegInf) ? 0.f : fast_exp2(m[nt] - M);
+            if (g == 0) {
+                frame.l[wave][n] = lsum[nt] * f;
+                if (wave == 0) frame.mx[n] = M;
+            }
+            float* dst = &frame.acc[n * Frame<R, D>::kStride + 32 * g];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) atomicAdd(dst + 8 * e + dt, O[dt][nt][e] * f);
+        }
+        __syncthreads();
+        frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
+        __syncthreads();
+    }
+    if (nsplit > 1) merge_splits<R, D>(a, si, unit, nsplit, frame);
+}
+
+// ---------------------------------------------------------------------------- vector kernel
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+    template <int N>
+    __device__ static __forceinline__ void load(const float* p, float (&x)[N]) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(p + i);
+            x[i] = v.x;
+            x[i + 1] = v.y;
+            x[i + 2] = v.z;
+            x[i + 3] = v.w;
+        }
+    }
+};
+template <>
+struct Elem<uint16_t> {
+    template <int N>
+    __device__ static __forceinline__ void load(const uint16_t* p, float (&x)[N]) {
+#pragma unroll
+        for (int i = 0; i < N; i += 8) {
+            const uint4 v = load16(p + i);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4 && i + 2 * k < N; ++k) {
+                x[i + 2 * k] = bf16_lo(w[k]);
+                x[i + 2 * k + 1] = bf16_hi(w[k]);
+            }
+        }
+    }
+};
+// D = 64 bf16 gives 4 elements (8 bytes) per lane.
+template <>
+__device__ __forceinline__ void Elem<uint16_t>::load<4>(const uint16_t* p, float (&x)[4]) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    x[0] = bf16_lo(v.x);
+    x[1] = bf16_hi(v.x);
+    x[2] = bf16_lo(v.y);
+    x[3] = bf16_hi(v.y);
+}
+
+constexpr int kVecRows = 8;
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
+    constexpr int R = kVecRows;
+    constexpr int DPL = D / 16;  // head-dim elements per lane
+    __shared__ Frame<R, D> frame;
+
+    int unit, split;
+    if (!map_workgroup(a, unit, split)) return;
+    const SeqInfo si = seq_info(a, unit);
+    if (!si.ok) return;
+    const int nsplit = num_splits_for(a, si.nblk);
+    if (split >= nsplit) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r = lane & 15;  // head-dim slice [r * DPL, r * DPL + DPL)
+    const int g = lane >> 4;  // token row within the wave's 4
+    const T* __restrict__ qp = reinterpret_cast<const T*>(a.q);
+    const T* __restrict__ kp = reinterpret_cast<const T*>(a.k);
+    const T* __restrict__ vp = reinterpret_cast<const T*>(a.v);
+    const int t_begin = split * a.chunk_blocks * a.bs;
+    const int t_end = min(si.ctx, (split + 1) * a.chunk_blocks * a.bs);
+
+    const int nrows_total = si.rows > 0 ? si.rows : 1;
+    for (int row0 = 0; row0 < nrows_total; row0 += R) {
+        const int nrows = min(R, si.rows - row0);
+        frame_zero(frame);
+        float q[R][DPL];
+        int vis[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int n = row0 + i;
+            if (n < si.rows) {
+                Elem<T>::load(qp + out_row(a, si, n) * D + r * DPL, q[i]);
+                vis[i] = a.causal ? si.ctx - si.q_len + n / a.group + 1 : si.ctx;
+            } else {
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) q[i][d] = 0.f;
+                vis[i] = 0;
+            }
+        }
+        float m[R], l[R], acc[R][DPL];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            m[i] = kNegInf;
+            l[i] = 0.f;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) acc[i][d] = 0.f;
+        }
+
+        for (int t0 = t_begin + 4 * wave; t0 < t_end; t0 += 4 * kWaves) {
+            const int t = t0 + g;
+            const bool tok_ok = t < t_end;
+            int64_t blk = -1;
+            if (tok_ok) blk = checked_block(a, si.b, t / a.bs);
+            float kx[DPL], vx[DPL];
+            if (blk >= 0) {
+                const size_t off = (((size_t)blk * a.Hkv + si.kvh) * a.bs + (t % a.bs)) * D + r * DPL;
+                Elem<T>::load(kp + off, kx);
+                Elem<T>::load(vp + off, vx);
+            } else {
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) kx[d] = vx[d] = 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                float s = 0.f;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) s += q[i][d] * kx[d];
+                s = row16_sum(s);
+                s = (blk >= 0 && t < vis[i]) ? s * a.scale_log2 : kNegInf;
+                const float m_new = fmaxf(m[i], s);
+                const float mref = (m_new == kNegInf) ? 0.f : m_new;
+                const float alpha = fast_exp2(m[i] - mref);
+                const float p = fast_exp2(s - mref);
+                l[i] = l[i] * alpha + p;
+#pragma unroll
+                for (int d = 0; d < DPL; ++d) acc[i][d] = acc[i][d] * alpha + p * vx[d];
+                m[i] = m_new;
+            }
+        }
+
+        // Fold the four token rows of the wave (16-lane groups), then merge waves in LDS.
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            float M = fmaxf(m[i], shfl_xor_f(m[i], 16));
+            M = fmaxf(M, shfl_xor_f(M, 32));
+            const float f = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - M);
+            l[i] *= f;
+            l[i] += shfl_xor_f(l[i], 16);
+            l[i] += shfl_xor_f(l[i], 32);
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                float x = acc[i][d] * f;
+                x += shfl_xor_f(x, 16);
+                x += shfl_xor_f(x, 32);
+                acc[i][d] = x;
+            }
+            m[i] = M;
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) frame.m[wave][i] = m[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            float M = frame.m[0][i];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, frame.m[w][i]);
+            const float f = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - M);
+            if (lane == 0) {
+                frame.l[wave][i] = l[i] * f;
+                if (wave == 0) frame.mx[i] = M;
+            }
+            if (g == 0) {
+#pragma unroll
+                for (int d = 0; d < DPL; ++d)
+                    atomicAdd(&frame.acc[i * Frame<R, D>::kStride + r * DPL + d], acc[i][d] * f);
+            }
+        }
+        __syncthreads();
+        frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
+        __syncthreads();
+    }
+    if (nsplit > 1) merge_splits<R, D>(a, si, unit, nsplit, frame);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------ launcher
+
+int attention_rows_per_mfma_tile() { return 16; }
+
+hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t stream) {
+    const dim3 block(kThreads);
+    const dim3 grid((unsigned)(a.units_padded * a.splits));
+    if (grid.x == 0) return hipSuccess;
+    if (path == ATTN_KERNEL_MFMA) {
+        const int nt = (a.group * a.max_q_len + 15) / 16;
+        switch (nt <= 1 ? 1 : nt >= 5 ? 5 : nt) {
+            case 1: attn_mfma_kernel<1><<<grid, block, 0, stream>>>(a); break;
+            case 2: attn_mfma_kernel<2><<<grid, block, 0, stream>>>(a); break;
+            case 3: attn_mfma_kernel<3><<<grid, block, 0, stream>>>(a); break;
+            case 4: attn_mfma_kernel<4><<<grid, block, 0, stream>>>(a); break;
+            default: attn_mfma_kernel<5><<<grid, block, 0, stream>>>(a); break;
+        }
+    } else {
+        const bool bf16 = a.dtype_bf16;
+        if (a.D == 128) {
+            if (bf16) attn_vector_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
+            else attn_vector_kernel<float, 128><<<grid, block, 0, stream>>>(a);
+        } else {
+            if (bf16) attn_vector_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
+            else attn_vector_kernel<float, 64><<<grid, block, 0, stream>>>(a);
+        }
+    }
+    return hipGetLastError();
+}
+
+}  // namespace kyro

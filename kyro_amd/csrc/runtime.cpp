@@ -1,0 +1,450 @@
+// Host runtime behind include/kyro_verify.h: contexts, device buffers, scratch arena, argument
+// validation, kernel selection and error reporting. No C++ exception leaves this file: each
+// entry point catches everything and returns a kyro_status (the Rust caller is built with
+// panic = "abort", Cargo.toml:41, so an unwinding exception would take the process down).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "kernels.hpp"
+#include "kyro_verify.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define KYRO_HIP(expr)                                                                        \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return fail(e_ == hipErrorOutOfMemory ? KYRO_EOOM : KYRO_EHIP, "%s failed: %s", \
+                        #expr, hipGetErrorString(e_));                                        \
+    } while (0)
+
+// Makes `dev` current for the scope and restores the caller's device afterwards.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t status = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) status = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+
+struct kyro_ctx_s {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;  // per-call scratch, stream-ordered
+    size_t arena_bytes = 0;
+    int* counters = nullptr;  // attention split counters, zero between calls
+    size_t counters_n = 0;
+    int* err = nullptr;  // device error word
+};
+
+struct kyro_buf_s {
+    int device = 0;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+namespace {
+
+int ensure_arena(kyro_ctx ctx, size_t bytes) {
+    if (bytes <= ctx->arena_bytes) return KYRO_OK;
+    const size_t want = align_up(std::max(bytes, ctx->arena_bytes * 3 / 2), size_t(1) << 20);
+    KYRO_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->arena) KYRO_HIP(hipFree(ctx->arena));
+    ctx->arena = nullptr;
+    ctx->arena_bytes = 0;
+    KYRO_HIP(hipMalloc(&ctx->arena, want));
+    ctx->arena_bytes = want;
+    return KYRO_OK;
+}
+
+int ensure_counters(kyro_ctx ctx, size_t n) {
+    if (n <= ctx->counters_n) return KYRO_OK;
+    const size_t want = align_up(std::max(n, ctx->counters_n * 2), 1024);
+    KYRO_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->counters) KYRO_HIP(hipFree(ctx->counters));
+    ctx->counters = nullptr;
+    ctx->counters_n = 0;
+    KYRO_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->counters), want * sizeof(int)));
+    KYRO_HIP(hipMemset(ctx->counters, 0, want * sizeof(int)));
+    ctx->counters_n = want;
+    return KYRO_OK;
+}
+
+int check_ctx(kyro_ctx ctx) {
+    if (!ctx) return fail(KYRO_EINVAL, "null kyro_ctx");
+    return KYRO_OK;
+}
+
+int sync_and_report(kyro_ctx ctx) {
+    KYRO_HIP(hipStreamSynchronize(ctx->stream));
+    int err = 0;
+    KYRO_HIP(hipMemcpy(&err, ctx->err, sizeof(int), hipMemcpyDeviceToHost));
+    if (err == 0) return KYRO_OK;
+    KYRO_HIP(hipMemset(ctx->err, 0, sizeof(int)));
+    std::string msg = "device-side validation failed:";
+    if (err & kyro::ERR_BLOCK_ID) msg += " block_table entry outside [0, num_blocks);";
+    if (err & kyro::ERR_CTX_LEN) msg += " context length < 0 or > max_blocks_per_seq * block_size;";
+    if (err & kyro::ERR_Q_LAYOUT) msg += " q_start_loc not monotone / out of range, or q_len > max_q_len;";
+    if (err & kyro::ERR_TOKEN) msg += " draft token id >= vocab_size;";
+    if (err & kyro::ERR_NUM_DRAFT) msg += " num_draft outside [0, max_draft];";
+    if (err & kyro::ERR_NO_DRAFT) msg += " draft_logits is NULL but a sampled sequence has drafts;";
+    return fail(KYRO_EINVAL, "%s", msg.c_str());
+}
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return fail(KYRO_EOOM, "host allocation failed");
+    } catch (const std::exception& e) {
+        return fail(KYRO_EHIP, "internal error: %s", e.what());
+    } catch (...) {
+        return fail(KYRO_EHIP, "internal error");
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kyro_last_error(void) { return g_last_error.c_str(); }
+
+int kyro_abi_version(void) { return KYRO_ABI_VERSION; }
+
+int kyro_ctx_create(int device, kyro_ctx* out) {
+    return guarded([&]() -> int {
+        if (!out) return fail(KYRO_EINVAL, "kyro_ctx_create: out is null");
+        *out = nullptr;
+        int n = 0;
+        KYRO_HIP(hipGetDeviceCount(&n));
+        if (device < 0 || device >= n)
+            return fail(KYRO_EINVAL, "kyro_ctx_create: device %d not in [0, %d)", device, n);
+        DeviceGuard dg(device);
+        KYRO_HIP(dg.status);
+        kyro_ctx ctx = new kyro_ctx_s();
+        ctx->device = device;
+        hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->err), sizeof(int));
+        if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
+        if (e != hipSuccess) {
+            if (ctx->err) (void)hipFree(ctx->err);
+            if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+            delete ctx;
+            return fail(KYRO_EHIP, "kyro_ctx_create: %s", hipGetErrorString(e));
+        }
+        ctx->stream = ctx->own_stream;
+        *out = ctx;
+        return KYRO_OK;
+    });
+}
+
+int kyro_ctx_destroy(kyro_ctx ctx) {
+    return guarded([&]() -> int {
+        if (!ctx) return KYRO_OK;
+        DeviceGuard dg(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+        if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+        if (ctx->arena) (void)hipFree(ctx->arena);
+        if (ctx->counters) (void)hipFree(ctx->counters);
+        if (ctx->err) (void)hipFree(ctx->err);
+        if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return KYRO_OK;
+    });
+}
+
+int kyro_ctx_set_stream(kyro_ctx ctx, void* hip_stream) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        hipStream_t next = static_cast<hipStream_t>(hip_stream);
+        if (next == ctx->stream) return KYRO_OK;
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        // The arena is ordered on one stream at a time: drain the old one before switching.
+        KYRO_HIP(hipStreamSynchronize(ctx->stream));
+        ctx->stream = next;
+        return KYRO_OK;
+    });
+}
+
+int kyro_ctx_reserve(kyro_ctx ctx, size_t bytes) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        return ensure_arena(ctx, bytes);
+    });
+}
+
+int kyro_sync(kyro_ctx ctx) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        return sync_and_report(ctx);
+    });
+}
+
+int kyro_check(kyro_ctx ctx) { return kyro_sync(ctx); }
+
+int kyro_buf_alloc(kyro_ctx ctx, size_t bytes, kyro_buf* out) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!out) return fail(KYRO_EINVAL, "kyro_buf_alloc: out is null");
+        *out = nullptr;
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        void* p = nullptr;
+        KYRO_HIP(hipMalloc(&p, bytes ? bytes : 1));
+        kyro_buf b = new kyro_buf_s();
+        b->device = ctx->device;
+        b->ptr = p;
+        b->bytes = bytes;
+        *out = b;
+        return KYRO_OK;
+    });
+}
+
+int kyro_buf_free(kyro_buf buf) {
+    return guarded([&]() -> int {
+        if (!buf) return KYRO_OK;
+        DeviceGuard dg(buf->device);
+        if (buf->ptr) KYRO_HIP(hipFree(buf->ptr));
+        delete buf;
+        return KYRO_OK;
+    });
+}
+
+void* kyro_buf_ptr(kyro_buf buf) { return buf ? buf->ptr : nullptr; }
+
+size_t kyro_buf_size(kyro_buf buf) { return buf ? buf->bytes : 0; }
+
+int kyro_buf_upload(kyro_ctx ctx, kyro_buf dst, size_t dst_offset, const void* src, size_t bytes) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!dst || (!src && bytes)) return fail(KYRO_EINVAL, "kyro_buf_upload: null buffer");
+        if (dst_offset > dst->bytes || bytes > dst->bytes - dst_offset)
+            return fail(KYRO_EINVAL, "kyro_buf_upload: %zu bytes at offset %zu exceed buffer of %zu",
+                        bytes, dst_offset, dst->bytes);
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        KYRO_HIP(hipMemcpyAsync(static_cast<char*>(dst->ptr) + dst_offset, src, bytes,
+                                hipMemcpyHostToDevice, ctx->stream));
+        KYRO_HIP(hipStreamSynchronize(ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, size_t bytes) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!src || (!dst && bytes)) return fail(KYRO_EINVAL, "kyro_buf_download: null buffer");
+        if (src_offset > src->bytes || bytes > src->bytes - src_offset)
+            return fail(KYRO_EINVAL, "kyro_buf_download: %zu bytes at offset %zu exceed buffer of %zu",
+                        bytes, src_offset, src->bytes);
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        KYRO_HIP(hipMemcpyAsync(dst, static_cast<const char*>(src->ptr) + src_offset, bytes,
+                                hipMemcpyDeviceToHost, ctx->stream));
+        KYRO_HIP(hipStreamSynchronize(ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, const void* query,
+                            const int32_t* q_start_loc, const void* key_cache,
+                            const void* value_cache, const int64_t* block_table,
+                            const int64_t* context_lens, void* out) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!p) return fail(KYRO_EINVAL, "paged_attention: params is null");
+        if (p->block_size <= 0 || p->num_heads <= 0 || p->head_dim <= 0 || p->num_kv_heads <= 0)
+            return fail(KYRO_EINVAL, "paged_attention: block_size/num_heads/head_dim/num_kv_heads must be > 0");
+        if (p->num_heads % p->num_kv_heads != 0)
+            return fail(KYRO_EINVAL, "paged_attention: num_heads %d not a multiple of num_kv_heads %d",
+                        p->num_heads, p->num_kv_heads);
+        if (p->batch_size < 0 || p->total_q < 0 || p->max_blocks_per_seq < 0 || p->num_blocks < 0)
+            return fail(KYRO_EINVAL, "paged_attention: negative shape");
+        if (p->dtype != KYRO_F32 && p->dtype != KYRO_BF16)
+            return fail(KYRO_EINVAL, "paged_attention: dtype %d unknown", p->dtype);
+        if (p->out_dtype != KYRO_F32 && p->out_dtype != KYRO_BF16)
+            return fail(KYRO_EINVAL, "paged_attention: out_dtype %d unknown", p->out_dtype);
+        if (!q_start_loc && p->total_q != p->batch_size)
+            return fail(KYRO_EINVAL, "paged_attention: total_q %d != batch_size %d without q_start_loc",
+                        p->total_q, p->batch_size);
+        if (p->head_dim != 64 && p->head_dim != 128)
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: 64, 128)", p->head_dim);
+        if (p->path < KYRO_ATTN_AUTO || p->path > KYRO_ATTN_MFMA)
+            return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
+        if (p->batch_size == 0 || p->total_q == 0) return KYRO_OK;
+        if (!query || !key_cache || !value_cache || !block_table || !context_lens || !out)
+            return fail(KYRO_EINVAL, "paged_attention: null device pointer");
+        if (p->max_blocks_per_seq == 0 || p->num_blocks == 0) {
+            // Only context length 0 is possible; the kernels still write the zero rows.
+        }
+        const int group = p->num_heads / p->num_kv_heads;
+        int max_q_len = p->max_q_len;
+        if (max_q_len <= 0) max_q_len = q_start_loc ? p->total_q : 1;
+        if (!q_start_loc) max_q_len = 1;
+
+        const bool mfma_ok = p->dtype == KYRO_BF16 && p->head_dim == 128 && p->block_size == 16;
+        int kernel;
+        if (p->path == KYRO_ATTN_MFMA) {
+            if (!mfma_ok)
+                return fail(KYRO_EUNSUPPORTED,
+                            "paged_attention: the MFMA kernel needs bf16, head_dim 128, block_size 16");
+            kernel = kyro::ATTN_KERNEL_MFMA;
+        } else if (p->path == KYRO_ATTN_VECTOR) {
+            kernel = kyro::ATTN_KERNEL_VECTOR;
+        } else {
+            kernel = (mfma_ok && group * max_q_len >= 4) ? kyro::ATTN_KERNEL_MFMA : kyro::ATTN_KERNEL_VECTOR;
+        }
+
+        kyro::AttnArgs a{};
+        a.q = query;
+        a.q_start = q_start_loc;
+        a.k = key_cache;
+        a.v = value_cache;
+        a.table = block_table;
+        a.ctx_lens = context_lens;
+        a.out = out;
+        a.B = p->batch_size;
+        a.H = p->num_heads;
+        a.Hkv = p->num_kv_heads;
+        a.group = group;
+        a.D = p->head_dim;
+        a.bs = p->block_size;
+        a.max_blocks = p->max_blocks_per_seq;
+        a.num_blocks = p->num_blocks;
+        a.total_q = p->total_q;
+        a.max_q_len = max_q_len;
+        a.rows_cap = group * max_q_len;
+        a.causal = p->causal ? 1 : 0;
+        a.out_bf16 = p->out_dtype == KYRO_BF16;
+        a.dtype_bf16 = p->dtype == KYRO_BF16;
+        const double scale = p->scale > 0 ? (double)p->scale : 1.0 / std::sqrt((double)p->head_dim);
+        a.scale_log2 = (float)(scale * 1.4426950408889634);
+        a.units = p->batch_size * p->num_kv_heads;
+        a.units_padded = (a.units + 7) / 8 * 8;
+
+        // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
+        const int mb = std::max(1, p->max_blocks_per_seq);
+        int splits = p->num_splits;
+        if (splits <= 0) {
+            const int want_wgs = 1024;
+            splits = std::max(1, (want_wgs + a.units - 1) / a.units);
+            splits = std::min(splits, std::max(1, mb / 16));
+        }
+        splits = std::min(splits, mb);
+        int chunk = (mb + splits - 1) / splits;
+        chunk = (chunk + 1) / 2 * 2;
+        splits = (mb + chunk - 1) / chunk;
+        a.splits = splits;
+        a.chunk_blocks = chunk;
+
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        size_t ws_bytes = 0;
+        if (splits > 1) {
+            const size_t rows = (size_t)a.units * splits * a.rows_cap;
+            ws_bytes = align_up(rows * sizeof(float), 256) * 2 + align_up(rows * a.D * sizeof(float), 256);
+            if (int rc = ensure_arena(ctx, ws_bytes)) return rc;
+            if (int rc = ensure_counters(ctx, (size_t)a.units)) return rc;
+            char* base = static_cast<char*>(ctx->arena);
+            a.ws_m = reinterpret_cast<float*>(base);
+            a.ws_l = reinterpret_cast<float*>(base + align_up(rows * sizeof(float), 256));
+            a.ws_acc = reinterpret_cast<float*>(base + 2 * align_up(rows * sizeof(float), 256));
+            a.counters = ctx->counters;
+        }
+        a.err = ctx->err;
+        KYRO_HIP(kyro::launch_paged_attention(a, kernel, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void* target_logits,
+                     const void* draft_logits, const uint32_t* draft_tokens,
+                     const int32_t* num_draft, const float* temperature, const float* u_accept,
+                     const float* u_resample, int32_t* out_accepted, uint32_t* out_tokens,
+                     float* out_p_draft, float* out_q_draft) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!p) return fail(KYRO_EINVAL, "spec_verify: params is null");
+        if (p->batch_size < 0 || p->max_draft < 0 || p->vocab_size <= 0)
+            return fail(KYRO_EINVAL, "spec_verify: need batch_size >= 0, max_draft >= 0, vocab_size > 0");
+        if (p->max_draft > 63)
+            return fail(KYRO_EUNSUPPORTED, "spec_verify: max_draft %d > 63", p->max_draft);
+        if (p->logits_dtype != KYRO_F32)
+            return fail(KYRO_EUNSUPPORTED, "spec_verify: logits_dtype must be KYRO_F32");
+        if (p->batch_size == 0) return KYRO_OK;
+        if (!target_logits || !num_draft || !temperature || !u_resample || !out_accepted || !out_tokens)
+            return fail(KYRO_EINVAL, "spec_verify: null device pointer");
+        if (p->max_draft > 0 && (!draft_tokens || !u_accept))
+            return fail(KYRO_EINVAL, "spec_verify: draft_tokens and u_accept are required when max_draft > 0");
+        kyro::SpecArgs a{};
+        a.target = static_cast<const float*>(target_logits);
+        a.draft = static_cast<const float*>(draft_logits);
+        a.draft_tokens = draft_tokens;
+        a.num_draft = num_draft;
+        a.temperature = temperature;
+        a.u_accept = u_accept;
+        a.u_res = u_resample;
+        a.out_accepted = out_accepted;
+        a.out_tokens = out_tokens;
+        a.out_p = out_p_draft;
+        a.out_q = out_q_draft;
+        a.B = p->batch_size;
+        a.kmax = p->max_draft;
+        a.V = p->vocab_size;
+        a.chunk = kyro::kSpecChunk;
+        a.C = (a.V + a.chunk - 1) / a.chunk;
+        const bool aligned = (reinterpret_cast<uintptr_t>(target_logits) % 16 == 0) &&
+                             (reinterpret_cast<uintptr_t>(draft_logits) % 16 == 0);
+        a.vec4 = (a.V % 4 == 0) && aligned;
+        const size_t stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
+        const size_t plan_b = align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
+        const size_t csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b)) return rc;
+        char* base = static_cast<char*>(ctx->arena);
+        a.stats = reinterpret_cast<float2*>(base);
+        a.plan = reinterpret_cast<kyro::SpecPlan*>(base + stats_b);
+        a.csum = reinterpret_cast<float2*>(base + stats_b + plan_b);
+        a.err = ctx->err;
+        KYRO_HIP(kyro::launch_spec_verify(a, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+"""Shared helpers for the GPU parity tests: move workload arrays to the device, run the oracle on a
+subset of sequences, and compare verify results with the documented exemptions."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+from kyro_amd import workloads as wl
+
+ATOL_BF16 = 2e-2   # attention outputs, bf16 inputs
+ATOL_F32 = 1e-3    # attention outputs, f32 inputs
+PROB_ATOL = 1e-5   # p_i(x_i), q_i(x_i)
+MARGIN = 1e-5      # decisions with |u - boundary| below this may differ under f32 rounding
+
+
+def to_device(a: np.ndarray, device, bf16: bool = False) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if bf16:
+        t = t.view(torch.bfloat16)
+    return t.to(device)
+
+
+def attention_tensors(case: wl.AttentionCase, device):
+    bf16 = case.dtype == "bf16"
+    return dict(
+        query=to_device(case.query, device, bf16),
+        key_cache=to_device(case.key_cache, device, bf16),
+        value_cache=to_device(case.value_cache, device, bf16),
+        block_table=to_device(case.block_table, device),
+        context_lens=to_device(case.context_lens, device),
+        q_start_loc=to_device(case.q_start_loc, device),
+    )
+
+
+def oracle_attention(case: wl.AttentionCase, seqs=None, causal=True) -> dict:
+    """Oracle rows for the chosen sequences, gathering only their blocks (so a full-size case is
+    checked without running the oracle over the whole batch). Returns {seq: [q_len, H, D]}."""
+    seqs = range(case.batch) if seqs is None else seqs
+    res = {}
+    for b in seqs:
+        ctx = int(case.context_lens[b])
+        nb = max(1, -(-ctx // case.block_size))
+        blocks = case.block_table[b, :nb]
+        q0, q1 = int(case.q_start_loc[b]), int(case.q_start_loc[b + 1])
+        res[b] = oracle.paged_attention_mq(
+            case.query[q0:q1], case.key_cache[blocks], case.value_cache[blocks],
+            np.arange(nb, dtype=np.int64)[None], np.array([ctx], np.int64),
+            num_heads=case.num_heads, num_kv_heads=case.num_kv_heads, head_dim=case.head_dim,
+            block_size=case.block_size, q_start_loc=np.array([0, q1 - q0], np.int32), causal=causal,
+            threads=8)
+    return res
+
+
+def assert_attention_close(out: torch.Tensor, case: wl.AttentionCase, expected: dict, atol: float):
+    got = out.float().cpu().numpy()
+    worst = 0.0
+    for b, ref in expected.items():
+        q0, q1 = int(case.q_start_loc[b]), int(case.q_start_loc[b + 1])
+        err = float(np.max(np.abs(got[q0:q1] - ref))) if q1 > q0 else 0.0
+        worst = max(worst, err)
+        assert np.isfinite(got[q0:q1]).all(), f"non-finite output in sequence {b}"
+        assert err <= atol, f"sequence {b}: max abs error {err:.3g} > {atol}"
+    return worst
+
+
+def verify_tensors(case: wl.VerifyCase, device, with_draft=True):
+    return dict(
+        target_logits=to_device(case.target, device),
+        draft_logits=to_device(case.draft, device) if with_draft else None,
+        draft_tokens=to_device(case.draft_tokens.astype(np.int32), device),
+        num_draft=to_device(case.num_draft.astype(np.int32), device),
+        temperature=to_device(case.temperature.astype(np.float32), device),
+        u_accept=to_device(case.u_accept, device),
+        u_resample=to_device(case.u_resample, device),
+    )
+
+
+def oracle_verify(case: wl.VerifyCase) -> dict:
+    return oracle.spec_verify(case.target, case.draft, case.draft_tokens, case.num_draft,
+                              case.temperature, case.u_accept, case.u_resample)
+
+
+def assert_verify_parity(res, case: wl.VerifyCase, orc: dict, max_exempt: int = 0):
+    """Accepted lengths and emitted tokens bit-exact, except decisions the oracle places within
+    MARGIN of a boundary. Probabilities within PROB_ATOL. Returns the number of exemptions."""
+    acc = res.accepted.cpu().numpy()
+    tok = res.tokens.cpu().numpy().view(np.uint32)
+    exempt = 0
+    for b in range(case.batch):
+        a_g, a_o = int(acc[b]), int(orc["accepted"][b])
+        if a_g != a_o:
+            i = min(a_g, a_o)
+            m = orc["accept_margin"][b, i]
+            assert m < MARGIN, f"seq {b}: accepted {a_g} vs oracle {a_o}, margin {m:.3g} at position {i}"
+            exempt += 1
+            continue
+        if not np.array_equal(tok[b], orc["tokens"][b]):
+            assert np.array_equal(tok[b, :a_g], orc["tokens"][b, :a_g]), f"seq {b}: accepted drafts differ"
+            m = orc["resample_margin"][b]
+            assert m < MARGIN, (f"seq {b}: emitted {tok[b, a_g]} vs oracle {orc['tokens'][b, a_g]}, "
+                                f"resample margin {m:.3g}")
+            exempt += 1
+    assert exempt <= max_exempt, f"{exempt} margin exemptions"
+    if res.p_draft is not None:
+        for name in ("p_draft", "q_draft"):
+            g = getattr(res, name).cpu().numpy().astype(np.float64)
+            o = orc[name]
+            both = ~np.isnan(g) & ~np.isnan(o)
+            if both.any():
+                err = np.max(np.abs(g[both] - o[both]))
+                assert err <= PROB_ATOL, f"{name} max abs error {err:.3g}"
+    return exempt

@@ -1,0 +1,78 @@
+"""The C ABI without a GPU: the library loads, exports every function include/kyro_verify.h
+declares, and rejects bad arguments with a status code and a message (no crash, no exception)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from kyro_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", f) for f in sorted(os.listdir(os.path.join(ROOT, "include")))
+           if f.endswith(".h")]
+
+
+def declared_functions():
+    names = []
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(kyro_[a-z0-9_]+)\s*\(",
+                            text, flags=re.M)
+    return names
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for required in ("kyro_paged_attention_mq", "kyro_spec_verify", "kyro_ctx_create",
+                     "kyro_last_error", "kyro_buf_alloc"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers the same set
+    assert set(declared_functions()) == set(_lib._SIGNATURES)
+
+
+def test_abi_version():
+    assert _lib.lib().kyro_abi_version() == 1
+
+
+def test_null_context_is_einval():
+    lib = _lib.lib()
+    params = _lib.PagedAttentionParams(16, 8, 64, 2, 1, 1, 4, 4, _lib.KYRO_F32, _lib.KYRO_F32, 1, 0.0, 0, 0, 0)
+    rc = lib.kyro_paged_attention_mq(None, ctypes.byref(params), None, None, None, None, None, None, None)
+    assert rc == _lib.KYRO_EINVAL
+    assert "null kyro_ctx" in _lib.last_error()
+    sp = _lib.SpecVerifyParams(1, 1, 10, _lib.KYRO_F32)
+    rc = lib.kyro_spec_verify(None, ctypes.byref(sp), *([None] * 12))
+    assert rc == _lib.KYRO_EINVAL
+    assert lib.kyro_sync(None) == _lib.KYRO_EINVAL
+
+
+def test_buffer_helpers_tolerate_null():
+    lib = _lib.lib()
+    assert lib.kyro_buf_ptr(None) is None
+    assert lib.kyro_buf_size(None) == 0
+    assert lib.kyro_buf_free(None) == _lib.KYRO_OK
+    assert lib.kyro_ctx_destroy(None) == _lib.KYRO_OK
+    out = ctypes.c_void_p()
+    assert lib.kyro_buf_alloc(None, 16, ctypes.byref(out)) == _lib.KYRO_EINVAL
+
+
+def test_bad_device_is_an_error_not_a_crash():
+    out = ctypes.c_void_p()
+    rc = _lib.lib().kyro_ctx_create(-1, ctypes.byref(out))
+    assert rc in (_lib.KYRO_EINVAL, _lib.KYRO_EHIP)
+    assert out.value is None
+    assert _lib.last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(ImportError):
+        _lib.lib()

@@ -1,0 +1,202 @@
+"""Paged attention on the GPU against the oracle, through the C ABI (kyro_paged_attention_mq).
+
+Mirrors the reference's own tests (src/model/attention_kernel.rs:154-227) and then checks values:
+small cases against the oracle on every sequence, full-size workloads on a subset of sequences,
+and size-independent properties (split count, kernel choice, block permutation) at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kyro_amd
+from kyro_amd import workloads as wl
+from tests import helpers as h
+
+pytestmark = pytest.mark.gpu
+
+
+def make_attention(block_size, num_heads, head_dim, num_kv_heads):
+    return kyro_amd.PagedAttention(block_size, num_heads, head_dim, num_kv_heads)
+
+
+# ---------------------------------------------------- the reference's tests, on the GPU
+
+
+def test_paged_attention_creation():
+    attn = make_attention(16, 8, 64, 2)
+    assert (attn.block_size, attn.num_heads, attn.head_dim, attn.num_kv_heads) == (16, 8, 64, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_paged_attention_zero_context(gpu, dtype):
+    attn = make_attention(16, 8, 64, 2)
+    out = attn.forward(torch.zeros((1, 8, 64), dtype=dtype, device=gpu),
+                       torch.zeros((4, 2, 16, 64), dtype=dtype, device=gpu),
+                       torch.zeros((4, 2, 16, 64), dtype=dtype, device=gpu),
+                       torch.zeros((1, 4), dtype=torch.int64, device=gpu),
+                       torch.zeros((1,), dtype=torch.int64, device=gpu))
+    assert tuple(out.shape) == (1, 8, 64)
+    assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("ctx", [8, 24])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_paged_attention_mha_all_ones(gpu, ctx, dtype):
+    """Single block (ctx 8) and multi-block over the aliased table [0,0,0,0] (ctx 24)."""
+    attn = make_attention(16, 8, 64, 8)
+    out = attn.forward(torch.ones((1, 8, 64), dtype=dtype, device=gpu),
+                       torch.ones((4, 8, 16, 64), dtype=dtype, device=gpu),
+                       torch.ones((4, 8, 16, 64), dtype=dtype, device=gpu),
+                       torch.zeros((1, 4), dtype=torch.int64, device=gpu),
+                       torch.full((1,), ctx, dtype=torch.int64, device=gpu))
+    assert tuple(out.shape) == (1, 8, 64)
+    torch.testing.assert_close(out, torch.ones_like(out), atol=1e-6, rtol=0)
+
+
+# ---------------------------------------------------------------- parity with the oracle
+
+SMALL = [
+    # (heads, kv heads, D, ctx lens, q lens)
+    ((8, 2), 64, [17, 40, 5, 33, 16, 1], [1, 5, 3, 2, 4, 1]),
+    ((4, 4), 128, [100, 16, 48, 3], [5, 5, 5, 3]),
+    ((32, 8), 128, [129, 300, 40, 257], [8, 8, 8, 8]),
+    ((64, 8), 128, [260, 50, 9, 700], [9, 1, 4, 6]),
+    ((8, 1), 128, [33, 77], [1, 2]),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", SMALL, ids=lambda s: f"{s[0][0]}x{s[0][1]}d{s[1]}")
+@pytest.mark.parametrize("path", ["vector", "mfma", "auto"])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_small_parity(gpu, dtype, shape, path, splits):
+    (H, Hkv), D, ctx, ql = shape
+    if path == "mfma" and (dtype != "bf16" or D != 128):
+        pytest.skip("the MFMA kernel is bf16 / head_dim 128 only")
+    case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
+                                  head_dim=D, dtype=dtype, seed=21, num_blocks=200)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, H, D, Hkv)
+    out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                       t["context_lens"], q_start_loc=t["q_start_loc"], path=path,
+                       num_splits=splits)
+    h.assert_attention_close(out, case, h.oracle_attention(case),
+                             h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
+
+
+def test_bf16_output_and_noncausal(gpu):
+    case = wl.make_attention_case(context_lens=[90, 31], q_lens=[4, 2], num_heads=16, num_kv_heads=4,
+                                  dtype="bf16", seed=8)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 16, 128, 4)
+    exp = h.oracle_attention(case, causal=False)
+    for path in ("vector", "mfma"):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                           t["context_lens"], q_start_loc=t["q_start_loc"], causal=False,
+                           out_dtype=torch.bfloat16, path=path)
+        assert out.dtype == torch.bfloat16
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16)
+
+
+def test_query_rows_without_visible_keys_are_zero(gpu):
+    """q_len > ctx under the causal rule: the first rows see no key and come out zero."""
+    case = wl.make_attention_case(context_lens=[3], q_lens=[5], num_heads=4, num_kv_heads=4,
+                                  dtype="bf16", seed=2)
+    t = h.attention_tensors(case, gpu)
+    for path in ("vector", "mfma"):
+        out = make_attention(16, 4, 128, 4).forward(
+            t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+            q_start_loc=t["q_start_loc"], path=path)
+        assert torch.count_nonzero(out[:2]) == 0
+        assert torch.count_nonzero(out[2:]) > 0
+
+
+def test_repeat_calls_are_bitwise_identical(gpu):
+    case = wl.gqa_llama3_8b(batch=4, ctx=1000)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 32, 128, 8)
+    outs = [attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                         t["context_lens"], q_start_loc=t["q_start_loc"], num_splits=4)
+            for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+# ---------------------------------------------------------------- full-size workloads
+
+
+def _full(case, gpu, seqs, **kw):
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(case.block_size, case.num_heads, case.head_dim, case.num_kv_heads)
+    out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                       t["context_lens"], q_start_loc=t["q_start_loc"], **kw)
+    h.assert_attention_close(out, case, h.oracle_attention(case, seqs), h.ATOL_BF16)
+    return t, attn, out
+
+
+def test_full_mha_llama2_7b(gpu):
+    case = wl.mha_llama2_7b()
+    t, attn, out = _full(case, gpu, [0, 7, 15])
+    for path in ("vector", "mfma"):
+        other = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                             t["context_lens"], q_start_loc=t["q_start_loc"], path=path)
+        assert (other - out).abs().max().item() < 1e-2
+
+
+def test_full_gqa_llama3_8b_properties(gpu):
+    """Full Llama-3-8B verify shape: oracle on three sequences; the split count and the kernel
+    choice do not change the result; permuting the physical blocks does not either."""
+    case = wl.gqa_llama3_8b()
+    t, attn, out = _full(case, gpu, [0, 31, 63], out_dtype=torch.float32)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    for kw in (dict(num_splits=1), dict(num_splits=16), dict(path="vector", num_splits=2)):
+        other = attn.forward(*args, q_start_loc=t["q_start_loc"], **kw)
+        assert (other - out).abs().max().item() < 1e-2, kw
+    nb = t["key_cache"].shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(0)).to(gpu)
+    k2 = torch.empty_like(t["key_cache"])
+    v2 = torch.empty_like(t["value_cache"])
+    k2[perm] = t["key_cache"]
+    v2[perm] = t["value_cache"]
+    out2 = attn.forward(t["query"], k2, v2, perm[t["block_table"]], t["context_lens"],
+                        q_start_loc=t["q_start_loc"])
+    assert torch.equal(out, out2)
+
+
+def test_full_skewed_prefix(gpu):
+    case = wl.skewed_prefix()
+    order = np.argsort(case.context_lens)
+    _full(case, gpu, [int(order[0]), int(order[len(order) // 2]), int(order[-1])])
+
+
+def test_full_mixed_llama3_70b(gpu):
+    case, k = wl.mixed_llama3_70b()
+    pick = [int(np.argmin(k)), int(np.argmax(k)), int(np.argmax(case.context_lens))]
+    _full(case, gpu, pick)
+
+
+# ------------------------------------------------------------------------- error paths
+
+
+def test_bad_block_id_and_context_length_raise(gpu):
+    attn = make_attention(16, 8, 64, 2)
+    q = torch.ones((1, 8, 64), device=gpu)
+    kv = torch.ones((4, 2, 16, 64), device=gpu)
+    with pytest.raises(kyro_amd.KyroError, match="block_table"):
+        attn.forward(q, kv, kv, torch.tensor([[0, 9]], device=gpu), torch.tensor([20], device=gpu))
+    with pytest.raises(kyro_amd.KyroError, match="context length"):
+        attn.forward(q, kv, kv, torch.tensor([[0, 1]], device=gpu), torch.tensor([33], device=gpu))
+    # the context recovers: the next valid call succeeds
+    out = attn.forward(q, kv, kv, torch.tensor([[0, 1]], device=gpu), torch.tensor([20], device=gpu))
+    torch.testing.assert_close(out, torch.ones_like(out))
+
+
+def test_host_validation(gpu):
+    attn = make_attention(16, 8, 64, 2)
+    q = torch.ones((1, 8, 64), device=gpu)
+    kv = torch.ones((4, 2, 16, 64), device=gpu)
+    with pytest.raises(TypeError):
+        attn.forward(q, kv.half(), kv.half(), torch.zeros((1, 4), dtype=torch.int64, device=gpu),
+                     torch.tensor([4], device=gpu))
+    with pytest.raises(kyro_amd.KyroError, match="MFMA"):
+        attn.forward(q, kv, kv, torch.zeros((1, 4), dtype=torch.int64, device=gpu),
+                     torch.tensor([4], device=gpu), path="mfma")

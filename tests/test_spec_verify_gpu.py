@@ -1,0 +1,129 @@
+"""Fused acceptance sampling on the GPU against the oracle, through the C ABI (kyro_spec_verify).
+
+Accepted lengths and emitted tokens must match bit for bit, except decisions the oracle places
+within 1e-5 of a boundary; probabilities at the draft tokens within 1e-5.
+"""
+import numpy as np
+import pytest
+import scipy.special
+import scipy.stats
+import torch
+
+import kyro_amd
+from kyro_amd import workloads as wl
+from tests import helpers as h
+
+pytestmark = pytest.mark.gpu
+
+
+def run(case, gpu, with_draft=True, return_probs=True):
+    t = h.verify_tensors(case, gpu, with_draft)
+    return kyro_amd.verify_drafts(**t, return_probs=return_probs)
+
+
+def test_rejection_only_b8_matches_oracle(gpu):
+    case = wl.rejection_only_b8()
+    res = run(case, gpu)
+    h.assert_verify_parity(res, case, h.oracle_verify(case))
+
+
+def test_greedy_reference_semantics(gpu):
+    """speculative.rs:315-323 with the bonus token; ties -> lowest index."""
+    V, k = 10, 4
+    t = np.zeros((3, k + 1, V), np.float32)
+    top = [[3, 1, 4, 1, 5], [2, 7, 1, 8, 2], [0, 0, 0, 0, 9]]
+    for b in range(3):
+        for i in range(k + 1):
+            t[b, i, top[b][i]] = 5.0
+    t[2, 1, 6] = 5.0
+    case = wl.VerifyCase(t, np.zeros((3, k, V), np.float32),
+                         np.array([[3, 1, 4, 1], [2, 7, 3, 8], [0, 0, 9, 0]], np.int32),
+                         np.full(3, k, np.int32), np.zeros(3, np.float32),
+                         np.full((3, k), 0.5, np.float32), np.full(3, 0.5, np.float32))
+    res = run(case, gpu, with_draft=False)
+    assert res.emitted() == [[3, 1, 4, 1, 5], [2, 7, 1], [0, 0, 0]]
+    h.assert_verify_parity(res, case, h.oracle_verify(case))
+
+
+def test_reference_sample_token_kats_as_k0(gpu):
+    """worker.rs:395-431 as k = 0 verify steps (plain decode): argmax at T = 0, the dominant
+    logit at T = 2."""
+    rows = [[0.1, 0.2, 0.3, 0.4, 0.5, 10.0, 0.1, 0.2], [1.0, 2.0, 3.0, 0.5, 0.1, 0, 0, 0],
+            [100.0, 0, 0, 0, 0, 0, 0, 0]]
+    t = np.array(rows, np.float32)[:, None, :]
+    rows_T = np.array([0.0, 0.0, 2.0], np.float32)
+    case = wl.VerifyCase(t, np.zeros((3, 0, 8), np.float32), np.zeros((3, 0), np.int32),
+                         np.zeros(3, np.int32), rows_T, np.zeros((3, 0), np.float32),
+                         np.array([0.3, 0.9, 0.999], np.float32))
+    res = run(case, gpu, with_draft=False)
+    assert res.accepted.cpu().tolist() == [0, 0, 0]
+    assert res.tokens[:, 0].cpu().tolist() == [5, 2, 0]
+
+
+@pytest.mark.parametrize("vocab", [37, 1000, 32000, 50001])
+@pytest.mark.parametrize("T", [0.0, 0.7, 1.0, 1.6])
+def test_parity_over_vocab_and_temperature(gpu, vocab, T):
+    case = wl.make_verify_case(batch=24, kmax=5, vocab=vocab, target_sigma=2.5, noise_sigma=0.8,
+                               temperature=T, num_draft=np.arange(24) % 6, seed=vocab)
+    res = run(case, gpu)
+    h.assert_verify_parity(res, case, h.oracle_verify(case), max_exempt=1)
+
+
+def test_identical_draft_accepts_all(gpu):
+    case = wl.make_verify_case(batch=16, kmax=4, vocab=5000, target_sigma=2.0, noise_sigma=0.0,
+                               temperature=1.0, seed=3)
+    res = run(case, gpu)
+    assert (res.accepted.cpu() == 4).all()
+    h.assert_verify_parity(res, case, h.oracle_verify(case))
+
+
+def test_mixed_batch_reduced(gpu):
+    k = wl.rng(0, wl.S_KSEQ).integers(0, 9, size=32)
+    case = wl.verify_mixed(k, vocab=20000)
+    h.assert_verify_parity(run(case, gpu), case, h.oracle_verify(case), max_exempt=1)
+
+
+def test_full_llama3_8b(gpu):
+    case = wl.verify_llama3_8b()
+    res = run(case, gpu)
+    h.assert_verify_parity(res, case, h.oracle_verify(case), max_exempt=1)
+    assert 0 < res.accepted.float().mean().item() < 7
+
+
+def test_full_mixed_llama3_70b(gpu):
+    _, k = wl.mixed_llama3_70b()
+    case = wl.verify_mixed(k)
+    h.assert_verify_parity(run(case, gpu), case, h.oracle_verify(case), max_exempt=1)
+
+
+def test_first_token_law_is_p0(gpu):
+    """Leviathan et al. 2023, Thm 1 on the GPU: with x ~ q the first emitted token follows p."""
+    V, N = 8, 120_000
+    g = np.random.default_rng(7)
+    t_row = np.array([2.0, 0.5, -1.0, 1.5, 0.0, -0.5, 1.0, -2.0], np.float32)
+    d_row = np.array([0.0, 2.0, 1.0, -1.0, 0.5, 1.5, -1.0, 0.0], np.float32)
+    q = scipy.special.softmax(d_row.astype(np.float64))
+    p = scipy.special.softmax(t_row.astype(np.float64))
+    x = np.searchsorted(np.cumsum(q), g.random(N)).clip(0, V - 1).astype(np.int32)
+    case = wl.VerifyCase(np.broadcast_to(np.stack([t_row, t_row])[None], (N, 2, V)).copy(),
+                         np.broadcast_to(d_row[None, None], (N, 1, V)).copy(), x[:, None],
+                         np.ones(N, np.int32), np.ones(N, np.float32),
+                         g.random((N, 1)).astype(np.float32), g.random(N).astype(np.float32))
+    res = run(case, gpu, return_probs=False)
+    counts = np.bincount(res.tokens[:, 0].cpu().numpy(), minlength=V)
+    assert scipy.stats.chisquare(counts, p * N).pvalue > 1e-4
+
+
+def test_bad_inputs_raise_and_recover(gpu):
+    case = wl.make_verify_case(batch=2, kmax=2, vocab=100, target_sigma=1.0, noise_sigma=1.0,
+                               temperature=1.0, seed=1)
+    t = h.verify_tensors(case, gpu)
+    bad = dict(t)
+    bad["num_draft"] = torch.tensor([3, 1], dtype=torch.int32, device=gpu)
+    with pytest.raises(kyro_amd.KyroError, match="num_draft"):
+        kyro_amd.verify_drafts(**bad)
+    bad = dict(t)
+    bad["draft_tokens"] = torch.tensor([[5, 100], [1, 2]], dtype=torch.int32, device=gpu)
+    with pytest.raises(kyro_amd.KyroError, match="draft token"):
+        kyro_amd.verify_drafts(**bad)
+    h.assert_verify_parity(kyro_amd.verify_drafts(**t, return_probs=True), case, h.oracle_verify(case))
