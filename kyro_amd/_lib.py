@@ -67,7 +67,7 @@ _SIGNATURES = {
     "kyro_buf_upload": ([_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t], ctypes.c_int),
     "kyro_buf_download": ([_P, _P, _P, ctypes.c_size_t, ctypes.c_size_t], ctypes.c_int),
     "kyro_paged_attention_mq": ([_P, ctypes.POINTER(PagedAttentionParams)] + [_P] * 7, ctypes.c_int),
-    "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 12, ctypes.c_int),
+    "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
 }
 
 

@@ -124,11 +124,6 @@ struct Frame {
     int last;
 };
 
-template <int R, int D>
-__device__ __forceinline__ void frame_zero(Frame<R, D>& f) {
-    for (int i = threadIdx.x; i < R * Frame<R, D>::kStride; i += kThreads) f.acc[i] = 0.f;
-}
-
 // After every wave has added its rescaled accumulator: either normalise and store the rows
 // (single split) or park the split's partial state in the workspace.
 template <int R, int D>
@@ -238,7 +233,6 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     const int nrows_total = si.rows > 0 ? si.rows : 1;
     for (int row0 = 0; row0 < nrows_total; row0 += R) {
         const int nrows = min(R, si.rows - row0);
-        frame_zero(frame);
 
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
         bf16x8 qB[NT][4];
@@ -379,24 +373,37 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             for (int nt = 0; nt < NT; ++nt) frame.m[wave][nt * 16 + r] = m[nt];
         }
         __syncthreads();
+        float f[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int n = nt * 16 + r;
             float M = frame.m[0][n];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) M = fmaxf(M, frame.m[w][n]);
-            const float f = (m[nt] == kNegInf) ? 0.f : fast_exp2(m[nt] - M);
+            f[nt] = (m[nt] == kNegInf) ? 0.f : fast_exp2(m[nt] - M);
             if (g == 0) {
-                frame.l[wave][n] = lsum[nt] * f;
+                frame.l[wave][n] = lsum[nt] * f[nt];
                 if (wave == 0) frame.mx[n] = M;
             }
-            float* dst = &frame.acc[n * Frame<R, D>::kStride + 32 * g];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) atomicAdd(dst + 8 * e + dt, O[dt][nt][e] * f);
         }
-        __syncthreads();
+        // Waves add their rescaled accumulators in a fixed order (wave 0 stores), so the result
+        // is bitwise reproducible. Lane (r, g) owns head dims 32 g + 8 e + dt of row 16 nt + r.
+        for (int w = 0; w < kWaves; ++w) {
+            if (wave == w) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    float* dst = &frame.acc[(nt * 16 + r) * Frame<R, D>::kStride + 32 * g];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int dt = 0; dt < 8; ++dt) {
+                            const float v = O[dt][nt][e] * f[nt];
+                            dst[8 * e + dt] = (w == 0) ? v : dst[8 * e + dt] + v;
+                        }
+                }
+            }
+            __syncthreads();
+        }
         frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
         __syncthreads();
     }
@@ -475,7 +482,6 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
     const int nrows_total = si.rows > 0 ? si.rows : 1;
     for (int row0 = 0; row0 < nrows_total; row0 += R) {
         const int nrows = min(R, si.rows - row0);
-        frame_zero(frame);
         float q[R][DPL];
         int vis[R];
 #pragma unroll
@@ -554,23 +560,32 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
             for (int i = 0; i < R; ++i) frame.m[wave][i] = m[i];
         }
         __syncthreads();
+        float f[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             float M = frame.m[0][i];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) M = fmaxf(M, frame.m[w][i]);
-            const float f = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - M);
+            f[i] = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - M);
             if (lane == 0) {
-                frame.l[wave][i] = l[i] * f;
+                frame.l[wave][i] = l[i] * f[i];
                 if (wave == 0) frame.mx[i] = M;
             }
-            if (g == 0) {
-#pragma unroll
-                for (int d = 0; d < DPL; ++d)
-                    atomicAdd(&frame.acc[i * Frame<R, D>::kStride + r * DPL + d], acc[i][d] * f);
-            }
         }
-        __syncthreads();
+        // Fixed-order merge (wave 0 stores, the others add in turn): bitwise reproducible.
+        for (int w = 0; w < kWaves; ++w) {
+            if (wave == w && g == 0) {
+#pragma unroll
+                for (int i = 0; i < R; ++i)
+#pragma unroll
+                    for (int d = 0; d < DPL; ++d) {
+                        float* p = &frame.acc[i * Frame<R, D>::kStride + r * DPL + d];
+                        const float v = acc[i][d] * f[i];
+                        *p = (w == 0) ? v : *p + v;
+                    }
+            }
+            __syncthreads();
+        }
         frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
         __syncthreads();
     }

@@ -48,7 +48,7 @@ def test_null_context_is_einval():
     assert rc == _lib.KYRO_EINVAL
     assert "null kyro_ctx" in _lib.last_error()
     sp = _lib.SpecVerifyParams(1, 1, 10, _lib.KYRO_F32)
-    rc = lib.kyro_spec_verify(None, ctypes.byref(sp), *([None] * 12))
+    rc = lib.kyro_spec_verify(None, ctypes.byref(sp), *([None] * 11))
     assert rc == _lib.KYRO_EINVAL
     assert lib.kyro_sync(None) == _lib.KYRO_EINVAL
 
