@@ -19,6 +19,10 @@ enum ErrorBits : int {
 
 enum AttnKernel : int { ATTN_KERNEL_VECTOR = 1, ATTN_KERNEL_MFMA = 2 };
 
+// Upper bound on the blocks one attention workgroup streams (its split); the block ids of a
+// split are staged in LDS.
+constexpr int kMaxChunkBlocks = 1024;
+
 struct AttnArgs {
     const void* q;
     const int32_t* q_start;  // [B+1] or nullptr (row b belongs to sequence b)
@@ -30,7 +34,6 @@ struct AttnArgs {
     float* ws_m;     // [units, splits, rows_cap]
     float* ws_l;     // [units, splits, rows_cap]
     float* ws_acc;   // [units, splits, rows_cap, D]
-    int* counters;   // [units], zero between calls
     int* err;        // device error word
     int B, H, Hkv, group, D, bs;
     int max_blocks, num_blocks, total_q, max_q_len, rows_cap;
@@ -68,12 +71,14 @@ struct SpecArgs {
     float2* stats;   // [B, 2 kmax + 1, C]: {max, sum exp} (sampled) or {max, index bits} (greedy)
     SpecPlan* plan;  // [B]
     float2* csum;    // [B, C]: {residual mass, p mass} of the resampled row, per chunk
+    float* gath;     // [B, 2 kmax + 1]: logit of the row's draft token (sampled rows < k)
     int* err;
     int B, kmax, V, C, chunk, vec4;
 };
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
 
-constexpr int kSpecChunk = 8192;  // vocabulary entries per workgroup in the streaming passes
+constexpr int kSpecChunk = 8192;
+constexpr int kMaxDraft = 63;  // one wave holds the acceptance decisions of a sequence  // vocabulary entries per workgroup in the streaming passes
 
 }  // namespace kyro

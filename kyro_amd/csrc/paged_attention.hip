@@ -9,7 +9,9 @@
 // Every query row that reads that kv head — the GQA group x the sequence's q_len rows — is
 // processed together, so each K/V byte is read from HBM exactly once. The 4 waves stream disjoint
 // blocks of the split with private online-softmax state and merge through LDS at the end; splits
-// of one (sequence, kv head) merge through a small workspace, in the last workgroup to finish.
+// of one (sequence, kv head) park their partial state in a workspace that attn_combine_kernel
+// merges (a kernel boundary orders the two passes; an agent-scope fence per workgroup, which
+// writes back the XCD's L2, cost more than the whole second launch).
 // Workgroups are numbered so that all splits of one (sequence, kv head) land on one XCD (the
 // dispatcher deals workgroups round-robin over the 8 XCDs), keeping that merge in one L2.
 //
@@ -121,7 +123,6 @@ struct Frame {
     float m[kWaves][R];
     float l[kWaves][R];
     float mx[R];
-    int last;
 };
 
 // After every wave has added its rescaled accumulator: either normalise and store the rows
@@ -159,20 +160,17 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int 
     }
 }
 
-// Called by every workgroup of a multi-split unit once all its rows are parked. The last
-// workgroup to arrive merges the splits and writes the output, then re-arms the counter.
-template <int R, int D>
-__device__ void merge_splits(const AttnArgs& a, const SeqInfo& si, int unit, int nsplit,
-                             Frame<R, D>& f) {
-    __threadfence();  // release this workgroup's partials (agent scope)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = atomicAdd(&a.counters[unit], 1);
-        f.last = (prev == nsplit - 1);
-    }
-    __syncthreads();
-    if (!f.last) return;
-    __threadfence();  // acquire the other workgroups' partials
+// Second pass for multi-split units: merges the parked partial states of every split of one
+// (sequence, kv head) and writes the normalised rows. One workgroup per unit; units whose
+// sequence needed a single split were stored directly by the first pass and exit here.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
+    const int unit = blockIdx.x;
+    if (unit >= a.units) return;
+    const SeqInfo si = seq_info(a, unit);
+    if (!si.ok) return;
+    const int nsplit = num_splits_for(a, si.nblk);
+    if (nsplit <= 1) return;
     constexpr int Q = D / 4;
     const size_t base = (size_t)unit * a.splits * a.rows_cap;
     for (int idx = threadIdx.x; idx < si.rows * Q; idx += kThreads) {
@@ -196,7 +194,6 @@ __device__ void merge_splits(const AttnArgs& a, const SeqInfo& si, int unit, int
         const float inv = L > 0.f ? 1.f / L : 0.f;
         store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
     }
-    if (threadIdx.x == 0) a.counters[unit] = 0;
 }
 
 // ------------------------------------------------------------------------------ MFMA kernel
@@ -204,11 +201,73 @@ __device__ void merge_splits(const AttnArgs& a, const SeqInfo& si, int unit, int
 constexpr int kMfmaD = 128;
 constexpr int kMfmaBS = 16;
 
+#ifndef KYRO_KV_NONTEMPORAL
+#define KYRO_KV_NONTEMPORAL 0
+#endif
+#ifndef KYRO_PREFETCH_DEPTH
+#define KYRO_PREFETCH_DEPTH 1
+#endif
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// K/V bytes are read exactly once: optionally stream them past the caches.
+__device__ __forceinline__ uint4 load16_kv(const uint16_t* p) {
+#if KYRO_KV_NONTEMPORAL
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+#else
+    return load16(p);
+#endif
+}
+
+// K and V of one pair of 16-token blocks, already in MFMA operand layout (K) or ready for the
+// in-register transpose (V). 64 VGPRs.
+struct KVPair {
+    bf16x8 k[2][4];  // [block][head-dim step]: token r, head dims 32 s + 8 g .. + 7
+    uint4 v[2][4];   // [block][e]: token 4 g + e, head dims 8 r .. 8 r + 7
+};
+
+// Issues the 16 loads of one block pair. A negative block id reads as zeros (never dereferenced).
+__device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict__ kp,
+                                          const uint16_t* __restrict__ vp, int blk0, int blk1,
+                                          size_t block_stride, size_t kv_off, int r, int g) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi) {
+        const int blk = bi ? blk1 : blk0;
+        if (blk >= 0) {
+            const size_t base = (size_t)blk * block_stride + kv_off;
+            const uint16_t* kb = kp + base + (size_t)r * kMfmaD + 8 * g;
+            const uint16_t* vb = vp + base + (size_t)(4 * g) * kMfmaD + 8 * r;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, load16_kv(kb + 32 * s));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p.v[bi][e] = load16_kv(vb + (size_t)e * kMfmaD);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p.v[bi][e] = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+// Stages the block ids of the workgroup's split in LDS (validated once, -1 for a bad id), so the
+// streaming loop never waits on a table load before issuing K/V loads.
+__device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo& si, int blk_begin,
+                                                int blk_end, int* s_blk) {
+    for (int i = blk_begin + (int)threadIdx.x; i < blk_end; i += kThreads) {
+        const int64_t blk = checked_block(a, si.b, i);
+        s_blk[i - blk_begin] = (int)blk;
+    }
+    __syncthreads();
+}
+
 template <int NT>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     constexpr int D = kMfmaD;
     constexpr int R = NT * 16;
     __shared__ Frame<R, D> frame;
+    __shared__ int s_blk[kMaxChunkBlocks];
 
     int unit, split;
     if (!map_workgroup(a, unit, split)) return;
@@ -229,12 +288,21 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     const size_t head_stride = (size_t)kMfmaBS * D;               // one (block, kv head) slab
     const size_t block_stride = (size_t)a.Hkv * head_stride;      // one block, all kv heads
     const size_t kv_off = (size_t)si.kvh * head_stride;
+    const float c = a.scale_log2;
+    // Tokens below full_vis are visible to every query row of the sequence.
+    const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
+
+    stage_block_ids(a, si, blk_begin, blk_end, s_blk);
+    auto blk_at = [&](int i) -> int {
+        return i < blk_end ? __builtin_amdgcn_readfirstlane(s_blk[i - blk_begin]) : -1;
+    };
 
     const int nrows_total = si.rows > 0 ? si.rows : 1;
     for (int row0 = 0; row0 < nrows_total; row0 += R) {
         const int nrows = min(R, si.rows - row0);
 
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
+        // Padding rows (n >= rows) get Q = 0 and full visibility; they are never stored.
         bf16x8 qB[NT][4];
         int vis[NT];
 #pragma unroll
@@ -250,11 +318,11 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             } else {
 #pragma unroll
                 for (int s = 0; s < 4; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-                vis[nt] = 0;
+                vis[nt] = si.ctx;
             }
         }
 
-        float m[NT], lsum[NT];
+        float m[NT], lsum[NT];  // running max (log2 units, scaled) and this lane's partial sum
         f32x4 O[8][NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -264,68 +332,51 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             for (int dt = 0; dt < 8; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
-        // Each wave takes pairs of blocks (32 tokens = one K-step of the PV MFMA).
-        for (int pb = blk_begin + 2 * wave; pb < blk_end; pb += 2 * kWaves) {
-            int64_t blk[2];
-            blk[0] = checked_block(a, si.b, pb);
-            blk[1] = (pb + 1 < blk_end) ? checked_block(a, si.b, pb + 1) : -1;
-
-            bf16x8 kA[2][4];
-            uint4 vin[2][4];
-#pragma unroll
-            for (int bi = 0; bi < 2; ++bi) {
-                if (blk[bi] >= 0) {
-                    const uint16_t* kb = kp + (size_t)blk[bi] * block_stride + kv_off + (size_t)r * D + 8 * g;
-                    const uint16_t* vb = vp + (size_t)blk[bi] * block_stride + kv_off + (size_t)(4 * g) * D + 8 * r;
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) kA[bi][s] = __builtin_bit_cast(bf16x8, load16(kb + 32 * s));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) vin[bi][e] = load16(vb + (size_t)e * D);
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) kA[bi][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) vin[bi][e] = make_uint4(0, 0, 0, 0);
-                }
-            }
-
+        // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
+        auto compute = [&](const KVPair& kv, int pb, int blk0, int blk1) {
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
             f32x4 S[2][NT];
 #pragma unroll
             for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
-                    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kA[bi][s], qB[nt][s], c, 0, 0, 0);
-                    S[bi][nt] = c;
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv.k[bi][s], qB[nt][s], acc, 0, 0, 0);
+                    S[bi][nt] = acc;
                 }
-
+            const bool full = blk0 >= 0 && blk1 >= 0 && (pb + 2) * kMfmaBS <= full_vis;
             bf16x8 pB[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 float sv[8];
-                float mx = kNegInf;
 #pragma unroll
                 for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int t = (pb + bi) * kMfmaBS + 4 * g + e;
-                        const bool ok = blk[bi] >= 0 && t < vis[nt];
-                        const float x = ok ? S[bi][nt][e] * a.scale_log2 : kNegInf;
-                        sv[bi * 4 + e] = x;
-                        mx = fmaxf(mx, x);
-                    }
+                    for (int e = 0; e < 4; ++e) sv[bi * 4 + e] = S[bi][nt][e];
+                if (!full) {
+#pragma unroll
+                    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int t = (pb + bi) * kMfmaBS + 4 * g + e;
+                            const bool ok = (bi ? blk1 : blk0) >= 0 && t < vis[nt];
+                            if (!ok) sv[bi * 4 + e] = kNegInf;
+                        }
+                }
+                float mx = sv[0];
+#pragma unroll
+                for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
                 mx = fmaxf(mx, shfl_xor_f(mx, 16));
                 mx = fmaxf(mx, shfl_xor_f(mx, 32));
-                const float m_new = fmaxf(m[nt], mx);
+                const float m_new = fmaxf(m[nt], mx * c);
                 const float mref = (m_new == kNegInf) ? 0.f : m_new;
                 const float alpha = fast_exp2(m[nt] - mref);
                 float ps = 0.f;
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    sv[i] = fast_exp2(sv[i] - mref);
+                    sv[i] = fast_exp2(__builtin_fmaf(sv[i], c, -mref));
                     ps += sv[i];
                 }
                 lsum[nt] = lsum[nt] * alpha + ps;
@@ -349,15 +400,98 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                 const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
                 const int w = dt >> 1;
                 uint4 av;
-                av.x = __builtin_amdgcn_perm(((const uint32_t*)&vin[0][1])[w], ((const uint32_t*)&vin[0][0])[w], sel);
-                av.y = __builtin_amdgcn_perm(((const uint32_t*)&vin[0][3])[w], ((const uint32_t*)&vin[0][2])[w], sel);
-                av.z = __builtin_amdgcn_perm(((const uint32_t*)&vin[1][1])[w], ((const uint32_t*)&vin[1][0])[w], sel);
-                av.w = __builtin_amdgcn_perm(((const uint32_t*)&vin[1][3])[w], ((const uint32_t*)&vin[1][2])[w], sel);
+                av.x = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][1])[w], ((const uint32_t*)&kv.v[0][0])[w], sel);
+                av.y = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][3])[w], ((const uint32_t*)&kv.v[0][2])[w], sel);
+                av.z = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][1])[w], ((const uint32_t*)&kv.v[1][0])[w], sel);
+                av.w = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][3])[w], ((const uint32_t*)&kv.v[1][2])[w], sel);
                 const bf16x8 A = __builtin_bit_cast(bf16x8, av);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
                     O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, pB[nt], O[dt][nt], 0, 0, 0);
             }
+        };
+
+        // Each wave streams the pairs w, w + 4, w + 8, ... of the split. The loads of the next
+        // pair are issued before the current pair is computed (two register buffers, unrolled).
+        // With four or more row tiles the accumulators leave no room for a second buffer.
+        KVPair bufA, bufB;
+        int pb = blk_begin + 2 * wave;
+        int a0 = -1, a1 = -1, b0 = -1, b1 = -1;
+        constexpr bool kDepth2 = KYRO_PREFETCH_DEPTH >= 2 && NT <= 2;
+        constexpr int kStep = 2 * kWaves;
+        if constexpr (kDepth2) {  // two pairs in flight while one is computed
+            KVPair bufC;
+            int c0 = -1, c1 = -1;
+            if (pb < blk_end) {
+                a0 = blk_at(pb);
+                a1 = blk_at(pb + 1);
+                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+            }
+            if (pb + kStep < blk_end) {
+                b0 = blk_at(pb + kStep);
+                b1 = blk_at(pb + kStep + 1);
+                load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+            }
+            while (pb < blk_end) {
+                int pf = pb + 2 * kStep;
+                if (pf < blk_end) {
+                    c0 = blk_at(pf);
+                    c1 = blk_at(pf + 1);
+                    load_pair(bufC, kp, vp, c0, c1, block_stride, kv_off, r, g);
+                }
+                compute(bufA, pb, a0, a1);
+                pb += kStep;
+                if (pb >= blk_end) break;
+                pf = pb + 2 * kStep;
+                if (pf < blk_end) {
+                    a0 = blk_at(pf);
+                    a1 = blk_at(pf + 1);
+                    load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                }
+                compute(bufB, pb, b0, b1);
+                pb += kStep;
+                if (pb >= blk_end) break;
+                pf = pb + 2 * kStep;
+                if (pf < blk_end) {
+                    b0 = blk_at(pf);
+                    b1 = blk_at(pf + 1);
+                    load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                }
+                compute(bufC, pb, c0, c1);
+                pb += kStep;
+            }
+        }
+        if constexpr (NT >= 4) {
+            for (; pb < blk_end; pb += 2 * kWaves) {
+                a0 = blk_at(pb);
+                a1 = blk_at(pb + 1);
+                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                compute(bufA, pb, a0, a1);
+            }
+        }
+        if (!kDepth2 && NT < 4 && pb < blk_end) {
+            a0 = blk_at(pb);
+            a1 = blk_at(pb + 1);
+            load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+        }
+        while (!kDepth2 && NT < 4 && pb < blk_end) {
+            int pn = pb + 2 * kWaves;
+            if (pn < blk_end) {
+                b0 = blk_at(pn);
+                b1 = blk_at(pn + 1);
+                load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+            }
+            compute(bufA, pb, a0, a1);
+            pb = pn;
+            if (pb >= blk_end) break;
+            pn = pb + 2 * kWaves;
+            if (pn < blk_end) {
+                a0 = blk_at(pn);
+                a1 = blk_at(pn + 1);
+                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+            }
+            compute(bufB, pb, b0, b1);
+            pb = pn;
         }
 
         // Row sums: each lane summed its own 8 tokens per pair; fold the four 16-lane groups.
@@ -407,7 +541,6 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
         __syncthreads();
     }
-    if (nsplit > 1) merge_splits<R, D>(a, si, unit, nsplit, frame);
 }
 
 // ---------------------------------------------------------------------------- vector kernel
@@ -589,7 +722,6 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
         frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
         __syncthreads();
     }
-    if (nsplit > 1) merge_splits<R, D>(a, si, unit, nsplit, frame);
 }
 
 }  // namespace
@@ -620,6 +752,11 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
             if (bf16) attn_vector_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
             else attn_vector_kernel<float, 64><<<grid, block, 0, stream>>>(a);
         }
+    }
+    if (a.splits > 1) {
+        const dim3 cgrid((unsigned)a.units);
+        if (a.D == 128) attn_combine_kernel<128><<<cgrid, block, 0, stream>>>(a);
+        else attn_combine_kernel<64><<<cgrid, block, 0, stream>>>(a);
     }
     return hipGetLastError();
 }

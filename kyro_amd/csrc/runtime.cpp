@@ -61,8 +61,6 @@ struct kyro_ctx_s {
     hipStream_t stream = nullptr;
     void* arena = nullptr;  // per-call scratch, stream-ordered
     size_t arena_bytes = 0;
-    int* counters = nullptr;  // attention split counters, zero between calls
-    size_t counters_n = 0;
     int* err = nullptr;  // device error word
 };
 
@@ -83,19 +81,6 @@ int ensure_arena(kyro_ctx ctx, size_t bytes) {
     ctx->arena_bytes = 0;
     KYRO_HIP(hipMalloc(&ctx->arena, want));
     ctx->arena_bytes = want;
-    return KYRO_OK;
-}
-
-int ensure_counters(kyro_ctx ctx, size_t n) {
-    if (n <= ctx->counters_n) return KYRO_OK;
-    const size_t want = align_up(std::max(n, ctx->counters_n * 2), 1024);
-    KYRO_HIP(hipStreamSynchronize(ctx->stream));
-    if (ctx->counters) KYRO_HIP(hipFree(ctx->counters));
-    ctx->counters = nullptr;
-    ctx->counters_n = 0;
-    KYRO_HIP(hipMalloc(reinterpret_cast<void**>(&ctx->counters), want * sizeof(int)));
-    KYRO_HIP(hipMemset(ctx->counters, 0, want * sizeof(int)));
-    ctx->counters_n = want;
     return KYRO_OK;
 }
 
@@ -175,7 +160,6 @@ int kyro_ctx_destroy(kyro_ctx ctx) {
         (void)hipStreamSynchronize(ctx->stream);
         if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
         if (ctx->arena) (void)hipFree(ctx->arena);
-        if (ctx->counters) (void)hipFree(ctx->counters);
         if (ctx->err) (void)hipFree(ctx->err);
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
@@ -361,13 +345,18 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         const int mb = std::max(1, p->max_blocks_per_seq);
         int splits = p->num_splits;
         if (splits <= 0) {
-            const int want_wgs = 1024;
-            splits = std::max(1, (want_wgs + a.units - 1) / a.units);
-            splits = std::min(splits, std::max(1, mb / 16));
+            // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
+            // one CU streaming it alone; more splits only when the units cannot cover the chip's
+            // 256 CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
+            constexpr int kTargetChunk = 256, kCUs = 256, kMinChunk = 16;
+            splits = (mb + kTargetChunk - 1) / kTargetChunk;
+            if (a.units * splits < kCUs)
+                splits = std::min((kCUs + a.units - 1) / a.units, std::max(1, mb / kMinChunk));
         }
         splits = std::min(splits, mb);
+        splits = std::max(splits, (mb + kyro::kMaxChunkBlocks - 1) / kyro::kMaxChunkBlocks);
         int chunk = (mb + splits - 1) / splits;
-        chunk = (chunk + 1) / 2 * 2;
+        chunk = std::min((chunk + 1) / 2 * 2, kyro::kMaxChunkBlocks);
         splits = (mb + chunk - 1) / chunk;
         a.splits = splits;
         a.chunk_blocks = chunk;
@@ -379,12 +368,10 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             const size_t rows = (size_t)a.units * splits * a.rows_cap;
             ws_bytes = align_up(rows * sizeof(float), 256) * 2 + align_up(rows * a.D * sizeof(float), 256);
             if (int rc = ensure_arena(ctx, ws_bytes)) return rc;
-            if (int rc = ensure_counters(ctx, (size_t)a.units)) return rc;
             char* base = static_cast<char*>(ctx->arena);
             a.ws_m = reinterpret_cast<float*>(base);
             a.ws_l = reinterpret_cast<float*>(base + align_up(rows * sizeof(float), 256));
             a.ws_acc = reinterpret_cast<float*>(base + 2 * align_up(rows * sizeof(float), 256));
-            a.counters = ctx->counters;
         }
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_paged_attention(a, kernel, ctx->stream));
@@ -402,8 +389,8 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         if (!p) return fail(KYRO_EINVAL, "spec_verify: params is null");
         if (p->batch_size < 0 || p->max_draft < 0 || p->vocab_size <= 0)
             return fail(KYRO_EINVAL, "spec_verify: need batch_size >= 0, max_draft >= 0, vocab_size > 0");
-        if (p->max_draft > 63)
-            return fail(KYRO_EUNSUPPORTED, "spec_verify: max_draft %d > 63", p->max_draft);
+        if (p->max_draft > kyro::kMaxDraft)
+            return fail(KYRO_EUNSUPPORTED, "spec_verify: max_draft %d > %d", p->max_draft, kyro::kMaxDraft);
         if (p->logits_dtype != KYRO_F32)
             return fail(KYRO_EUNSUPPORTED, "spec_verify: logits_dtype must be KYRO_F32");
         if (p->batch_size == 0) return KYRO_OK;
@@ -434,13 +421,15 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         const size_t stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
         const size_t plan_b = align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
         const size_t csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
+        const size_t gath_b = align_up((size_t)a.B * (2 * a.kmax + 1) * sizeof(float), 256);
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b)) return rc;
+        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b + gath_b)) return rc;
         char* base = static_cast<char*>(ctx->arena);
         a.stats = reinterpret_cast<float2*>(base);
         a.plan = reinterpret_cast<kyro::SpecPlan*>(base + stats_b);
         a.csum = reinterpret_cast<float2*>(base + stats_b + plan_b);
+        a.gath = reinterpret_cast<float*>(base + stats_b + plan_b + csum_b);
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_spec_verify(a, ctx->stream));
         return KYRO_OK;

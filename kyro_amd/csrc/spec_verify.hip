@@ -5,18 +5,22 @@
 // first rejection, from p after full acceptance) and the greedy argmax-match rule of the reference
 // when T <= 0. Draws are sample_token's inverse-CDF walk in index order (src/worker.rs:352-360).
 //
-// Four stream-ordered kernels, sized so the dominant pass spreads over the whole chip:
-//   1. spec_stats_kernel      grid (sequence x vocab chunk, row): one streaming pass over every
-//                              needed logit row; per chunk {max, sum exp2((x - max) log2e / T)},
-//                              or {max, first argmax} for greedy rows. Draft rows of greedy
-//                              sequences and rows past a sequence's k are never read.
-//   2. spec_accept_kernel     one wave per sequence: merges the chunk statistics, evaluates
-//                              u_i q_i(x_i) < p_i(x_i) in lane i and finds the first rejection
-//                              with a ballot; greedy sequences finish here.
-//   3. spec_resample_kernel   grid (sequence x vocab chunk): residual (and p) mass per chunk of the
-//                              one row that is resampled.
-//   4. spec_pick_kernel       one workgroup per sequence: locates the chunk holding u * total,
-//                              then walks that chunk in index order with a block scan.
+// Three stream-ordered kernels, sized so the dominant pass spreads over the whole chip:
+//   1. spec_stats_kernel     grid (sequence x vocab chunk, row): one streaming pass over every
+//                             needed logit row; per chunk {max, sum exp2((x - max) log2e / T)},
+//                             or {max, first argmax} for greedy rows, and the logit at the
+//                             row's draft token as it streams past. Draft rows of greedy
+//                             sequences and rows past a sequence's k are never read.
+//   2. spec_resample_kernel  grid (sequence x vocab chunk): wave 0 of every workgroup merges the
+//                             sequence's chunk statistics and runs the acceptance scan (lane i
+//                             tests u_i q_i(x_i) < p_i(x_i), a ballot finds the first rejection);
+//                             the chunk-0 workgroup stores the outputs. Then the workgroup sums the
+//                             residual (and p) mass of its chunk of the one row to resample.
+//   3. spec_pick_kernel      one workgroup per sequence: locates the chunk holding u * total with
+//                             a block scan of the chunk sums, then walks that chunk in index order.
+// Right after the streaming pass every dependent global round trip costs microseconds (cold
+// caches and translations), so each kernel issues all loads that do not depend on another load
+// at entry, and acceptance is recomputed per workgroup rather than handed over by a launch.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -55,13 +59,18 @@ __device__ __forceinline__ ArgMax argmax_pick(ArgMax a, ArgMax b) {
     return (b.v > a.v || (b.v == a.v && b.i < a.i)) ? b : a;
 }
 
-__device__ ArgMax block_argmax(ArgMax x, float* shv, int* shi) {
+__device__ __forceinline__ ArgMax wave_argmax(ArgMax x) {
     for (int m = 32; m >= 1; m >>= 1) {
         ArgMax o;
         o.v = __shfl_xor(x.v, m, 64);
         o.i = __shfl_xor(x.i, m, 64);
         x = argmax_pick(x, o);
     }
+    return x;
+}
+
+__device__ ArgMax block_argmax(ArgMax x, float* shv, int* shi) {
+    x = wave_argmax(x);
     if ((threadIdx.x & 63) == 0) {
         shv[threadIdx.x >> 6] = x.v;
         shi[threadIdx.x >> 6] = x.i;
@@ -141,12 +150,14 @@ __device__ __forceinline__ float draw_mass(const SpecPlan& pl, float t, float d,
     return fmaxf(p - q, 0.f);
 }
 
+// ------------------------------------------------------------------------- pass 1: statistics
+
 __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     __shared__ float shv[4];
     __shared__ int shi[4];
     const int c = blockIdx.x % a.C, b = blockIdx.x / a.C, row = blockIdx.y;
     const int k = a.num_draft[b];
-    if (k < 0 || k > a.kmax) return;  // reported by spec_accept_kernel
+    if (k < 0 || k > a.kmax) return;  // reported by the acceptance pass
     const float T = a.temperature[b];
     const bool greedy = !(T > 0.f);
     const float* base;
@@ -160,9 +171,17 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     }
     const int v0 = c * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
+    // Sampled rows below k also hand their draft token's logit to the acceptance pass.
+    const int pos = row <= a.kmax ? row : row - a.kmax - 1;
+    const uint32_t tok = (!greedy && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
     float x[kPer];
     int idx[kPer];
     load_chunk_strided(base, v0, v1, a.vec4, x, idx);
+    if (tok >= (uint32_t)v0 && tok < (uint32_t)v1) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (idx[i] == (int)tok) a.gath[(size_t)b * (2 * a.kmax + 1) + row] = x[i];
+    }
     float2* out = a.stats + ((size_t)b * (2 * a.kmax + 1) + row) * a.C + c;
     if (greedy) {
         ArgMax best = {kNegInf, 0x7fffffff};
@@ -187,109 +206,309 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     if (threadIdx.x == 0) *out = make_float2(m, s);
 }
 
-// Merges the per-chunk {max, sum} of one row into {max, 1 / sum}.
-__device__ __forceinline__ void merge_row(const float2* st, int C, float c2, float& m, float& inv_z) {
-    m = kNegInf;
-    for (int c = 0; c < C; ++c) m = fmaxf(m, st[c].x);
-    float z = 0.f;
-    if (m != kNegInf)
-        for (int c = 0; c < C; ++c) z += st[c].y * fast_exp2((st[c].x - m) * c2);
-    inv_z = z > 0.f ? 1.f / z : 0.f;
+// ------------------------------------------------------------------------- pass 2: acceptance
+
+// Folds chunk statistic y into the running (max, sum) x of one lane.
+__device__ __forceinline__ float2 fold_stats(float2 x, float2 y, float c2) {
+    const float m = fmaxf(x.x, y.x);
+    if (m == kNegInf) return x;
+    return make_float2(m, x.y * fast_exp2((x.x - m) * c2) + y.y * fast_exp2((y.x - m) * c2));
 }
 
-__device__ __forceinline__ int merge_argmax(const float2* st, int C) {
-    ArgMax best = {st[0].x, __float_as_int(st[0].y)};
-    for (int c = 1; c < C; ++c) best = argmax_pick(best, ArgMax{st[c].x, __float_as_int(st[c].y)});
-    return best.i;
-}
+struct AcceptShared {
+    SpecPlan plan;
+};
 
-__global__ __launch_bounds__(64) void spec_accept_kernel(SpecArgs a) {
-    const int b = blockIdx.x;
+constexpr int kChunkGroup = 16;  // chunk statistics a lane folds per batch of loads
+
+// Acceptance of sequence b, run by the first wave of a workgroup, in one round of loads (the
+// draft tokens' logits were captured by the statistics pass). Lane r owns statistics row r
+// (and row r + 64 when there are more than 64) and folds that row's chunk statistics itself;
+// lane i then decides draft i, reading the rows it needs from their owners with shuffles, and a
+// ballot finds the first rejection. When `writer` is set the sequence's outputs are stored.
+// The plan for the draw lands in sh.plan.
+__device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptShared& sh) {
     const int lane = threadIdx.x;
+    const int R = 2 * a.kmax + 1;
+    const int C = a.C;
+    const float2* st = a.stats + (size_t)b * R * C;
+    const int r0 = lane, r1 = lane + 64;
+    // Round 1: every load that does not depend on another load.
     const int k = a.num_draft[b];
-    uint32_t* toks = a.out_tokens + (size_t)b * (a.kmax + 1);
-    SpecPlan* plan = a.plan + b;
+    const float T = a.temperature[b];
+    const float ures = a.u_res[b];
+    uint32_t x = 0;
+    float u = 0.f, tx = 0.f, dx = 0.f;
     if (lane < a.kmax) {
+        x = a.draft_tokens[(size_t)b * a.kmax + lane];
+        u = a.u_accept[(size_t)b * a.kmax + lane];
+        tx = a.gath[(size_t)b * R + lane];               // target logit at x (sampled, lane < k)
+        dx = a.gath[(size_t)b * R + a.kmax + 1 + lane];  // draft logit at x
+    }
+    float2 y0[kChunkGroup], y1[kChunkGroup];
+#pragma unroll
+    for (int i = 0; i < kChunkGroup; ++i) {
+        y0[i] = (r0 < R && i < C) ? st[(size_t)r0 * C + i] : make_float2(kNegInf, 0.f);
+        y1[i] = (r1 < R && i < C) ? st[(size_t)r1 * C + i] : make_float2(kNegInf, 0.f);
+    }
+
+    uint32_t* toks = a.out_tokens + (size_t)b * (a.kmax + 1);
+    const bool greedy = !(T > 0.f);
+    int err = 0;
+    if (k < 0 || k > a.kmax) err = ERR_NUM_DRAFT;
+    else if (!greedy && k > 0 && a.draft == nullptr) err = ERR_NO_DRAFT;
+    else if (__any(lane < k && x >= (uint32_t)a.V)) err = ERR_TOKEN;
+    if (writer && lane < a.kmax) {
         if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = __builtin_nanf("");
         if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = __builtin_nanf("");
     }
-    if (k < 0 || k > a.kmax) {
-        if (lane == 0) {
-            latch_error(a.err, ERR_NUM_DRAFT);
-            a.out_accepted[b] = 0;
-            plan->mode = SPEC_DONE;
+    if (err) {
+        if (writer) {
+            if (lane == 0) {
+                latch_error(a.err, err);
+                a.out_accepted[b] = 0;
+                a.plan[b].mode = SPEC_DONE;
+            }
+            if (lane <= a.kmax) toks[lane] = 0xFFFFFFFFu;
         }
-        if (lane <= a.kmax) toks[lane] = 0xFFFFFFFFu;
-        return;
-    }
-    const float T = a.temperature[b];
-    const bool greedy = !(T > 0.f);
-    if (!greedy && k > 0 && a.draft == nullptr) {  // sampled drafts need draft logits
-        if (lane == 0) {
-            latch_error(a.err, ERR_NO_DRAFT);
-            a.out_accepted[b] = 0;
-            plan->mode = SPEC_DONE;
-        }
-        if (lane <= a.kmax) toks[lane] = 0xFFFFFFFFu;
+        if (lane == 0) sh.plan.mode = SPEC_DONE;
         return;
     }
     const float c2 = greedy ? 0.f : kLog2e / T;
-    const float2* st = a.stats + (size_t)b * (2 * a.kmax + 1) * a.C;
-    bool accept = true, bad = false;
-    uint32_t x = 0;
-    if (lane < k) {
-        x = a.draft_tokens[(size_t)b * a.kmax + lane];
-        if (x >= (uint32_t)a.V) {
-            bad = true;
-        } else if (greedy) {
-            accept = merge_argmax(st + (size_t)lane * a.C, a.C) == (int)x;
+    // Fold the owned rows. Rows that were not computed hold stale values and are never read.
+    float m0 = kNegInf, m1 = kNegInf, z0 = 0.f, z1 = 0.f;  // sampled: running max and sum
+    ArgMax g0 = {kNegInf, 0x7fffffff}, g1 = g0;             // greedy: running first argmax
+    for (int cb = 0; cb < C; cb += kChunkGroup) {
+        if (cb > 0) {  // more than kChunkGroup chunks: next batch of loads
+#pragma unroll
+            for (int i = 0; i < kChunkGroup; ++i) {
+                const int c = cb + i;
+                y0[i] = (r0 < R && c < C) ? st[(size_t)r0 * C + c] : make_float2(kNegInf, 0.f);
+                y1[i] = (r1 < R && c < C) ? st[(size_t)r1 * C + c] : make_float2(kNegInf, 0.f);
+            }
+        }
+        if (greedy) {
+#pragma unroll
+            for (int i = 0; i < kChunkGroup; ++i) {
+                if (cb + i >= C) continue;
+                g0 = argmax_pick(g0, ArgMax{y0[i].x, __float_as_int(y0[i].y)});
+                g1 = argmax_pick(g1, ArgMax{y1[i].x, __float_as_int(y1[i].y)});
+            }
         } else {
-            float mt, izt, md, izd;
-            merge_row(st + (size_t)lane * a.C, a.C, c2, mt, izt);
-            merge_row(st + (size_t)(a.kmax + 1 + lane) * a.C, a.C, c2, md, izd);
-            const float p = fast_exp2((target_row(a, b, lane)[x] - mt) * c2) * izt;
-            const float q = fast_exp2((draft_row(a, b, lane)[x] - md) * c2) * izd;
-            const float u = a.u_accept[(size_t)b * a.kmax + lane];
-            accept = !(q > 0.f) || (u * q < p);
-            if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = p;
-            if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = q;
+            float b0 = kNegInf, b1 = kNegInf;
+#pragma unroll
+            for (int i = 0; i < kChunkGroup; ++i) {
+                b0 = fmaxf(b0, y0[i].x);
+                b1 = fmaxf(b1, y1[i].x);
+            }
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < kChunkGroup; ++i) {
+                if (y0[i].x != kNegInf) s0 += y0[i].y * fast_exp2((y0[i].x - b0) * c2);
+                if (y1[i].x != kNegInf) s1 += y1[i].y * fast_exp2((y1[i].x - b1) * c2);
+            }
+            const float2 f0 = fold_stats(make_float2(m0, z0), make_float2(b0, s0), c2);
+            const float2 f1 = fold_stats(make_float2(m1, z1), make_float2(b1, s1), c2);
+            m0 = f0.x;
+            z0 = f0.y;
+            m1 = f1.x;
+            z1 = f1.y;
         }
     }
-    if (__any(bad)) {
-        if (lane == 0) {
-            latch_error(a.err, ERR_TOKEN);
-            a.out_accepted[b] = 0;
-            plan->mode = SPEC_DONE;
+    const float iz0 = z0 > 0.f ? 1.f / z0 : 0.f;
+    const float iz1 = z1 > 0.f ? 1.f / z1 : 0.f;
+    // Value of statistics row rho from its owner lane (every lane takes part in both shuffles).
+    auto row_val = [&](float v0, float v1, int rho) {
+        const float w0 = __shfl(v0, rho & 63, 64);
+        const float w1 = __shfl(v1, rho & 63, 64);
+        return rho < 64 ? w0 : w1;
+    };
+    auto row_arg = [&](int rho) {
+        const int w0 = __shfl(g0.i, rho & 63, 64);
+        const int w1 = __shfl(g1.i, rho & 63, 64);
+        return rho < 64 ? w0 : w1;
+    };
+    bool accept = true;
+    const int dr = a.kmax + 1 + lane;  // this lane's draft row
+    if (greedy) {
+        const int top = row_arg(lane);
+        accept = lane >= k || top == (int)x;
+    } else {
+        const float mt = row_val(m0, m1, lane), izt = row_val(iz0, iz1, lane);
+        const float md = row_val(m0, m1, dr), izd = row_val(iz0, iz1, dr);
+        if (lane < k) {
+            const float p = fast_exp2((tx - mt) * c2) * izt;
+            const float q = fast_exp2((dx - md) * c2) * izd;
+            accept = !(q > 0.f) || (u * q < p);
+            if (writer) {
+                if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = p;
+                if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = q;
+            }
         }
-        if (lane <= a.kmax) toks[lane] = 0xFFFFFFFFu;
-        return;
     }
     const unsigned long long rejected = __ballot(lane < k && !accept);
     const int j = rejected ? __ffsll((long long)rejected) - 1 : k;
-    if (lane <= a.kmax) toks[lane] = (lane < j) ? x : 0xFFFFFFFFu;
+    if (writer && lane <= a.kmax) toks[lane] = (lane < j) ? x : 0xFFFFFFFFu;
+    // Row j's statistics (uniform source lane, so every lane shuffles).
+    const int jt = greedy ? row_arg(j) : 0;
+    const float mj = row_val(m0, m1, j), izj = row_val(iz0, iz1, j);
+    const float mdj = row_val(m0, m1, a.kmax + 1 + j), izdj = row_val(iz0, iz1, a.kmax + 1 + j);
     if (lane != 0) return;
-    a.out_accepted[b] = j;
-    if (greedy) {
-        toks[j] = (uint32_t)merge_argmax(st + (size_t)j * a.C, a.C);
-        plan->mode = SPEC_DONE;
-        return;
-    }
     SpecPlan pl;
-    pl.mode = j < k ? SPEC_RESIDUAL : SPEC_PLAIN;
     pl.row = j;
-    pl.c2 = c2;
-    pl.u = a.u_res[b];
-    merge_row(st + (size_t)j * a.C, a.C, c2, pl.mt, pl.inv_zt);
-    pl.md = 0.f;
-    pl.inv_zd = 0.f;
-    if (j < k) merge_row(st + (size_t)(a.kmax + 1 + j) * a.C, a.C, c2, pl.md, pl.inv_zd);
-    *plan = pl;
+    if (greedy) {
+        pl.mode = SPEC_DONE;
+        if (writer) toks[j] = (uint32_t)jt;
+    } else {
+        pl.mode = j < k ? SPEC_RESIDUAL : SPEC_PLAIN;
+        pl.c2 = c2;
+        pl.u = ures;
+        pl.mt = mj;
+        pl.inv_zt = izj;
+        pl.md = j < k ? mdj : 0.f;
+        pl.inv_zd = j < k ? izdj : 0.f;
+    }
+    if (writer) {
+        a.out_accepted[b] = j;
+        a.plan[b] = pl;
+    }
+    sh.plan = pl;
 }
 
+struct DrawShared {
+    int chunk, last_chunk, pick, last;
+    float rem;
+    float wsum[4];
+    float red[8];
+};
+
+// Inverse-CDF draw for sequence b from its chunk sums (a.csum; my_r / my_p are this thread's
+// run totals, loaded by the caller), run by a whole workgroup.
+// Locates the chunk holding u * total with a block scan of the chunk masses (thread t owns the
+// contiguous run [t * per, t * per + per), so the scan keeps index order), then walks that
+// chunk in index order and stores the token at out_tokens[b][pl.row].
+__device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawShared& ds,
+                           float my_r, float my_p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float2* cs = a.csum + (size_t)b * a.C;
+    const int per = (a.C + kT - 1) / kT;
+    const int c0 = threadIdx.x * per;
+    if (threadIdx.x == 0) {
+        ds.chunk = 0x7fffffff;
+        ds.last_chunk = -1;
+        ds.pick = 0x7fffffff;
+        ds.last = -1;
+    }
+    float R = wave_sum(my_r), P = wave_sum(my_p);
+    if (lane == 0) {
+        ds.red[wave] = R;
+        ds.red[4 + wave] = P;
+    }
+    __syncthreads();
+    R = (ds.red[0] + ds.red[1]) + (ds.red[2] + ds.red[3]);
+    P = (ds.red[4] + ds.red[5]) + (ds.red[6] + ds.red[7]);
+    // A residual that vanished (p == q up to rounding) falls back to drawing from p.
+    const bool use_res = (pl.mode == SPEC_RESIDUAL) && R > 0.f;
+    const float target = pl.u * (use_res ? R : P);
+    const float mine = use_res ? my_r : my_p;
+    float inc = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += y;
+    }
+    if (lane == 63) ds.wsum[wave] = inc;
+    __syncthreads();
+    float ex = inc - mine;
+    for (int w2 = 0; w2 < wave; ++w2) ex += ds.wsum[w2];
+    if (mine > 0.f) {
+        if (ex + mine >= target) {
+            float cum = ex;  // walk this thread's run in order
+            for (int c = c0; c < min(a.C, c0 + per); ++c) {
+                const float w = use_res ? cs[c].x : cs[c].y;
+                if (w > 0.f && cum + w >= target) {
+                    atomicMin(&ds.chunk, c);
+                    break;
+                }
+                cum += w;
+            }
+        }
+        for (int c = min(a.C, c0 + per) - 1; c >= c0; --c)
+            if ((use_res ? cs[c].x : cs[c].y) > 0.f) {
+                atomicMax(&ds.last_chunk, c);
+                break;
+            }
+    }
+    __syncthreads();
+    // The thread whose run holds the winning chunk derives the remainder from its scan prefix.
+    const int won = ds.chunk;
+    if (won != 0x7fffffff && won >= c0 && won < c0 + per) {
+        float cum = ex;
+        for (int c = c0; c < won; ++c) cum += use_res ? cs[c].x : cs[c].y;
+        ds.rem = target - cum;
+    } else if (won == 0x7fffffff && threadIdx.x == 0) {  // rounding left u * total past the end
+        ds.chunk = ds.last_chunk < 0 ? a.C - 1 : ds.last_chunk;
+        ds.rem = __builtin_huge_valf();
+    }
+    __syncthreads();
+    const int chunk = ds.chunk;
+    const float rem = ds.rem;
+    const int v0 = chunk * a.chunk;
+    const int v1 = min(a.V, v0 + a.chunk);
+    float t[kPer], d[kPer], w[kPer];
+    int idx[kPer];
+    load_chunk_contig(target_row(a, b, pl.row), v0, v1, a.vec4, t, idx);
+    if (use_res) load_chunk_contig(draft_row(a, b, pl.row), v0, v1, a.vec4, d, idx);
+    float ts = 0.f;
+    int my_last = -1;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        w[i] = idx[i] >= 0 ? draw_mass(pl, t[i], use_res ? d[i] : 0.f, use_res) : 0.f;
+        ts += w[i];
+        if (w[i] > 0.f) my_last = idx[i];
+    }
+    // Exclusive scan of the per-thread sums in thread (= index) order.
+    float inc2 = ts;
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(inc2, o, 64);
+        if (lane >= o) inc2 += y;
+    }
+    if (lane == 63) ds.wsum[wave] = inc2;
+    __syncthreads();
+    float ex2 = inc2 - ts;
+    for (int w2 = 0; w2 < wave; ++w2) ex2 += ds.wsum[w2];
+    if (ex2 < rem && ex2 + ts >= rem) {
+        float cum = ex2;
+        int pick = my_last;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            if (w[i] > 0.f) {
+                cum += w[i];
+                if (cum >= rem) {
+                    pick = idx[i];
+                    break;
+                }
+            }
+        }
+        atomicMin(&ds.pick, pick);
+    }
+    atomicMax(&ds.last, my_last);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int v = ds.pick != 0x7fffffff ? ds.pick : ds.last;
+        if (v < 0) v = v1 - 1;
+        a.out_tokens[(size_t)b * (a.kmax + 1) + pl.row] = (uint32_t)v;
+    }
+}
+
+// Acceptance (wave 0, redundantly per chunk workgroup) fused with the residual mass of one chunk
+// of the resampled row.
 __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
+    __shared__ AcceptShared acc;
     __shared__ float sh[4];
     const int c = blockIdx.x % a.C, b = blockIdx.x / a.C;
-    const SpecPlan pl = a.plan[b];
+    if (threadIdx.x < 64) accept_sequence(a, b, c == 0, acc);
+    __syncthreads();
+    const SpecPlan pl = acc.plan;
     if (pl.mode == SPEC_DONE) return;
     const bool residual = pl.mode == SPEC_RESIDUAL;
     const int v0 = c * a.chunk;
@@ -311,101 +530,24 @@ __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
     if (threadIdx.x == 0) a.csum[(size_t)b * a.C + c] = make_float2(sr, sp);
 }
 
+// ------------------------------------------------------------------------------- pass 3: draw
+
 __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
-    __shared__ int s_chunk;
-    __shared__ float s_rem;
-    __shared__ int s_use_res;
-    __shared__ float s_wsum[4];
-    __shared__ int s_pick;
-    __shared__ int s_last;
+    __shared__ DrawShared ds;
     const int b = blockIdx.x;
+    // The chunk sums and the plan are independent loads: issue both before using either.
+    const float2* cs = a.csum + (size_t)b * a.C;
+    const int per = (a.C + kT - 1) / kT;
+    const int c0 = threadIdx.x * per;
+    float my_r = 0.f, my_p = 0.f;
+    for (int c = c0; c < min(a.C, c0 + per); ++c) {
+        const float2 w = cs[c];
+        my_r += w.x;
+        my_p += w.y;
+    }
     const SpecPlan pl = a.plan[b];
     if (pl.mode == SPEC_DONE) return;
-    const float2* cs = a.csum + (size_t)b * a.C;
-    if (threadIdx.x == 0) {
-        float R = 0.f, P = 0.f;
-        for (int c = 0; c < a.C; ++c) {
-            R += cs[c].x;
-            P += cs[c].y;
-        }
-        const int use_res = (pl.mode == SPEC_RESIDUAL) && R > 0.f;
-        const float target = pl.u * (use_res ? R : P);
-        float cum = 0.f;
-        int chunk = -1, last_pos = -1;
-        float rem = 0.f;
-        for (int c = 0; c < a.C; ++c) {
-            const float w = use_res ? cs[c].x : cs[c].y;
-            if (w > 0.f) {
-                last_pos = c;
-                if (cum + w >= target) {
-                    chunk = c;
-                    rem = target - cum;
-                    break;
-                }
-            }
-            cum += w;
-        }
-        if (chunk < 0) {  // rounding left u * total beyond the last boundary
-            chunk = last_pos < 0 ? a.C - 1 : last_pos;
-            rem = __builtin_huge_valf();
-        }
-        s_chunk = chunk;
-        s_rem = rem;
-        s_use_res = use_res;
-        s_pick = 0x7fffffff;
-        s_last = -1;
-    }
-    __syncthreads();
-    const int chunk = s_chunk;
-    const float rem = s_rem;
-    const bool residual = s_use_res != 0;
-    const int v0 = chunk * a.chunk;
-    const int v1 = min(a.V, v0 + a.chunk);
-    float t[kPer], d[kPer], w[kPer];
-    int idx[kPer];
-    load_chunk_contig(target_row(a, b, pl.row), v0, v1, a.vec4, t, idx);
-    if (residual) load_chunk_contig(draft_row(a, b, pl.row), v0, v1, a.vec4, d, idx);
-    float ts = 0.f;
-    int my_last = -1;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        w[i] = idx[i] >= 0 ? draw_mass(pl, t[i], residual ? d[i] : 0.f, residual) : 0.f;
-        ts += w[i];
-        if (w[i] > 0.f) my_last = idx[i];
-    }
-    // Exclusive scan of the per-thread sums in thread (= index) order.
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float inc = ts;
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += y;
-    }
-    if (lane == 63) s_wsum[wave] = inc;
-    __syncthreads();
-    float ex = inc - ts;
-    for (int w2 = 0; w2 < wave; ++w2) ex += s_wsum[w2];
-    if (ex < rem && ex + ts >= rem) {
-        float cum = ex;
-        int pick = my_last;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            if (w[i] > 0.f) {
-                cum += w[i];
-                if (cum >= rem) {
-                    pick = idx[i];
-                    break;
-                }
-            }
-        }
-        atomicMin(&s_pick, pick);
-    }
-    atomicMax(&s_last, my_last);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int v = s_pick != 0x7fffffff ? s_pick : s_last;
-        if (v < 0) v = v1 - 1;
-        a.out_tokens[(size_t)b * (a.kmax + 1) + pl.row] = (uint32_t)v;
-    }
+    draw_token(a, b, pl, ds, my_r, my_p);
 }
 
 }  // namespace
@@ -413,7 +555,6 @@ __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
     spec_stats_kernel<<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
-    spec_accept_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
     spec_resample_kernel<<<dim3(a.C * a.B), kT, 0, stream>>>(a);
     spec_pick_kernel<<<dim3(a.B), kT, 0, stream>>>(a);
     return hipGetLastError();
