@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -109,9 +110,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--path", default="auto", choices=["auto", "vector", "mfma"])
     ap.add_argument("--splits", type=int, default=0, help="context splits (0 = automatic)")
-    ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+
+        n = args.calibrate_copy << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "copies": 5}))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} (WORLD_SIZE {world}) is not supported; "
@@ -168,10 +183,13 @@ def main():
     step_gbs = (a_bytes + s_bytes) / sec_per_step / 1e9
 
     traffic = None
-    pmc_path = os.path.join(ROOT, "profiles", "attention_llama3_8b_pmc.json")
+    # HBM bytes per attention launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded
+    # in profiles/ (counters need runs of their own, so they are not read live here).
+    pmc_path = os.path.join(ROOT, "profiles", "attention_llama3_8b_pmc.md")
     if os.path.exists(pmc_path):
         with open(pmc_path) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            m = re.search(r"^hbm_bytes_per_launch:\s*(\d+)", f.read(), flags=re.M)
+        traffic = int(m.group(1)) if m else None
 
     baseline = None
     if not args.no_cpu_baseline:

@@ -200,3 +200,19 @@ def test_host_validation(gpu):
     with pytest.raises(kyro_amd.KyroError, match="MFMA"):
         attn.forward(q, kv, kv, torch.zeros((1, 4), dtype=torch.int64, device=gpu),
                      torch.tensor([4], device=gpu), path="mfma")
+
+
+@pytest.mark.parametrize("path", ["vector", "mfma"])
+def test_mha_b2_matches_golden_fixture(gpu, path):
+    """Committed expected outputs (tests/golden/attention_mha_b2.npz): Llama-2-7B heads, bf16."""
+    import os
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "attention_mha_b2.npz"))
+    case = wl.make_attention_case(context_lens=[17, 40], q_lens=[5, 5], num_heads=32, num_kv_heads=32,
+                                  dtype="bf16", seed=0)
+    t = h.attention_tensors(case, gpu)
+    out = make_attention(16, 32, 128, 32).forward(
+        t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+        q_start_loc=t["q_start_loc"], path=path)
+    err = (out.cpu().numpy() - z["expected"]).__abs__().max()
+    assert err <= h.ATOL_BF16, err

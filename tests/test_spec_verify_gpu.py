@@ -127,3 +127,23 @@ def test_bad_inputs_raise_and_recover(gpu):
     with pytest.raises(kyro_amd.KyroError, match="draft token"):
         kyro_amd.verify_drafts(**bad)
     h.assert_verify_parity(kyro_amd.verify_drafts(**t, return_probs=True), case, h.oracle_verify(case))
+
+
+def test_rejection_only_b8_matches_golden_fixture(gpu):
+    """Committed expected outputs (tests/golden/rejection_b8.json), same exemption rule."""
+    import json
+    import os
+
+    with open(os.path.join(os.path.dirname(__file__), "golden", "rejection_b8.json")) as f:
+        g = json.load(f)
+    case = wl.rejection_only_b8()
+    res = run(case, gpu)
+    fixture = {
+        "accepted": np.array(g["accepted"], np.int32),
+        "tokens": np.array(g["tokens"], np.uint32),
+        "accept_margin": np.array([[np.nan if v is None else v for v in r] for r in g["accept_margin"]]),
+        "resample_margin": np.array(g["resample_margin"]),
+        "p_draft": np.array([[np.nan if v is None else v for v in r] for r in g["p_draft"]]),
+        "q_draft": np.array([[np.nan if v is None else v for v in r] for r in g["q_draft"]]),
+    }
+    h.assert_verify_parity(res, case, fixture)
