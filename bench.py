@@ -103,6 +103,87 @@ def cpu_baseline(sample: int, threads: int):
     }
 
 
+def _median_us(fn, warmup, steps):
+    """Median per-call time of fn() in µs from HIP events on the current stream."""
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    for _ in range(warmup):
+        fn()
+    kyro_amd.sync(0)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    kyro_amd.sync(0)
+    return float(np.median([e0.elapsed_time(e1) for e0, e1 in ev])) * 1e3
+
+
+def other_workload(name, warmup, steps):
+    """One JSON line for a non-default workload: the attention kernel (when the workload has one)
+    and the sampler (when it has one), each on its algorithmic bytes. Inputs come from
+    kyro_amd.workloads (seeded numpy), uploaded before timing."""
+    import torch
+
+    import kyro_amd
+    from kyro_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+
+    def up(a, bf16=False):
+        t = torch.from_numpy(a)
+        return (t.view(torch.bfloat16) if bf16 else t).to(dev)
+
+    acase = vcase = None
+    if name == "mha-llama2-7b":
+        acase = wl.mha_llama2_7b()
+    elif name == "rejection-b8":
+        vcase = wl.rejection_only_b8()
+    elif name == "skewed-prefix":
+        acase, vcase = wl.skewed_prefix(), wl.verify_skewed()
+    elif name == "mixed-llama3-70b":
+        acase, k = wl.mixed_llama3_70b()
+        vcase = wl.verify_mixed(k)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    line = {"workload": name}
+    total_us = 0.0
+    if acase is not None:
+        bf16 = acase.dtype == "bf16"
+        t = dict(q=up(acase.query, bf16), kc=up(acase.key_cache, bf16), vc=up(acase.value_cache, bf16),
+                 table=up(acase.block_table), ctx=up(acase.context_lens), qs=up(acase.q_start_loc))
+        attn = kyro_amd.PagedAttention(acase.block_size, acase.num_heads, acase.head_dim, acase.num_kv_heads)
+        out = torch.empty(t["q"].shape, dtype=torch.bfloat16, device=dev)
+        logical = acase.kv_bytes() + acase.q_out_bytes(2)
+        unique = acase.unique_kv_bytes() + acase.q_out_bytes(2)
+        res = {"logical_bytes": logical, "unique_bytes": unique, "context_tokens": int(acase.context_lens.sum())}
+        for path in ("auto", "vector", "mfma"):
+            us = _median_us(lambda: attn.forward_async(
+                t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"],
+                max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
+            res[path] = {"us": us, "GB_s_unique": unique / us / 1e3, "frac_unique": unique / us / 1e3 / PEAK_HBM_GBS,
+                         "GB_s_logical": logical / us / 1e3}
+        line["attention"] = res
+        total_us += res["auto"]["us"]
+    if vcase is not None:
+        vt = dict(target_logits=up(vcase.target), draft_logits=up(vcase.draft),
+                  draft_tokens=up(vcase.draft_tokens.astype("int32")), num_draft=up(vcase.num_draft),
+                  temperature=up(vcase.temperature), u_accept=up(vcase.u_accept), u_resample=up(vcase.u_resample))
+        us = _median_us(lambda: kyro_amd.verify_drafts_async(**vt), warmup, steps)
+        r = kyro_amd.verify_drafts(**vt)
+        emitted = int((r.accepted.cpu() + 1).sum().item())
+        s_bytes = vcase.logit_bytes()
+        line["sampler"] = {"us": us, "algorithmic_bytes": s_bytes, "GB_s": s_bytes / us / 1e3,
+                           "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1}
+        total_us += us
+        line["verified_tok_s_at_measured_parts"] = emitted / (total_us * 1e-6)
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -115,7 +196,18 @@ def main():
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
+    ap.add_argument("--workload", default="llama3-8b",
+                    choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
+                             "mixed-llama3-70b", "others"],
+                    help="llama3-8b (default) prints the benchmark line; the others print one "
+                         "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
+    if args.workload != "llama3-8b":
+        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b"]
+                 if args.workload == "others" else [args.workload])
+        for n in names:
+            other_workload(n, args.warmup, args.steps)
+        return
     if args.calibrate_copy:
         import torch
 

@@ -78,7 +78,10 @@ struct SpecArgs {
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
 
-constexpr int kSpecChunk = 8192;
-constexpr int kMaxDraft = 63;  // one wave holds the acceptance decisions of a sequence  // vocabulary entries per workgroup in the streaming passes
+#ifndef KYRO_SPEC_CHUNK
+#define KYRO_SPEC_CHUNK 4096
+#endif
+constexpr int kSpecChunk = KYRO_SPEC_CHUNK;  // vocabulary entries per workgroup in the streaming passes
+constexpr int kMaxDraft = 63;                // one wave holds the acceptance decisions of a sequence
 
 }  // namespace kyro

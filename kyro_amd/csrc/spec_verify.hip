@@ -82,10 +82,22 @@ __device__ ArgMax block_argmax(ArgMax x, float* shv, int* shi) {
     return r;
 }
 
-// Loads this thread's share of chunk [v0, v1) of a row: strided (coalesced) layout.
-__device__ __forceinline__ void load_chunk_strided(const float* row, int v0, int v1, int vec4,
-                                                   float (&x)[kPer], int (&idx)[kPer]) {
-    if (vec4) {
+// A chunk [v0, v1) of a row is shared by the workgroup in one of two layouts. Strided (the
+// streaming passes): consecutive threads take consecutive 16-byte vectors (or floats), so every
+// load instruction is coalesced. Contiguous (the draw): thread t owns [v0 + t kPer, + kPer), so
+// index order within a thread is preserved. Positions past v1 load as -inf, which every consumer
+// maps to zero mass; element indices are recomputed from the position, not stored.
+template <bool VEC>
+__device__ __forceinline__ int strided_index(int v0, int i) {
+    if constexpr (VEC) return v0 + ((i >> 2) * kT + (int)threadIdx.x) * 4 + (i & 3);
+    else return v0 + i * kT + (int)threadIdx.x;
+}
+
+__device__ __forceinline__ int contig_index(int v0, int i) { return v0 + (int)threadIdx.x * kPer + i; }
+
+template <bool VEC>
+__device__ __forceinline__ void load_strided(const float* row, int v0, int v1, float (&x)[kPer]) {
+    if constexpr (VEC) {
 #pragma unroll
         for (int it = 0; it < kPer / 4; ++it) {
             const int v = v0 + (it * kT + (int)threadIdx.x) * 4;
@@ -95,42 +107,34 @@ __device__ __forceinline__ void load_chunk_strided(const float* row, int v0, int
             x[it * 4 + 1] = f.y;
             x[it * 4 + 2] = f.z;
             x[it * 4 + 3] = f.w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) idx[it * 4 + e] = (v < v1) ? v + e : -1;
         }
     } else {
 #pragma unroll
-        for (int it = 0; it < kPer; ++it) {
-            const int v = v0 + it * kT + (int)threadIdx.x;
-            x[it] = (v < v1) ? row[v] : kNegInf;
-            idx[it] = (v < v1) ? v : -1;
+        for (int i = 0; i < kPer; ++i) {
+            const int v = strided_index<false>(v0, i);
+            x[i] = v < v1 ? row[v] : kNegInf;
         }
     }
 }
 
-// Loads a contiguous run of kPer logits per thread (index order preserved within the thread).
-__device__ __forceinline__ void load_chunk_contig(const float* row, int v0, int v1, int vec4,
-                                                  float (&x)[kPer], int (&idx)[kPer]) {
-    const int t0 = v0 + (int)threadIdx.x * kPer;
-    if (vec4) {
+template <bool VEC>
+__device__ __forceinline__ void load_contig(const float* row, int v0, int v1, float (&x)[kPer]) {
+    if constexpr (VEC) {
 #pragma unroll
         for (int it = 0; it < kPer / 4; ++it) {
-            const int v = t0 + it * 4;
+            const int v = contig_index(v0, it * 4);
             float4 f = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
             if (v < v1) f = *reinterpret_cast<const float4*>(row + v);
             x[it * 4 + 0] = f.x;
             x[it * 4 + 1] = f.y;
             x[it * 4 + 2] = f.z;
             x[it * 4 + 3] = f.w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) idx[it * 4 + e] = (v < v1) ? v + e : -1;
         }
     } else {
 #pragma unroll
-        for (int it = 0; it < kPer; ++it) {
-            const int v = t0 + it;
-            x[it] = (v < v1) ? row[v] : kNegInf;
-            idx[it] = (v < v1) ? v : -1;
+        for (int i = 0; i < kPer; ++i) {
+            const int v = contig_index(v0, i);
+            x[i] = v < v1 ? row[v] : kNegInf;
         }
     }
 }
@@ -152,6 +156,7 @@ __device__ __forceinline__ float draw_mass(const SpecPlan& pl, float t, float d,
 
 // ------------------------------------------------------------------------- pass 1: statistics
 
+template <bool VEC>
 __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     __shared__ float shv[4];
     __shared__ int shi[4];
@@ -175,19 +180,20 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     const int pos = row <= a.kmax ? row : row - a.kmax - 1;
     const uint32_t tok = (!greedy && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
     float x[kPer];
-    int idx[kPer];
-    load_chunk_strided(base, v0, v1, a.vec4, x, idx);
+    load_strided<VEC>(base, v0, v1, x);
     if (tok >= (uint32_t)v0 && tok < (uint32_t)v1) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
-            if (idx[i] == (int)tok) a.gath[(size_t)b * (2 * a.kmax + 1) + row] = x[i];
+            if (strided_index<VEC>(v0, i) == (int)tok) a.gath[(size_t)b * (2 * a.kmax + 1) + row] = x[i];
     }
     float2* out = a.stats + ((size_t)b * (2 * a.kmax + 1) + row) * a.C + c;
     if (greedy) {
         ArgMax best = {kNegInf, 0x7fffffff};
 #pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (idx[i] >= 0) best = argmax_pick(best, ArgMax{x[i], idx[i]});
+        for (int i = 0; i < kPer; ++i) {
+            const int v = strided_index<VEC>(v0, i);
+            if (v < v1) best = argmax_pick(best, ArgMax{x[i], v});
+        }
         best = block_argmax(best, shv, shi);
         if (threadIdx.x == 0) *out = make_float2(best.v, __int_as_float(best.i));
         return;
@@ -219,7 +225,7 @@ struct AcceptShared {
     SpecPlan plan;
 };
 
-constexpr int kChunkGroup = 16;  // chunk statistics a lane folds per batch of loads
+constexpr int kChunkGroup = 32;  // chunk statistics a lane folds per batch of loads
 
 // Acceptance of sequence b, run by the first wave of a workgroup, in one round of loads (the
 // draft tokens' logits were captured by the statistics pass). Lane r owns statistics row r
@@ -245,12 +251,10 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
         tx = a.gath[(size_t)b * R + lane];               // target logit at x (sampled, lane < k)
         dx = a.gath[(size_t)b * R + a.kmax + 1 + lane];  // draft logit at x
     }
-    float2 y0[kChunkGroup], y1[kChunkGroup];
+    float2 y[kChunkGroup];  // first batch of this lane's row statistics
 #pragma unroll
-    for (int i = 0; i < kChunkGroup; ++i) {
-        y0[i] = (r0 < R && i < C) ? st[(size_t)r0 * C + i] : make_float2(kNegInf, 0.f);
-        y1[i] = (r1 < R && i < C) ? st[(size_t)r1 * C + i] : make_float2(kNegInf, 0.f);
-    }
+    for (int i = 0; i < kChunkGroup; ++i)
+        y[i] = (r0 < R && i < C) ? st[(size_t)r0 * C + i] : make_float2(kNegInf, 0.f);
 
     uint32_t* toks = a.out_tokens + (size_t)b * (a.kmax + 1);
     const bool greedy = !(T > 0.f);
@@ -276,45 +280,39 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
     }
     const float c2 = greedy ? 0.f : kLog2e / T;
     // Fold the owned rows. Rows that were not computed hold stale values and are never read.
+    // The first batch of row r0 is already in y; later batches (more than kChunkGroup chunks, or
+    // the second row of sequences with more than 64 statistics rows) are loaded here.
+    auto fold_row = [&](int r, bool preloaded, float& m, float& z, ArgMax& g) {
+        for (int cb = 0; cb < C; cb += kChunkGroup) {
+            if (cb > 0 || !preloaded) {
+#pragma unroll
+                for (int i = 0; i < kChunkGroup; ++i) {
+                    const int c = cb + i;
+                    y[i] = (r < R && c < C) ? st[(size_t)r * C + c] : make_float2(kNegInf, 0.f);
+                }
+            }
+            if (greedy) {
+#pragma unroll
+                for (int i = 0; i < kChunkGroup; ++i)
+                    if (cb + i < C) g = argmax_pick(g, ArgMax{y[i].x, __float_as_int(y[i].y)});
+            } else {
+                float bm = kNegInf;
+#pragma unroll
+                for (int i = 0; i < kChunkGroup; ++i) bm = fmaxf(bm, y[i].x);
+                float bs = 0.f;
+#pragma unroll
+                for (int i = 0; i < kChunkGroup; ++i)
+                    if (y[i].x != kNegInf) bs += y[i].y * fast_exp2((y[i].x - bm) * c2);
+                const float2 f = fold_stats(make_float2(m, z), make_float2(bm, bs), c2);
+                m = f.x;
+                z = f.y;
+            }
+        }
+    };
     float m0 = kNegInf, m1 = kNegInf, z0 = 0.f, z1 = 0.f;  // sampled: running max and sum
     ArgMax g0 = {kNegInf, 0x7fffffff}, g1 = g0;             // greedy: running first argmax
-    for (int cb = 0; cb < C; cb += kChunkGroup) {
-        if (cb > 0) {  // more than kChunkGroup chunks: next batch of loads
-#pragma unroll
-            for (int i = 0; i < kChunkGroup; ++i) {
-                const int c = cb + i;
-                y0[i] = (r0 < R && c < C) ? st[(size_t)r0 * C + c] : make_float2(kNegInf, 0.f);
-                y1[i] = (r1 < R && c < C) ? st[(size_t)r1 * C + c] : make_float2(kNegInf, 0.f);
-            }
-        }
-        if (greedy) {
-#pragma unroll
-            for (int i = 0; i < kChunkGroup; ++i) {
-                if (cb + i >= C) continue;
-                g0 = argmax_pick(g0, ArgMax{y0[i].x, __float_as_int(y0[i].y)});
-                g1 = argmax_pick(g1, ArgMax{y1[i].x, __float_as_int(y1[i].y)});
-            }
-        } else {
-            float b0 = kNegInf, b1 = kNegInf;
-#pragma unroll
-            for (int i = 0; i < kChunkGroup; ++i) {
-                b0 = fmaxf(b0, y0[i].x);
-                b1 = fmaxf(b1, y1[i].x);
-            }
-            float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-            for (int i = 0; i < kChunkGroup; ++i) {
-                if (y0[i].x != kNegInf) s0 += y0[i].y * fast_exp2((y0[i].x - b0) * c2);
-                if (y1[i].x != kNegInf) s1 += y1[i].y * fast_exp2((y1[i].x - b1) * c2);
-            }
-            const float2 f0 = fold_stats(make_float2(m0, z0), make_float2(b0, s0), c2);
-            const float2 f1 = fold_stats(make_float2(m1, z1), make_float2(b1, s1), c2);
-            m0 = f0.x;
-            z0 = f0.y;
-            m1 = f1.x;
-            z1 = f1.y;
-        }
-    }
+    fold_row(r0, true, m0, z0, g0);
+    if (R > 64) fold_row(r1, false, m1, z1, g1);
     const float iz0 = z0 > 0.f ? 1.f / z0 : 0.f;
     const float iz1 = z1 > 0.f ? 1.f / z1 : 0.f;
     // Value of statistics row rho from its owner lane (every lane takes part in both shuffles).
@@ -387,6 +385,7 @@ struct DrawShared {
 // Locates the chunk holding u * total with a block scan of the chunk masses (thread t owns the
 // contiguous run [t * per, t * per + per), so the scan keeps index order), then walks that
 // chunk in index order and stores the token at out_tokens[b][pl.row].
+template <bool VEC>
 __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawShared& ds,
                            float my_r, float my_p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -455,16 +454,15 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
     const int v0 = chunk * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
     float t[kPer], d[kPer], w[kPer];
-    int idx[kPer];
-    load_chunk_contig(target_row(a, b, pl.row), v0, v1, a.vec4, t, idx);
-    if (use_res) load_chunk_contig(draft_row(a, b, pl.row), v0, v1, a.vec4, d, idx);
+    load_contig<VEC>(target_row(a, b, pl.row), v0, v1, t);
+    if (use_res) load_contig<VEC>(draft_row(a, b, pl.row), v0, v1, d);
     float ts = 0.f;
     int my_last = -1;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-        w[i] = idx[i] >= 0 ? draw_mass(pl, t[i], use_res ? d[i] : 0.f, use_res) : 0.f;
+        w[i] = draw_mass(pl, t[i], use_res ? d[i] : kNegInf, use_res);  // -inf past v1 -> 0
         ts += w[i];
-        if (w[i] > 0.f) my_last = idx[i];
+        if (w[i] > 0.f) my_last = contig_index(v0, i);
     }
     // Exclusive scan of the per-thread sums in thread (= index) order.
     float inc2 = ts;
@@ -484,7 +482,7 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
             if (w[i] > 0.f) {
                 cum += w[i];
                 if (cum >= rem) {
-                    pick = idx[i];
+                    pick = contig_index(v0, i);
                     break;
                 }
             }
@@ -502,6 +500,7 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
 
 // Acceptance (wave 0, redundantly per chunk workgroup) fused with the residual mass of one chunk
 // of the resampled row.
+template <bool VEC>
 __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
     __shared__ AcceptShared acc;
     __shared__ float sh[4];
@@ -514,13 +513,11 @@ __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
     const int v0 = c * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
     float t[kPer], d[kPer];
-    int idx[kPer];
-    load_chunk_strided(target_row(a, b, pl.row), v0, v1, a.vec4, t, idx);
-    if (residual) load_chunk_strided(draft_row(a, b, pl.row), v0, v1, a.vec4, d, idx);
+    load_strided<VEC>(target_row(a, b, pl.row), v0, v1, t);
+    if (residual) load_strided<VEC>(draft_row(a, b, pl.row), v0, v1, d);
     float sr = 0.f, sp = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        if (idx[i] < 0) continue;
+    for (int i = 0; i < kPer; ++i) {  // positions past v1 hold -inf: zero mass
         const float p = fast_exp2((t[i] - pl.mt) * pl.c2) * pl.inv_zt;
         sp += p;
         if (residual) sr += fmaxf(p - fast_exp2((d[i] - pl.md) * pl.c2) * pl.inv_zd, 0.f);
@@ -532,6 +529,7 @@ __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
 
 // ------------------------------------------------------------------------------- pass 3: draw
 
+template <bool VEC>
 __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
     __shared__ DrawShared ds;
     const int b = blockIdx.x;
@@ -547,16 +545,22 @@ __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
     }
     const SpecPlan pl = a.plan[b];
     if (pl.mode == SPEC_DONE) return;
-    draw_token(a, b, pl, ds, my_r, my_p);
+    draw_token<VEC>(a, b, pl, ds, my_r, my_p);
 }
 
 }  // namespace
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
-    spec_stats_kernel<<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
-    spec_resample_kernel<<<dim3(a.C * a.B), kT, 0, stream>>>(a);
-    spec_pick_kernel<<<dim3(a.B), kT, 0, stream>>>(a);
+    if (a.vec4) {
+        spec_stats_kernel<true><<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
+        spec_resample_kernel<true><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
+        spec_pick_kernel<true><<<dim3(a.B), kT, 0, stream>>>(a);
+    } else {
+        spec_stats_kernel<false><<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
+        spec_resample_kernel<false><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
+        spec_pick_kernel<false><<<dim3(a.B), kT, 0, stream>>>(a);
+    }
     return hipGetLastError();
 }
 
