@@ -40,7 +40,12 @@ struct AttnArgs {
     int causal, out_bf16, dtype_bf16;
     float scale_log2;  // softmax scale * log2(e)
     int splits, chunk_blocks, units, units_padded;
+    int row_groups;  // workgroups per (unit, split), each covering rows_per_group rows
 };
+
+// Query rows one attention workgroup covers.
+constexpr int kVectorRowsPerGroup = 8;
+inline int mfma_rows_per_group(int rows) { return rows <= 16 ? 16 : 32; }
 
 hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
 

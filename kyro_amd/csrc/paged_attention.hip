@@ -41,14 +41,18 @@ struct SeqInfo {
     bool ok;
 };
 
-// Workgroup -> (unit = sequence * Hkv + kv head, split). Consecutive workgroups go to different
-// XCDs; the splits of one unit share (blockIdx % 8) and therefore one XCD.
-__device__ __forceinline__ bool map_workgroup(const AttnArgs& a, int& unit, int& split) {
+// Workgroup -> (unit = sequence * Hkv + kv head, split, row group). Consecutive workgroups go to
+// different XCDs; the splits and row groups of one unit share (blockIdx % 8) and therefore one
+// XCD, and a unit's row groups are dispatched back to back, so the K/V they all read is fetched
+// from HBM once and served to the others from that XCD's L2.
+__device__ __forceinline__ bool map_workgroup(const AttnArgs& a, int& unit, int& split, int& rg) {
     const int wg = blockIdx.x;
     const int xcd = wg & 7;
     const int local = wg >> 3;
-    unit = (local / a.splits) * 8 + xcd;
-    split = local % a.splits;
+    rg = local % a.row_groups;
+    const int rest = local / a.row_groups;
+    split = rest % a.splits;
+    unit = (rest / a.splits) * 8 + xcd;
     return unit < a.units;
 }
 
@@ -129,14 +133,13 @@ struct Frame {
 // (single split) or park the split's partial state in the workspace.
 template <int R, int D>
 __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int split, int nsplit,
-                            int row0, int nrows, Frame<R, D>& f) {
+                            int row0, int nrows, Frame<R, D>& f, int nslots = kWaves) {
     constexpr int Q = D / 4;
     if (nsplit == 1) {
         for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
             const int n = idx / Q, d = (idx - n * Q) * 4;
             float L = 0.f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) L += f.l[w][n];
+            for (int w = 0; w < nslots; ++w) L += f.l[w][n];
             const float inv = L > 0.f ? 1.f / L : 0.f;
             const float* src = &f.acc[n * Frame<R, D>::kStride + d];
             store_row4<D>(a, out_row(a, si, row0 + n), d, src[0] * inv, src[1] * inv, src[2] * inv,
@@ -147,8 +150,7 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int 
     const size_t base = ((size_t)unit * a.splits + split) * a.rows_cap;
     for (int n = threadIdx.x; n < nrows; n += kThreads) {
         float L = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) L += f.l[w][n];
+        for (int w = 0; w < nslots; ++w) L += f.l[w][n];
         a.ws_m[base + row0 + n] = f.mx[n];
         a.ws_l[base + row0 + n] = L;
     }
@@ -201,25 +203,6 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
 constexpr int kMfmaD = 128;
 constexpr int kMfmaBS = 16;
 
-#ifndef KYRO_KV_NONTEMPORAL
-#define KYRO_KV_NONTEMPORAL 0
-#endif
-#ifndef KYRO_PREFETCH_DEPTH
-#define KYRO_PREFETCH_DEPTH 1
-#endif
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// K/V bytes are read exactly once: optionally stream them past the caches.
-__device__ __forceinline__ uint4 load16_kv(const uint16_t* p) {
-#if KYRO_KV_NONTEMPORAL
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v[0], v[1], v[2], v[3]);
-#else
-    return load16(p);
-#endif
-}
-
 // K and V of one pair of 16-token blocks, already in MFMA operand layout (K) or ready for the
 // in-register transpose (V). 64 VGPRs.
 struct KVPair {
@@ -239,9 +222,9 @@ __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict_
             const uint16_t* kb = kp + base + (size_t)r * kMfmaD + 8 * g;
             const uint16_t* vb = vp + base + (size_t)(4 * g) * kMfmaD + 8 * r;
 #pragma unroll
-            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, load16_kv(kb + 32 * s));
+            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, load16(kb + 32 * s));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p.v[bi][e] = load16_kv(vb + (size_t)e * kMfmaD);
+            for (int e = 0; e < 4; ++e) p.v[bi][e] = load16(vb + (size_t)e * kMfmaD);
         } else {
 #pragma unroll
             for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
@@ -262,19 +245,24 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
     __syncthreads();
 }
 
-template <int NT>
+// A workgroup covers NTW 16-row tiles of its unit's rows (NTW 1 or 2: the accumulators of two
+// tiles plus two K/V pair buffers fill the register file without spills); units with more rows
+// (a large GQA group times many draft positions) get one workgroup per 32-row group.
+template <int NTW>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     constexpr int D = kMfmaD;
-    constexpr int R = NT * 16;
-    __shared__ Frame<R, D> frame;
+    constexpr int RW = NTW * 16;  // rows of one wave (one tile group)
+    __shared__ Frame<RW, D> frame;
     __shared__ int s_blk[kMaxChunkBlocks];
 
-    int unit, split;
-    if (!map_workgroup(a, unit, split)) return;
+    int unit, split, rg;
+    if (!map_workgroup(a, unit, split, rg)) return;
     const SeqInfo si = seq_info(a, unit);
     if (!si.ok) return;
     const int nsplit = num_splits_for(a, si.nblk);
     if (split >= nsplit) return;
+    const int row0 = rg * RW;
+    if (row0 > 0 && row0 >= si.rows) return;  // this row group is past the sequence's rows
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -297,16 +285,13 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         return i < blk_end ? __builtin_amdgcn_readfirstlane(s_blk[i - blk_begin]) : -1;
     };
 
-    const int nrows_total = si.rows > 0 ? si.rows : 1;
-    for (int row0 = 0; row0 < nrows_total; row0 += R) {
-        const int nrows = min(R, si.rows - row0);
-
+    {
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
         // Padding rows (n >= rows) get Q = 0 and full visibility; they are never stored.
-        bf16x8 qB[NT][4];
-        int vis[NT];
+        bf16x8 qB[NTW][4];
+        int vis[NTW];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
             const int n = row0 + nt * 16 + r;
             if (n < si.rows) {
                 const int j = n / a.group;
@@ -322,10 +307,10 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             }
         }
 
-        float m[NT], lsum[NT];  // running max (log2 units, scaled) and this lane's partial sum
-        f32x4 O[8][NT];
+        float m[NTW], lsum[NTW];  // running max (log2 units, scaled) and this lane's partial sum
+        f32x4 O[8][NTW];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
             m[nt] = kNegInf;
             lsum[nt] = 0.f;
 #pragma unroll
@@ -335,11 +320,11 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
         auto compute = [&](const KVPair& kv, int pb, int blk0, int blk1) {
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
-            f32x4 S[2][NT];
+            f32x4 S[2][NTW];
 #pragma unroll
             for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
+                for (int nt = 0; nt < NTW; ++nt) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
@@ -347,9 +332,9 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                     S[bi][nt] = acc;
                 }
             const bool full = blk0 >= 0 && blk1 >= 0 && (pb + 2) * kMfmaBS <= full_vis;
-            bf16x8 pB[NT];
+            bf16x8 pB[NTW];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
+            for (int nt = 0; nt < NTW; ++nt) {
                 float sv[8];
 #pragma unroll
                 for (int bi = 0; bi < 2; ++bi)
@@ -406,110 +391,62 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                 av.w = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][3])[w], ((const uint32_t*)&kv.v[1][2])[w], sel);
                 const bf16x8 A = __builtin_bit_cast(bf16x8, av);
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
+                for (int nt = 0; nt < NTW; ++nt)
                     O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, pB[nt], O[dt][nt], 0, 0, 0);
             }
         };
 
         // Each wave streams the pairs w, w + 4, w + 8, ... of the split. The loads of the next
         // pair are issued before the current pair is computed (two register buffers, unrolled).
-        // With four or more row tiles the accumulators leave no room for a second buffer.
-        KVPair bufA, bufB;
-        int pb = blk_begin + 2 * wave;
-        int a0 = -1, a1 = -1, b0 = -1, b1 = -1;
-        constexpr bool kDepth2 = KYRO_PREFETCH_DEPTH >= 2 && NT <= 2;
-        constexpr int kStep = 2 * kWaves;
-        if constexpr (kDepth2) {  // two pairs in flight while one is computed
-            KVPair bufC;
-            int c0 = -1, c1 = -1;
+        constexpr int step = 2 * kWaves;
+        {
+            KVPair bufA, bufB;
+            int pb = blk_begin + 2 * wave;
+            int a0 = -1, a1 = -1, b0 = -1, b1 = -1;
             if (pb < blk_end) {
                 a0 = blk_at(pb);
                 a1 = blk_at(pb + 1);
                 load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
             }
-            if (pb + kStep < blk_end) {
-                b0 = blk_at(pb + kStep);
-                b1 = blk_at(pb + kStep + 1);
-                load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
-            }
             while (pb < blk_end) {
-                int pf = pb + 2 * kStep;
-                if (pf < blk_end) {
-                    c0 = blk_at(pf);
-                    c1 = blk_at(pf + 1);
-                    load_pair(bufC, kp, vp, c0, c1, block_stride, kv_off, r, g);
+                int pn = pb + step;
+                if (pn < blk_end) {
+                    b0 = blk_at(pn);
+                    b1 = blk_at(pn + 1);
+                    load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
                 }
                 compute(bufA, pb, a0, a1);
-                pb += kStep;
+                pb = pn;
                 if (pb >= blk_end) break;
-                pf = pb + 2 * kStep;
-                if (pf < blk_end) {
-                    a0 = blk_at(pf);
-                    a1 = blk_at(pf + 1);
+                pn = pb + step;
+                if (pn < blk_end) {
+                    a0 = blk_at(pn);
+                    a1 = blk_at(pn + 1);
                     load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 }
                 compute(bufB, pb, b0, b1);
-                pb += kStep;
-                if (pb >= blk_end) break;
-                pf = pb + 2 * kStep;
-                if (pf < blk_end) {
-                    b0 = blk_at(pf);
-                    b1 = blk_at(pf + 1);
-                    load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
-                }
-                compute(bufC, pb, c0, c1);
-                pb += kStep;
+                pb = pn;
             }
-        }
-        if constexpr (NT >= 4) {
-            for (; pb < blk_end; pb += 2 * kWaves) {
-                a0 = blk_at(pb);
-                a1 = blk_at(pb + 1);
-                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
-                compute(bufA, pb, a0, a1);
-            }
-        }
-        if (!kDepth2 && NT < 4 && pb < blk_end) {
-            a0 = blk_at(pb);
-            a1 = blk_at(pb + 1);
-            load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
-        }
-        while (!kDepth2 && NT < 4 && pb < blk_end) {
-            int pn = pb + 2 * kWaves;
-            if (pn < blk_end) {
-                b0 = blk_at(pn);
-                b1 = blk_at(pn + 1);
-                load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
-            }
-            compute(bufA, pb, a0, a1);
-            pb = pn;
-            if (pb >= blk_end) break;
-            pn = pb + 2 * kWaves;
-            if (pn < blk_end) {
-                a0 = blk_at(pn);
-                a1 = blk_at(pn + 1);
-                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
-            }
-            compute(bufB, pb, b0, b1);
-            pb = pn;
         }
 
         // Row sums: each lane summed its own 8 tokens per pair; fold the four 16-lane groups.
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
             lsum[nt] += shfl_xor_f(lsum[nt], 16);
             lsum[nt] += shfl_xor_f(lsum[nt], 32);
         }
 
-        // Merge the four waves: common max, rescale, add into LDS.
+        // Merge the four waves: common max, then the rescaled accumulators are added into LDS in
+        // a fixed order (wave 0 stores), so the result is bitwise reproducible. Lane (r, g) owns
+        // head dims 32 g + 8 e + dt of row 16 nt + r.
         if (g == 0) {
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) frame.m[wave][nt * 16 + r] = m[nt];
+            for (int nt = 0; nt < NTW; ++nt) frame.m[wave][nt * 16 + r] = m[nt];
         }
         __syncthreads();
-        float f[NT];
+        float f[NTW];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int nt = 0; nt < NTW; ++nt) {
             const int n = nt * 16 + r;
             float M = frame.m[0][n];
 #pragma unroll
@@ -520,13 +457,11 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                 if (wave == 0) frame.mx[n] = M;
             }
         }
-        // Waves add their rescaled accumulators in a fixed order (wave 0 stores), so the result
-        // is bitwise reproducible. Lane (r, g) owns head dims 32 g + 8 e + dt of row 16 nt + r.
         for (int w = 0; w < kWaves; ++w) {
             if (wave == w) {
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    float* dst = &frame.acc[(nt * 16 + r) * Frame<R, D>::kStride + 32 * g];
+                for (int nt = 0; nt < NTW; ++nt) {
+                    float* dst = &frame.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 32 * g];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -538,8 +473,8 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             }
             __syncthreads();
         }
-        frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
-        __syncthreads();
+        const int nrows = min(RW, si.rows - row0);
+        frame_flush<RW, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
     }
 }
 
@@ -587,7 +522,7 @@ __device__ __forceinline__ void Elem<uint16_t>::load<4>(const uint16_t* p, float
     x[3] = bf16_hi(v.y);
 }
 
-constexpr int kVecRows = 8;
+constexpr int kVecRows = kVectorRowsPerGroup;
 
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
@@ -595,12 +530,14 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
     constexpr int DPL = D / 16;  // head-dim elements per lane
     __shared__ Frame<R, D> frame;
 
-    int unit, split;
-    if (!map_workgroup(a, unit, split)) return;
+    int unit, split, rg;
+    if (!map_workgroup(a, unit, split, rg)) return;
     const SeqInfo si = seq_info(a, unit);
     if (!si.ok) return;
     const int nsplit = num_splits_for(a, si.nblk);
     if (split >= nsplit) return;
+    const int row0 = rg * R;
+    if (row0 > 0 && row0 >= si.rows) return;  // this row group is past the sequence's rows
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -612,8 +549,7 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
     const int t_begin = split * a.chunk_blocks * a.bs;
     const int t_end = min(si.ctx, (split + 1) * a.chunk_blocks * a.bs);
 
-    const int nrows_total = si.rows > 0 ? si.rows : 1;
-    for (int row0 = 0; row0 < nrows_total; row0 += R) {
+    {
         const int nrows = min(R, si.rows - row0);
         float q[R][DPL];
         int vis[R];
@@ -720,7 +656,6 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
             __syncthreads();
         }
         frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
-        __syncthreads();
     }
 }
 
@@ -728,21 +663,13 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------------------------ launcher
 
-int attention_rows_per_mfma_tile() { return 16; }
-
 hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t stream) {
     const dim3 block(kThreads);
-    const dim3 grid((unsigned)(a.units_padded * a.splits));
+    const dim3 grid((unsigned)(a.units_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
-        const int nt = (a.group * a.max_q_len + 15) / 16;
-        switch (nt <= 1 ? 1 : nt >= 5 ? 5 : nt) {
-            case 1: attn_mfma_kernel<1><<<grid, block, 0, stream>>>(a); break;
-            case 2: attn_mfma_kernel<2><<<grid, block, 0, stream>>>(a); break;
-            case 3: attn_mfma_kernel<3><<<grid, block, 0, stream>>>(a); break;
-            case 4: attn_mfma_kernel<4><<<grid, block, 0, stream>>>(a); break;
-            default: attn_mfma_kernel<5><<<grid, block, 0, stream>>>(a); break;
-        }
+        if (mfma_rows_per_group(a.rows_cap) == 16) attn_mfma_kernel<1><<<grid, block, 0, stream>>>(a);
+        else attn_mfma_kernel<2><<<grid, block, 0, stream>>>(a);
     } else {
         const bool bf16 = a.dtype_bf16;
         if (a.D == 128) {

@@ -340,18 +340,24 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         a.scale_log2 = (float)(scale * 1.4426950408889634);
         a.units = p->batch_size * p->num_kv_heads;
         a.units_padded = (a.units + 7) / 8 * 8;
+        // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
+        // (vector) or 16 / 32 (MFMA) rows that stream the same K/V.
+        const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
+                                                                    : kyro::kVectorRowsPerGroup;
+        a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
 
         // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
         const int mb = std::max(1, p->max_blocks_per_seq);
         int splits = p->num_splits;
         if (splits <= 0) {
             // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
-            // one CU streaming it alone; more splits only when the units cannot cover the chip's
-            // 256 CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
+            // one CU streaming it alone; more splits only when the workgroups cannot cover the
+            // chip's 256 CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
             constexpr int kTargetChunk = 256, kCUs = 256, kMinChunk = 16;
+            const int per_split = a.units * a.row_groups;
             splits = (mb + kTargetChunk - 1) / kTargetChunk;
-            if (a.units * splits < kCUs)
-                splits = std::min((kCUs + a.units - 1) / a.units, std::max(1, mb / kMinChunk));
+            if (per_split * splits < kCUs)
+                splits = std::min((kCUs + per_split - 1) / per_split, std::max(1, mb / kMinChunk));
         }
         splits = std::min(splits, mb);
         splits = std::max(splits, (mb + kyro::kMaxChunkBlocks - 1) / kyro::kMaxChunkBlocks);
@@ -360,6 +366,10 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         splits = (mb + chunk - 1) / chunk;
         a.splits = splits;
         a.chunk_blocks = chunk;
+        // One launch carries at most 2^32 - 1 work items along x.
+        if ((uint64_t)a.units_padded * splits * a.row_groups * 256 > 0xffffffffull)
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: %d units x %d splits x %d row groups is too large for one launch",
+                        a.units, splits, a.row_groups);
 
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
