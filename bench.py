@@ -69,8 +69,15 @@ def attention_bytes():
     return kv + q + q  # bf16 out has the query's size
 
 
-def sampler_bytes():
-    return B * (2 * K_DRAFT + 1) * VOCAB * 4
+def sampler_bytes(accepted=None):
+    """Logit bytes of every row (accepted None), or of the rows the acceptance scan evaluates:
+    target and draft rows 0 .. j of a sequence rejected at j, and every row (target 0 .. k,
+    draft 0 .. k - 1) of a fully accepted one. Each row counted once."""
+    if accepted is None:
+        return B * (2 * K_DRAFT + 1) * VOCAB * 4
+    j = accepted.cpu().long()
+    rows = (j + 1) + j.clamp(max=K_DRAFT - 1) + 1
+    return int(rows.sum().item()) * VOCAB * 4
 
 
 def cpu_baseline(sample: int, threads: int):
@@ -176,7 +183,7 @@ def other_workload(name, warmup, steps):
         us = _median_us(lambda: kyro_amd.verify_drafts_async(**vt), warmup, steps)
         r = kyro_amd.verify_drafts(**vt)
         emitted = int((r.accepted.cpu() + 1).sum().item())
-        s_bytes = vcase.logit_bytes()
+        s_bytes = vcase.logit_bytes(r.accepted.cpu().numpy())
         line["sampler"] = {"us": us, "algorithmic_bytes": s_bytes, "GB_s": s_bytes / us / 1e3,
                            "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1}
         total_us += us
@@ -191,6 +198,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--path", default="auto", choices=["auto", "vector", "mfma"])
     ap.add_argument("--splits", type=int, default=0, help="context splits (0 = automatic)")
+    ap.add_argument("--window", type=int, default=0,
+                    help="draft positions read before the first acceptance scan (0 = library default)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -248,7 +257,7 @@ def main():
         if ev is not None:
             ev[1].record()
         kyro_amd.verify_drafts_async(x["target"], x["draft"], x["tokens"], x["nd"], x["temp"],
-                                     x["u_acc"], x["u_res"], out=(acc, toks))
+                                     x["u_acc"], x["u_res"], out=(acc, toks), window=args.window)
         if ev is not None:
             ev[2].record()
 
@@ -270,7 +279,7 @@ def main():
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     samp_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
     emitted = int((acc.cpu() + 1).sum().item())
-    a_bytes, s_bytes = attention_bytes(), sampler_bytes()
+    a_bytes, s_bytes = attention_bytes(), sampler_bytes(acc)
     achieved = a_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = (a_bytes + s_bytes) / sec_per_step / 1e9
 
@@ -307,7 +316,7 @@ def main():
             "batch": B, "draft_k": K_DRAFT, "context": CTX, "q_heads": HQ, "kv_heads": HKV,
             "head_dim": D, "block_size": BS, "kv_dtype": "bf16", "vocab": VOCAB,
             "temperature": TEMP, "logits_dtype": "f32", "attention_path": args.path,
-            "splits": args.splits,
+            "splits": args.splits, "window": args.window,
         },
         "roofline": {
             "bound": "hbm",
@@ -328,8 +337,11 @@ def main():
             "attention_us": attn_ms * 1e3,
             "sampler_us": samp_ms * 1e3,
             "sampler_GB_s": s_bytes / (samp_ms * 1e-3) / 1e9,
+            "sampler_bytes_evaluated_rows": s_bytes,
+            "sampler_bytes_all_rows": sampler_bytes(),
             "tokens_per_step": emitted,
             "mean_accepted": emitted / B - 1,
+            "accepted_histogram": torch.bincount(acc.cpu().long(), minlength=K_DRAFT + 1).tolist(),
         },
     }
     print(json.dumps(line), flush=True)

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 1
+#define KYRO_ABI_VERSION 2
 
 typedef enum kyro_status {
     KYRO_OK = 0,
@@ -151,6 +151,10 @@ typedef struct kyro_spec_verify_params {
     int32_t max_draft;    /* kmax: target_logits has kmax+1 rows per sequence, draft kmax */
     int32_t vocab_size;   /* V */
     int32_t logits_dtype; /* kyro_dtype of both logits tensors (KYRO_F32) */
+    int32_t window;       /* draft positions whose logit rows are read before the first
+                             acceptance scan; rows after it are read only for sequences that
+                             accept all of them. 0 = default (2); >= max_draft reads every row
+                             in one pass. Outputs do not depend on it. */
 } kyro_spec_verify_params;
 
 /*
@@ -169,7 +173,9 @@ typedef struct kyro_spec_verify_params {
  * Outputs: out_accepted[b] = accepted drafts in [0, k]; out_tokens[b, 0..out_accepted[b]] = the
  * accepted drafts, out_tokens[b, out_accepted[b]] = the correction or bonus token, the rest
  * 0xFFFFFFFF. Optional (NULL to skip): out_p_draft[b,i] = p_i(x_i), out_q_draft[b,i] = q_i(x_i)
- * for i < k of sampled sequences (NaN elsewhere and for greedy sequences).
+ * for the drafts the scan evaluates, i <= out_accepted[b] and i < k, of sampled sequences; NaN
+ * elsewhere (the scan stops at the first rejection, as the loop of speculative.rs:315-323) and
+ * for greedy sequences.
  * Shapes: target_logits [B, kmax+1, V], draft_logits [B, kmax, V] (may be NULL when every
  * sequence is greedy or kmax == 0), draft_tokens [B, kmax] uint32, num_draft [B] int32,
  * temperature [B] f32, u_accept [B, kmax] f32, u_resample [B] f32; uniforms in (0, 1).

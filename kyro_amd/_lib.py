@@ -44,8 +44,11 @@ class SpecVerifyParams(ctypes.Structure):
     _fields_ = [
         ("batch_size", ctypes.c_int32), ("max_draft", ctypes.c_int32),
         ("vocab_size", ctypes.c_int32), ("logits_dtype", ctypes.c_int32),
+        ("window", ctypes.c_int32),
     ]
 
+
+ABI_VERSION = 2  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -87,6 +90,9 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.argtypes = argtypes
                 fn.restype = restype
+            if handle.kyro_abi_version() != ABI_VERSION:
+                raise ImportError(f"{LIB_PATH} has ABI version {handle.kyro_abi_version()}, this "
+                                  f"binding needs {ABI_VERSION}: rebuild with `python -m kyro_amd.build`")
             _lib = handle
     return _lib
 

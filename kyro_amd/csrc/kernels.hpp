@@ -59,7 +59,9 @@ struct SpecPlan {
     float u;           // u_resample
 };
 
-enum SpecMode : int { SPEC_DONE = 0, SPEC_RESIDUAL = 1, SPEC_PLAIN = 2 };
+// SPEC_PENDING: no decision within the statistics computed so far (the rows of the first draft
+// positions only); the remaining rows are needed.
+enum SpecMode : int { SPEC_DONE = 0, SPEC_RESIDUAL = 1, SPEC_PLAIN = 2, SPEC_PENDING = 3 };
 
 struct SpecArgs {
     const float* target;  // [B, kmax+1, V]
@@ -74,11 +76,15 @@ struct SpecArgs {
     float* out_p;
     float* out_q;
     float2* stats;   // [B, 2 kmax + 1, C]: {max, sum exp} (sampled) or {max, index bits} (greedy)
-    SpecPlan* plan;  // [B]
+    SpecPlan* plan;       // [B]: from the window's scan (SPEC_PENDING: see plan_tail)
+    SpecPlan* plan_tail;  // [B]: plan of a sequence that was pending, from the full scan
     float2* csum;    // [B, C]: {residual mass, p mass} of the resampled row, per chunk
     float* gath;     // [B, 2 kmax + 1]: logit of the row's draft token (sampled rows < k)
+    int2* tail;      // [B]: {items (row x chunk) left after the window, target rows left | greedy << 16}
     int* err;
     int B, kmax, V, C, chunk, vec4;
+    int win;          // draft positions whose rows the first statistics pass reads
+    int tail_wgs;     // workgroups of the pass over the remaining rows
 };
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
@@ -88,5 +94,14 @@ hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
 #endif
 constexpr int kSpecChunk = KYRO_SPEC_CHUNK;  // vocabulary entries per workgroup in the streaming passes
 constexpr int kMaxDraft = 63;                // one wave holds the acceptance decisions of a sequence
+#ifndef KYRO_SPEC_WINDOW
+#define KYRO_SPEC_WINDOW 2
+#endif
+constexpr int kSpecWindow = KYRO_SPEC_WINDOW;  // draft positions read before the first acceptance scan
+constexpr int kMaxLazyBatch = 2048;  // larger batches read every row in the first pass
+#ifndef KYRO_SPEC_TAIL_WGS
+#define KYRO_SPEC_TAIL_WGS 2048
+#endif
+constexpr int kSpecTailWgs = KYRO_SPEC_TAIL_WGS;  // workgroups of the pass over the remaining rows
 
 }  // namespace kyro

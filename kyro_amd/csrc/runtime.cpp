@@ -428,18 +428,29 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         const bool aligned = (reinterpret_cast<uintptr_t>(target_logits) % 16 == 0) &&
                              (reinterpret_cast<uintptr_t>(draft_logits) % 16 == 0);
         a.vec4 = (a.V % 4 == 0) && aligned;
+        // Rows of the first win draft positions are read for every sequence; the rest only for
+        // sequences still undecided after them, spread over up to kSpecTailWgs workgroups. Batches
+        // beyond kMaxLazyBatch read every row in the first pass.
+        if (p->window < 0) return fail(KYRO_EINVAL, "spec_verify: window must be >= 0");
+        a.win = p->window > 0 ? std::min(p->window, a.kmax + 1) : std::max(1, kyro::kSpecWindow);
+        if (a.B > kyro::kMaxLazyBatch) a.win = a.kmax + 1;
+        const long long tail_items = a.kmax >= a.win ? (long long)a.B * (2 * (a.kmax - a.win) + 1) * a.C : 1;
+        a.tail_wgs = (int)std::max(1LL, std::min((long long)kyro::kSpecTailWgs, tail_items));
         const size_t stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
-        const size_t plan_b = align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
+        const size_t plan_b = 2 * align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
         const size_t csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
         const size_t gath_b = align_up((size_t)a.B * (2 * a.kmax + 1) * sizeof(float), 256);
+        const size_t tail_b = align_up((size_t)a.B * sizeof(int2), 256);
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b + gath_b)) return rc;
+        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b + gath_b + tail_b)) return rc;
         char* base = static_cast<char*>(ctx->arena);
         a.stats = reinterpret_cast<float2*>(base);
         a.plan = reinterpret_cast<kyro::SpecPlan*>(base + stats_b);
+        a.plan_tail = reinterpret_cast<kyro::SpecPlan*>(base + stats_b + plan_b / 2);
         a.csum = reinterpret_cast<float2*>(base + stats_b + plan_b);
         a.gath = reinterpret_cast<float*>(base + stats_b + plan_b + csum_b);
+        a.tail = reinterpret_cast<int2*>(base + stats_b + plan_b + csum_b + gath_b);
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_spec_verify(a, ctx->stream));
         return KYRO_OK;

@@ -156,31 +156,22 @@ __device__ __forceinline__ float draw_mass(const SpecPlan& pl, float t, float d,
 
 // ------------------------------------------------------------------------- pass 1: statistics
 
+// Statistics row `row` of sequence b (target row i is row i, draft row i is row kmax + 1 + i).
+__device__ __forceinline__ const float* stats_row_base(const SpecArgs& a, int b, int row) {
+    return row <= a.kmax ? target_row(a, b, row) : draft_row(a, b, row - a.kmax - 1);
+}
+
+// Reduces chunk c of statistics row `row` (already loaded into x in the strided layout) to
+// {max, sum exp2((x - max) log2e / T)}, or {max, first argmax} for a greedy sequence, and keeps
+// the logit at the row's draft token (sampled rows below k) for the acceptance scan.
 template <bool VEC>
-__global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
-    __shared__ float shv[4];
-    __shared__ int shi[4];
-    const int c = blockIdx.x % a.C, b = blockIdx.x / a.C, row = blockIdx.y;
-    const int k = a.num_draft[b];
-    if (k < 0 || k > a.kmax) return;  // reported by the acceptance pass
-    const float T = a.temperature[b];
+__device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, int c, int k, float T,
+                                            const float (&x)[kPer], float* shv, int* shi) {
     const bool greedy = !(T > 0.f);
-    const float* base;
-    if (row <= a.kmax) {
-        if (row > k) return;
-        base = target_row(a, b, row);
-    } else {
-        const int i = row - a.kmax - 1;
-        if (greedy || i >= k || a.draft == nullptr) return;
-        base = draft_row(a, b, i);
-    }
     const int v0 = c * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
-    // Sampled rows below k also hand their draft token's logit to the acceptance pass.
     const int pos = row <= a.kmax ? row : row - a.kmax - 1;
     const uint32_t tok = (!greedy && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
-    float x[kPer];
-    load_strided<VEC>(base, v0, v1, x);
     if (tok >= (uint32_t)v0 && tok < (uint32_t)v1) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
@@ -212,6 +203,33 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     if (threadIdx.x == 0) *out = make_float2(m, s);
 }
 
+// Pass 1a: the rows of the first `win` draft positions (target rows 0 .. win - 1, draft rows
+// 0 .. win - 1), grid (sequence x vocab chunk, row). Rows past a sequence's k, and draft rows
+// of greedy sequences, are never read.
+template <bool VEC>
+__global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
+    __shared__ float shv[4];
+    __shared__ int shi[4];
+    const int c = blockIdx.x % a.C, b = blockIdx.x / a.C;
+    const int wt = min(a.win, a.kmax + 1);  // target rows in the window
+    const int y = blockIdx.y;
+    const int k = a.num_draft[b];
+    if (k < 0 || k > a.kmax) return;  // reported by the acceptance pass
+    const float T = a.temperature[b];
+    int row;
+    if (y < wt) {
+        if (y > k) return;
+        row = y;
+    } else {
+        const int i = y - wt;
+        if (!(T > 0.f) || i >= k || a.draft == nullptr) return;
+        row = a.kmax + 1 + i;
+    }
+    float x[kPer];
+    load_strided<VEC>(stats_row_base(a, b, row), c * a.chunk, min(a.V, c * a.chunk + a.chunk), x);
+    chunk_stats<VEC>(a, b, row, c, k, T, x, shv, shi);
+}
+
 // ------------------------------------------------------------------------- pass 2: acceptance
 
 // Folds chunk statistic y into the running (max, sum) x of one lane.
@@ -231,14 +249,19 @@ constexpr int kChunkGroup = 32;  // chunk statistics a lane folds per batch of l
 // draft tokens' logits were captured by the statistics pass). Lane r owns statistics row r
 // (and row r + 64 when there are more than 64) and folds that row's chunk statistics itself;
 // lane i then decides draft i, reading the rows it needs from their owners with shuffles, and a
-// ballot finds the first rejection. When `writer` is set the sequence's outputs are stored.
-// The plan for the draw lands in sh.plan.
-__device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptShared& sh) {
+// ballot finds the first rejection. Only the statistics of the first `avail` draft positions
+// (target and draft rows 0 .. avail - 1) are read: when neither a rejection nor the end of the
+// drafts falls inside them the plan is SPEC_PENDING. When `writer` is set (which needs a
+// decision) the sequence's outputs are stored, and the plan in plan_out[b]. The plan for the
+// draw also lands in sh.plan.
+__device__ void accept_sequence(const SpecArgs& a, int b, int avail, bool writer, SpecPlan* plan_out,
+                                AcceptShared& sh) {
     const int lane = threadIdx.x;
     const int R = 2 * a.kmax + 1;
     const int C = a.C;
     const float2* st = a.stats + (size_t)b * R * C;
     const int r0 = lane, r1 = lane + 64;
+    auto row_ok = [&](int r) { return r < R && (r <= a.kmax ? r < avail : r - a.kmax - 1 < avail); };
     // Round 1: every load that does not depend on another load.
     const int k = a.num_draft[b];
     const float T = a.temperature[b];
@@ -254,7 +277,7 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
     float2 y[kChunkGroup];  // first batch of this lane's row statistics
 #pragma unroll
     for (int i = 0; i < kChunkGroup; ++i)
-        y[i] = (r0 < R && i < C) ? st[(size_t)r0 * C + i] : make_float2(kNegInf, 0.f);
+        y[i] = (row_ok(r0) && i < C) ? st[(size_t)r0 * C + i] : make_float2(kNegInf, 0.f);
 
     uint32_t* toks = a.out_tokens + (size_t)b * (a.kmax + 1);
     const bool greedy = !(T > 0.f);
@@ -262,16 +285,16 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
     if (k < 0 || k > a.kmax) err = ERR_NUM_DRAFT;
     else if (!greedy && k > 0 && a.draft == nullptr) err = ERR_NO_DRAFT;
     else if (__any(lane < k && x >= (uint32_t)a.V)) err = ERR_TOKEN;
-    if (writer && lane < a.kmax) {
-        if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = __builtin_nanf("");
-        if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = __builtin_nanf("");
-    }
     if (err) {
         if (writer) {
+            if (lane < a.kmax) {
+                if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = __builtin_nanf("");
+                if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = __builtin_nanf("");
+            }
             if (lane == 0) {
                 latch_error(a.err, err);
                 a.out_accepted[b] = 0;
-                a.plan[b].mode = SPEC_DONE;
+                plan_out[b].mode = SPEC_DONE;
             }
             if (lane <= a.kmax) toks[lane] = 0xFFFFFFFFu;
         }
@@ -288,7 +311,7 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
 #pragma unroll
                 for (int i = 0; i < kChunkGroup; ++i) {
                     const int c = cb + i;
-                    y[i] = (r < R && c < C) ? st[(size_t)r * C + c] : make_float2(kNegInf, 0.f);
+                    y[i] = (row_ok(r) && c < C) ? st[(size_t)r * C + c] : make_float2(kNegInf, 0.f);
                 }
             }
             if (greedy) {
@@ -327,26 +350,32 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
         return rho < 64 ? w0 : w1;
     };
     bool accept = true;
+    const int lim = min(k, avail);     // drafts whose rows were read
     const int dr = a.kmax + 1 + lane;  // this lane's draft row
+    float p = __builtin_nanf(""), q = __builtin_nanf("");
     if (greedy) {
         const int top = row_arg(lane);
-        accept = lane >= k || top == (int)x;
+        accept = lane >= lim || top == (int)x;
     } else {
         const float mt = row_val(m0, m1, lane), izt = row_val(iz0, iz1, lane);
         const float md = row_val(m0, m1, dr), izd = row_val(iz0, iz1, dr);
-        if (lane < k) {
-            const float p = fast_exp2((tx - mt) * c2) * izt;
-            const float q = fast_exp2((dx - md) * c2) * izd;
+        if (lane < lim) {
+            p = fast_exp2((tx - mt) * c2) * izt;
+            q = fast_exp2((dx - md) * c2) * izd;
             accept = !(q > 0.f) || (u * q < p);
-            if (writer) {
-                if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = p;
-                if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = q;
-            }
         }
     }
-    const unsigned long long rejected = __ballot(lane < k && !accept);
+    const unsigned long long rejected = __ballot(lane < lim && !accept);
+    if (!rejected && k >= avail) {  // undecided: the bonus row or a later draft is outside the window
+        if (lane == 0) sh.plan.mode = SPEC_PENDING;
+        return;
+    }
     const int j = rejected ? __ffsll((long long)rejected) - 1 : k;
     if (writer && lane <= a.kmax) toks[lane] = (lane < j) ? x : 0xFFFFFFFFu;
+    if (writer && lane < a.kmax) {  // the scan stops at j: later positions are never evaluated
+        if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = lane <= j ? p : __builtin_nanf("");
+        if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = lane <= j ? q : __builtin_nanf("");
+    }
     // Row j's statistics (uniform source lane, so every lane shuffles).
     const int jt = greedy ? row_arg(j) : 0;
     const float mj = row_val(m0, m1, j), izj = row_val(iz0, iz1, j);
@@ -368,7 +397,7 @@ __device__ void accept_sequence(const SpecArgs& a, int b, bool writer, AcceptSha
     }
     if (writer) {
         a.out_accepted[b] = j;
-        a.plan[b] = pl;
+        plan_out[b] = pl;
     }
     sh.plan = pl;
 }
@@ -498,14 +527,135 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
     }
 }
 
-// Acceptance (wave 0, redundantly per chunk workgroup) fused with the residual mass of one chunk
-// of the resampled row.
+// Pass 2: acceptance over the window, one wave per sequence. A decided sequence gets its outputs
+// and its draw plan here. An undecided one (every draft in the window accepted, more drafts or
+// the bonus row beyond it) is marked SPEC_PENDING, with the (row, chunk) items of its remaining
+// rows for the next pass: the scan of speculative.rs:315-323 stops at the first rejection, so
+// rows after it are never needed.
+__global__ __launch_bounds__(64) void spec_decide_kernel(SpecArgs a) {
+    __shared__ AcceptShared acc;
+    const int b = blockIdx.x;
+    accept_sequence(a, b, a.win, true, a.plan, acc);
+    if (threadIdx.x != 0) return;
+    if (acc.plan.mode != SPEC_PENDING) {
+        a.tail[b] = make_int2(0, 0);
+        return;
+    }
+    const int k = a.num_draft[b];  // in [win, kmax]: the scan checked it
+    const bool greedy = !(a.temperature[b] > 0.f);
+    const int nt = k - a.win + 1;             // target rows win .. k
+    const int nd = greedy ? 0 : k - a.win;    // draft rows win .. k - 1
+    a.tail[b] = make_int2((nt + nd) * a.C, nt | (greedy ? 1 << 16 : 0));
+    a.plan[b].mode = SPEC_PENDING;
+}
+
+// Pass 3: the remaining rows of the pending sequences, spread evenly over a fixed grid. Every
+// workgroup scans the per-sequence item counts into LDS, then takes items blockIdx.x,
+// blockIdx.x + gridDim.x, ... (item -> sequence by the scan, -> row and chunk by division),
+// loading the next item before reducing the current one.
+template <bool VEC>
+__global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
+    __shared__ int s_pre[kMaxLazyBatch + 1];  // exclusive prefix of the item counts
+    __shared__ int s_info[kMaxLazyBatch];     // target rows left | greedy << 16
+    __shared__ int s_wsum[4];
+    __shared__ float shv[4];
+    __shared__ int shi[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int kTiles = kMaxLazyBatch / kT;
+    int2 ti[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {  // every load first, then the scan
+        const int i = t * kT + (int)threadIdx.x;
+        ti[t] = i < a.B ? a.tail[i] : make_int2(0, 0);
+    }
+    int carry = 0;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        if (t * kT >= a.B) break;
+        const int i = t * kT + (int)threadIdx.x;
+        int inc = ti[t].x;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += y;
+        }
+        if (lane == 63) s_wsum[wave] = inc;
+        __syncthreads();
+        int before = carry;
+        for (int w = 0; w < wave; ++w) before += s_wsum[w];
+        if (i < a.B) {
+            s_pre[i + 1] = before + inc;
+            s_info[i] = ti[t].y;
+        }
+        carry += (s_wsum[0] + s_wsum[1]) + (s_wsum[2] + s_wsum[3]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) s_pre[0] = 0;
+    __syncthreads();
+    const int total = s_pre[a.B];
+    int it = blockIdx.x;
+    if (it >= total) return;
+
+    // Item -> (sequence, statistics row, chunk): the last sequence whose prefix is <= item, by
+    // binary search from the previous item's sequence (items only grow).
+    int b = 0;
+    auto locate = [&](int item, int& row, int& c, int& k, bool& greedy) {
+        int hi = a.B - 1;
+        while (b < hi) {
+            const int mid = (b + hi + 1) >> 1;
+            if (s_pre[mid] <= item) b = mid;
+            else hi = mid - 1;
+        }
+        const int local = item - s_pre[b];
+        const int info = s_info[b];
+        const int nt = info & 0xffff;
+        greedy = (info >> 16) != 0;
+        k = nt + a.win - 1;
+        const int ri = local / a.C;
+        c = local - ri * a.C;
+        row = ri < nt ? a.win + ri : a.kmax + 1 + a.win + (ri - nt);
+    };
+    struct Item {
+        int b, row, c, k;
+        bool greedy;
+    };
+    auto load_item = [&](int item, Item& m, float (&x)[kPer]) {
+        locate(item, m.row, m.c, m.k, m.greedy);
+        m.b = b;
+        const int v0 = m.c * a.chunk;
+        load_strided<VEC>(stats_row_base(a, b, m.row), v0, min(a.V, v0 + a.chunk), x);
+    };
+    const int step = gridDim.x;
+    float xa[kPer], xb[kPer];
+    Item ma, mb;
+    load_item(it, ma, xa);
+    while (true) {
+        int nx = it + step;
+        if (nx < total) load_item(nx, mb, xb);
+        chunk_stats<VEC>(a, ma.b, ma.row, ma.c, ma.k, ma.greedy ? 0.f : a.temperature[ma.b], xa, shv, shi);
+        if (nx >= total) break;
+        it = nx;
+        nx = it + step;
+        if (nx < total) load_item(nx, ma, xa);
+        chunk_stats<VEC>(a, mb.b, mb.row, mb.c, mb.k, mb.greedy ? 0.f : a.temperature[mb.b], xb, shv, shi);
+        if (nx >= total) break;
+        it = nx;
+    }
+}
+
+// Residual (and p) mass of one chunk of the row to resample. The plan comes from the window's
+// scan; a sequence that was pending repeats the scan over all its rows here (wave 0, in every
+// chunk workgroup; the chunk-0 workgroup stores the outputs).
 template <bool VEC>
 __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
     __shared__ AcceptShared acc;
     __shared__ float sh[4];
     const int c = blockIdx.x % a.C, b = blockIdx.x / a.C;
-    if (threadIdx.x < 64) accept_sequence(a, b, c == 0, acc);
+    if (threadIdx.x < 64) {
+        const SpecPlan pl = a.plan[b];
+        // plan[b] is only read here; the full scan's plan goes to plan_tail.
+        if (pl.mode == SPEC_PENDING) accept_sequence(a, b, a.kmax + 1, c == 0, a.plan_tail, acc);
+        else if (threadIdx.x == 0) acc.plan = pl;
+    }
     __syncthreads();
     const SpecPlan pl = acc.plan;
     if (pl.mode == SPEC_DONE) return;
@@ -543,7 +693,8 @@ __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
         my_r += w.x;
         my_p += w.y;
     }
-    const SpecPlan pl = a.plan[b];
+    const SpecPlan p0 = a.plan[b], p1 = a.plan_tail[b];
+    const SpecPlan pl = p0.mode == SPEC_PENDING ? p1 : p0;
     if (pl.mode == SPEC_DONE) return;
     draw_token<VEC>(a, b, pl, ds, my_r, my_p);
 }
@@ -552,12 +703,19 @@ __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
+    // Window rows: target rows 0 .. min(win, kmax + 1) - 1, draft rows 0 .. min(win, kmax) - 1.
+    const dim3 wgrid(a.C * a.B, min(a.win, a.kmax + 1) + min(a.win, a.kmax));
+    const bool tail = a.kmax >= a.win;  // otherwise every sequence is decided by the window
     if (a.vec4) {
-        spec_stats_kernel<true><<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
+        spec_stats_kernel<true><<<wgrid, kT, 0, stream>>>(a);
+        spec_decide_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
+        if (tail) spec_stats_tail_kernel<true><<<dim3(a.tail_wgs), kT, 0, stream>>>(a);
         spec_resample_kernel<true><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
         spec_pick_kernel<true><<<dim3(a.B), kT, 0, stream>>>(a);
     } else {
-        spec_stats_kernel<false><<<dim3(a.C * a.B, 2 * a.kmax + 1), kT, 0, stream>>>(a);
+        spec_stats_kernel<false><<<wgrid, kT, 0, stream>>>(a);
+        spec_decide_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
+        if (tail) spec_stats_tail_kernel<false><<<dim3(a.tail_wgs), kT, 0, stream>>>(a);
         spec_resample_kernel<false><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
         spec_pick_kernel<false><<<dim3(a.B), kT, 0, stream>>>(a);
     }

@@ -44,8 +44,10 @@ def _dev_tensor(t, name, dtype, shape, device):
 
 
 def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, temperature,
-                        u_accept, u_resample, *, return_probs=False, out=None):
-    """Queues the verify kernels on torch's current stream; see :func:`verify_drafts`."""
+                        u_accept, u_resample, *, return_probs=False, out=None, window=0):
+    """Queues the verify kernels on torch's current stream; see :func:`verify_drafts`.
+    ``window``: draft positions whose logit rows are read before the first acceptance scan
+    (0 = the library default); a tuning knob only, outputs do not depend on it."""
     dev = target_logits.device
     if dev.type != "cuda":
         raise ValueError("verify_drafts runs on a GPU device; got " + str(dev))
@@ -70,7 +72,7 @@ def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, te
     if return_probs:
         p = torch.empty((B, kmax), dtype=torch.float32, device=dev)
         q = torch.empty((B, kmax), dtype=torch.float32, device=dev)
-    params = _lib.SpecVerifyParams(B, kmax, V, _lib.KYRO_F32)
+    params = _lib.SpecVerifyParams(B, kmax, V, _lib.KYRO_F32, int(window))
     ctx = _lib.context(dev.index or 0)
     ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
     ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
@@ -82,7 +84,7 @@ def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, te
 
 
 def verify_drafts(target_logits, draft_logits, draft_tokens, num_draft, temperature, u_accept,
-                  u_resample, *, return_probs=False):
+                  u_resample, *, return_probs=False, window=0):
     """Verifies a batch of drafts (src/speculative.rs:286-339, rejection rule per Leviathan et
     al. 2023) and synchronises.
 
@@ -92,6 +94,6 @@ def verify_drafts(target_logits, draft_logits, draft_tokens, num_draft, temperat
     Returns VerifyResult; ``emitted()`` gives verify_drafts' token lists.
     """
     res = verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, temperature,
-                              u_accept, u_resample, return_probs=return_probs)
+                              u_accept, u_resample, return_probs=return_probs, window=window)
     _lib.context(target_logits.device.index or 0).sync()
     return res

@@ -205,13 +205,19 @@ class VerifyCase:
     def batch(self):
         return int(self.target.shape[0])
 
-    def logit_bytes(self) -> int:
-        """Algorithmic logit bytes: target rows 0..k_b of every sequence, draft rows 0..k_b-1 of
-        sampled sequences (greedy sequences never read draft logits)."""
+    def logit_bytes(self, accepted=None) -> int:
+        """Algorithmic logit bytes, each row counted once. Without `accepted`: target rows
+        0..k_b of every sequence and draft rows 0..k_b-1 of sampled sequences (greedy sequences
+        never read draft logits). With the accepted lengths j_b: only the rows the acceptance
+        scan evaluates, target rows 0..j_b and draft rows 0..min(j_b, k_b - 1)."""
         V = self.target.shape[2]
         k = self.num_draft.astype(np.int64)
         sampled = self.temperature > 0
-        rows = int((k + 1).sum() + (k * sampled).sum())
+        if accepted is None:
+            rows = int((k + 1).sum() + (k * sampled).sum())
+        else:
+            j = np.asarray(accepted).astype(np.int64)
+            rows = int((j + 1).sum() + (np.minimum(j + 1, k) * sampled).sum())
         return rows * V * 4
 
 

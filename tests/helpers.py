@@ -103,8 +103,14 @@ def assert_verify_parity(res, case: wl.VerifyCase, orc: dict, max_exempt: int = 
             exempt += 1
     assert exempt <= max_exempt, f"{exempt} margin exemptions"
     if res.p_draft is not None:
+        # The scan stops at the first rejection: probabilities exist for drafts 0 .. accepted of
+        # sampled sequences and are NaN after it.
+        pos = np.arange(case.draft_tokens.shape[1])[None, :]
+        evaluated = ((pos < case.num_draft[:, None]) & (pos <= acc[:, None])
+                     & (case.temperature[:, None] > 0))
         for name in ("p_draft", "q_draft"):
             g = getattr(res, name).cpu().numpy().astype(np.float64)
+            assert np.array_equal(~np.isnan(g), evaluated), f"{name}: NaN pattern differs from the scan"
             o = orc[name]
             both = ~np.isnan(g) & ~np.isnan(o)
             if both.any():

@@ -83,6 +83,32 @@ def test_mixed_batch_reduced(gpu):
     h.assert_verify_parity(run(case, gpu), case, h.oracle_verify(case), max_exempt=1)
 
 
+@pytest.mark.parametrize("window", [1, 2, 3, 5, 9, 64])
+def test_window_does_not_change_outputs(gpu, window):
+    """Rows after the first window are read only for sequences that accept every draft in it;
+    every window gives the oracle's outputs, bit for bit the same as reading all rows at once."""
+    k = wl.rng(1, wl.S_KSEQ).integers(0, 9, size=40)
+    case = wl.verify_mixed(k, vocab=3000)
+    t = h.verify_tensors(case, gpu)
+    res = kyro_amd.verify_drafts(**t, return_probs=True, window=window)
+    h.assert_verify_parity(res, case, h.oracle_verify(case), max_exempt=1)
+    ref = kyro_amd.verify_drafts(**t, return_probs=True, window=64)
+    assert torch.equal(res.accepted, ref.accepted) and torch.equal(res.tokens, ref.tokens)
+    assert torch.equal(torch.nan_to_num(res.p_draft, -1.0), torch.nan_to_num(ref.p_draft, -1.0))
+
+
+def test_window_all_accepted_reads_bonus_row(gpu):
+    """Identical draft and target: every sequence passes the window and its bonus row comes from
+    the pass over the remaining rows."""
+    case = wl.make_verify_case(batch=12, kmax=6, vocab=4000, target_sigma=2.0, noise_sigma=0.0,
+                               temperature=1.0, num_draft=np.arange(12) % 7, seed=5)
+    t = h.verify_tensors(case, gpu)
+    for window in (1, 2, 6):
+        res = kyro_amd.verify_drafts(**t, return_probs=True, window=window)
+        assert res.accepted.cpu().tolist() == case.num_draft.tolist()
+        h.assert_verify_parity(res, case, h.oracle_verify(case))
+
+
 def test_full_llama3_8b(gpu):
     case = wl.verify_llama3_8b()
     res = run(case, gpu)
