@@ -99,6 +99,12 @@ def cpu_baseline(sample: int, threads: int):
                            vcase.temperature, vcase.u_accept, vcase.u_resample, precision="f32")
     t2 = time.perf_counter()
     tokens = int(np.sum(r["accepted"] + 1))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
     return {
         "value": tokens / (t2 - t0),
         "unit": "tok/s",
@@ -107,6 +113,8 @@ def cpu_baseline(sample: int, threads: int):
         "sample": (f"{sample} of {B} sequences of the same step (attention over ctx {CTX}, "
                    f"GQA {HQ}/{HKV}, then acceptance over V {VOCAB}); f32 CPU oracle, attention on "
                    f"{threads} threads ({t1 - t0:.2f} s), acceptance on 1 thread ({t2 - t1:.2f} s)"),
+        "cpu_model": model,
+        "host_cpus": os.cpu_count(),
     }
 
 
@@ -201,6 +209,8 @@ def main():
     ap.add_argument("--window", type=int, default=0,
                     help="draft positions read before the first acceptance scan (0 = library default)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU-baseline sample")
+    ap.add_argument("--cold-steps", type=int, default=20,
+                    help="extra steps timed one by one after a 512 MiB cache-flushing write (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
@@ -276,6 +286,33 @@ def main():
     kyro_amd.sync(0)
 
     sec_per_step = (t1 - t0) / args.steps
+
+    # Cold-cache timing: a 512 MiB read between steps evicts the L2s and the 256 MiB MALL; the
+    # events bracket the step only (the back-to-back loop above is what `value` reports). A
+    # flushing write would leave the caches full of dirty lines whose write-back then lands
+    # inside the next step's first kernel.
+    def spread(vals):
+        return {"median": float(np.median(vals)), "p10": float(np.percentile(vals, 10)),
+                "p90": float(np.percentile(vals, 90))}
+
+    def summary(evs):
+        return {"step_us": spread([e[0].elapsed_time(e[2]) * 1e3 for e in evs]),
+                "attention_us": spread([e[0].elapsed_time(e[1]) * 1e3 for e in evs]),
+                "sampler_us": spread([e[1].elapsed_time(e[2]) * 1e3 for e in evs])}
+
+    cold = None
+    if args.cold_steps > 0:
+        scratch = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        for _ in range(2):
+            scratch.sum()
+        cold_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.cold_steps)]
+        for ev in cold_events:
+            scratch.sum()
+            step(ev)
+        torch.cuda.synchronize()
+        kyro_amd.sync(0)
+        del scratch
+        cold = dict(steps=args.cold_steps, **summary(cold_events))
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     samp_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
     emitted = int((acc.cpu() + 1).sum().item())
@@ -342,6 +379,8 @@ def main():
             "tokens_per_step": emitted,
             "mean_accepted": emitted / B - 1,
             "accepted_histogram": torch.bincount(acc.cpu().long(), minlength=K_DRAFT + 1).tolist(),
+            "back_to_back": summary(events),
+            "cold_cache": cold,
         },
     }
     print(json.dumps(line), flush=True)
