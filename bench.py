@@ -119,7 +119,9 @@ def cpu_baseline(sample: int, threads: int):
 
 
 def _median_us(fn, warmup, steps):
-    """Median per-call time of fn() in µs from HIP events on the current stream."""
+    """Median per-call time of fn() in µs from HIP events on the current stream. The stream is
+    first held by a short spin kernel while every timed call is queued behind it, so the events
+    measure the GPU work and not the host's time to enqueue a small call."""
     import numpy as np
     import torch
 
@@ -129,6 +131,7 @@ def _median_us(fn, warmup, steps):
         fn()
     kyro_amd.sync(0)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda._sleep(int(5e6) * max(1, steps // 20))  # a few ms at gfx950 clocks
     for e0, e1 in ev:
         e0.record()
         fn()
@@ -136,6 +139,38 @@ def _median_us(fn, warmup, steps):
     torch.cuda.synchronize()
     kyro_amd.sync(0)
     return float(np.median([e0.elapsed_time(e1) for e0, e1 in ev])) * 1e3
+
+
+def kv_append_workload(warmup, steps):
+    """One JSON line for the paged KV write (kyro_paged_kv_append): the verify step's 8 new rows per
+    sequence of the Llama-3-8B workload, and a prefill of 4 x 2048 f32 rows into a bf16 cache.
+    Algorithmic bytes: rows read (K and V) + rows written into the cache; block ids, context lengths
+    and q_start_loc are a few KB."""
+    import torch
+
+    import kyro_amd
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    res = {"workload": "kv-append"}
+    for label, b, q, old, src in (("verify_llama3_8b", B, K_DRAFT + 1, CTX - K_DRAFT - 1, torch.bfloat16),
+                                  ("prefill_4x2048_f32_rows", 4, 2048, 0, torch.float32)):
+        ctx = old + q
+        mb = (ctx + BS - 1) // BS
+        nb = max(16384, b * mb)
+        kc = torch.zeros((nb, HKV, BS, D), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        table = torch.randperm(nb, generator=g, device=dev)[: b * mb].reshape(b, mb).contiguous()
+        ctx_t = torch.full((b,), ctx, dtype=torch.int64, device=dev)
+        qs = torch.arange(0, (b + 1) * q, q, dtype=torch.int32, device=dev)
+        k = torch.randn((b * q, HKV, D), generator=g, device=dev).to(src)
+        v = torch.randn((b * q, HKV, D), generator=g, device=dev).to(src)
+        kv = kyro_amd.PagedKVCache(BS, HKV, D)
+        us = _median_us(lambda: kv.append_kv_async(k, v, kc, vc, table, ctx_t, q_start_loc=qs, max_q_len=q),
+                        warmup, steps)
+        nbytes = 2 * b * q * HKV * D * (k.element_size() + 2)
+        res[label] = {"us": us, "algorithmic_bytes": nbytes, "GB_s": nbytes / us / 1e3, "rows": b * q}
+    print(json.dumps(res), flush=True)
 
 
 def other_workload(name, warmup, steps):
@@ -217,15 +252,18 @@ def main():
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
-                             "mixed-llama3-70b", "others"],
+                             "mixed-llama3-70b", "kv-append", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
-        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b"]
+        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append"]
                  if args.workload == "others" else [args.workload])
         for n in names:
-            other_workload(n, args.warmup, args.steps)
+            if n == "kv-append":
+                kv_append_workload(args.warmup, args.steps)
+            else:
+                other_workload(n, args.warmup, args.steps)
         return
     if args.calibrate_copy:
         import torch

@@ -11,6 +11,12 @@
  *                                       sampling conventions of sample_token
  *                                       (src/worker.rs:267-362)
  *
+ * and one writes the cache the attention reads:
+ *
+ *   kyro_paged_kv_append     replaces  KVCacheManager::append_kv (src/model/kv_cache.rs:49-75)
+ *                                       as called before attention (src/model/llama.rs:80-84),
+ *                                       for a block-table cache instead of per-request tensors
+ *
  * Everything else here is plumbing a Rust `extern "C"` block (or ctypes, or C++) binds to:
  * a per-device context that owns a HIP stream and a scratch arena, opaque device buffers,
  * and status codes with a thread-local message.
@@ -37,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 2
+#define KYRO_ABI_VERSION 3
 
 typedef enum kyro_status {
     KYRO_OK = 0,
@@ -186,6 +192,43 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* params,
                      const float* temperature, const float* u_accept, const float* u_resample,
                      int32_t* out_accepted, uint32_t* out_tokens,
                      float* out_p_draft, float* out_q_draft);
+
+/* ---------------------------------------------------------------- paged KV write */
+
+typedef struct kyro_kv_append_params {
+    int32_t block_size;          /* tokens per KV block */
+    int32_t num_kv_heads;        /* Hkv */
+    int32_t head_dim;            /* D, a multiple of 8 */
+    int32_t batch_size;          /* B */
+    int32_t total_q;             /* rows of key / value: B when q_start_loc is NULL */
+    int32_t max_blocks_per_seq;  /* width of block_table */
+    int32_t num_blocks;          /* leading dim of the caches; ids outside [0,num_blocks) latch EINVAL */
+    int32_t src_dtype;           /* kyro_dtype of key / value */
+    int32_t cache_dtype;         /* kyro_dtype of the caches; F32 -> BF16 rounds to nearest even */
+    int32_t max_q_len;           /* upper bound on new rows per sequence; 0 => 1 without
+                                    q_start_loc, total_q with it */
+} kyro_kv_append_params;
+
+/*
+ * Writes each sequence's new K/V rows into the block-table cache, where attention reads them.
+ * KVCacheManager::append_kv (src/model/kv_cache.rs:49-75) concatenates a request's new
+ * [1, seq_len, Hkv, D] rows onto its cache and grows num_cached_tokens by seq_len; llama.rs:80-84
+ * appends before attention, so the context length attention sees includes the new rows. Here the
+ * caller passes that context length: new row j of sequence b (q_len rows) goes to token position
+ * p = context_lens[b] - q_len + j, i.e. slot p % block_size of block block_table[b][p / block_size].
+ *   key, value   [total_q, Hkv, D]                  src_dtype
+ *   q_start_loc  [B+1] int32 as for kyro_paged_attention_mq; NULL => one row per sequence
+ *   block_table  [B, max_blocks_per_seq] int64
+ *   context_lens [B] int64, after the append (>= q_len, <= max_blocks_per_seq * block_size)
+ *   key_cache, value_cache [num_blocks, Hkv, block_size, D]  cache_dtype (written in place; a bf16 row widens exactly into an f32 cache)
+ * Only the new rows' slots are written. Two sequences must not map a new row to the same slot
+ * (shared prefix blocks hold only old tokens). A bad block id, context length or q_start_loc
+ * latches KYRO_EINVAL for the next kyro_sync and the offending rows are not written.
+ */
+int kyro_paged_kv_append(kyro_ctx ctx, const kyro_kv_append_params* params,
+                         const void* key, const void* value, const int32_t* q_start_loc,
+                         const int64_t* block_table, const int64_t* context_lens,
+                         void* key_cache, void* value_cache);
 
 #ifdef __cplusplus
 }

@@ -1,18 +1,21 @@
 """kyro_amd — the speculative-decoding verify step of Kyro on MI355X (gfx950).
 
-Two HIP kernels behind the C ABI in include/kyro_verify.h (libkyro_verify.so):
-multi-query paged attention over a block-table KV cache, and fused rejection-sampling
-acceptance. This package is the Python host mirror of the reference's interface:
+HIP kernels behind the C ABI in include/kyro_verify.h (libkyro_verify.so):
+multi-query paged attention over a block-table KV cache, fused rejection-sampling
+acceptance, and the paged KV write. This package is the Python host mirror of the reference's interface:
 
     PagedAttention(block_size, num_heads, head_dim, num_kv_heads).forward(...)
         (src/model/attention_kernel.rs:4-31)
     verify_drafts(...)  (src/speculative.rs:286-339, extended to p/q rejection sampling)
+    PagedKVCache(block_size, num_kv_heads, head_dim).append_kv(...)
+        (src/model/kv_cache.rs:49-75, for the block-table cache the attention reads)
 """
 from ._lib import Context, KyroError, context, lib
 from .attention import PagedAttention
+from .kv_cache import PagedKVCache
 from .speculative import VerifyResult, verify_drafts, verify_drafts_async
 
-__all__ = ["Context", "KyroError", "PagedAttention", "VerifyResult", "context", "lib",
+__all__ = ["Context", "KyroError", "PagedAttention", "PagedKVCache", "VerifyResult", "context", "lib",
            "sync", "verify_drafts", "verify_drafts_async"]
 
 

@@ -48,7 +48,13 @@ class SpecVerifyParams(ctypes.Structure):
     ]
 
 
-ABI_VERSION = 2  # KYRO_ABI_VERSION of include/kyro_verify.h
+class KvAppendParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "block_size", "num_kv_heads", "head_dim", "batch_size", "total_q", "max_blocks_per_seq",
+        "num_blocks", "src_dtype", "cache_dtype", "max_q_len")]
+
+
+ABI_VERSION = 3  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -71,6 +77,7 @@ _SIGNATURES = {
     "kyro_buf_download": ([_P, _P, _P, ctypes.c_size_t, ctypes.c_size_t], ctypes.c_int),
     "kyro_paged_attention_mq": ([_P, ctypes.POINTER(PagedAttentionParams)] + [_P] * 7, ctypes.c_int),
     "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
+    "kyro_paged_kv_append": ([_P, ctypes.POINTER(KvAppendParams)] + [_P] * 7, ctypes.c_int),
 }
 
 

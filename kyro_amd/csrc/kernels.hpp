@@ -9,7 +9,7 @@ namespace kyro {
 // Bits latched into the context's device error word. The host turns them into KYRO_EINVAL.
 enum ErrorBits : int {
     ERR_BLOCK_ID = 1,   // block_table entry outside [0, num_blocks)
-    ERR_CTX_LEN = 2,    // context length < 0 or > max_blocks_per_seq * block_size
+    ERR_CTX_LEN = 2,    // context length < 0 or > max_blocks_per_seq * block_size (kv append: < q_len)
     ERR_Q_LAYOUT = 4,   // q_start_loc not monotone, out of [0, total_q], or a q_len > max_q_len
     ERR_TOKEN = 8,      // draft token id >= vocab_size
     ERR_NUM_DRAFT = 16, // num_draft outside [0, max_draft]
@@ -88,6 +88,22 @@ struct SpecArgs {
 };
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
+
+struct KvAppendArgs {
+    const void* key;         // [total_q, Hkv, D] src dtype
+    const void* value;
+    const int32_t* q_start;  // [B+1] or nullptr
+    const int64_t* table;
+    const int64_t* ctx_lens;
+    void* kc;                // [num_blocks, Hkv, bs, D] cache dtype
+    void* vc;
+    int* err;
+    int B, Hkv, D, bs, max_blocks, num_blocks, total_q, max_q_len;
+    int src_bf16, cache_bf16;
+    int vecs_per_row;        // Hkv * D / 8: one thread moves 8 elements of K and of V
+};
+
+hipError_t launch_kv_append(const KvAppendArgs& a, hipStream_t stream);
 
 #ifndef KYRO_SPEC_CHUNK
 #define KYRO_SPEC_CHUNK 4096

@@ -97,7 +97,8 @@ int sync_and_report(kyro_ctx ctx) {
     KYRO_HIP(hipMemset(ctx->err, 0, sizeof(int)));
     std::string msg = "device-side validation failed:";
     if (err & kyro::ERR_BLOCK_ID) msg += " block_table entry outside [0, num_blocks);";
-    if (err & kyro::ERR_CTX_LEN) msg += " context length < 0 or > max_blocks_per_seq * block_size;";
+    if (err & kyro::ERR_CTX_LEN)
+        msg += " context length < 0 or > max_blocks_per_seq * block_size (or, for kv_append, below the new rows);";
     if (err & kyro::ERR_Q_LAYOUT) msg += " q_start_loc not monotone / out of range, or q_len > max_q_len;";
     if (err & kyro::ERR_TOKEN) msg += " draft token id >= vocab_size;";
     if (err & kyro::ERR_NUM_DRAFT) msg += " num_draft outside [0, max_draft];";
@@ -453,6 +454,61 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         a.tail = reinterpret_cast<int2*>(base + stats_b + plan_b + csum_b + gath_b);
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_spec_verify(a, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_paged_kv_append(kyro_ctx ctx, const kyro_kv_append_params* p, const void* key,
+                         const void* value, const int32_t* q_start_loc, const int64_t* block_table,
+                         const int64_t* context_lens, void* key_cache, void* value_cache) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        if (!p) return fail(KYRO_EINVAL, "kv_append: params is null");
+        if (p->block_size <= 0 || p->num_kv_heads <= 0 || p->head_dim <= 0 || p->batch_size < 0 ||
+            p->total_q < 0 || p->max_blocks_per_seq <= 0 || p->num_blocks <= 0 || p->max_q_len < 0)
+            return fail(KYRO_EINVAL, "kv_append: sizes must be positive (batch_size, total_q, max_q_len >= 0)");
+        if (p->head_dim % 8 != 0)
+            return fail(KYRO_EUNSUPPORTED, "kv_append: head_dim %d is not a multiple of 8", p->head_dim);
+        if ((p->src_dtype != KYRO_F32 && p->src_dtype != KYRO_BF16) ||
+            (p->cache_dtype != KYRO_F32 && p->cache_dtype != KYRO_BF16))
+            return fail(KYRO_EINVAL, "kv_append: unknown dtype");
+        if (!q_start_loc && p->total_q != p->batch_size)
+            return fail(KYRO_EINVAL, "kv_append: without q_start_loc total_q must equal batch_size");
+        if (p->batch_size == 0 || p->total_q == 0) return KYRO_OK;
+        if (!key || !value || !block_table || !context_lens || !key_cache || !value_cache)
+            return fail(KYRO_EINVAL, "kv_append: null device pointer");
+        const size_t row_vecs = (size_t)p->num_kv_heads * p->head_dim / 8;
+        if (row_vecs > (size_t)INT32_MAX / 2)
+            return fail(KYRO_EUNSUPPORTED, "kv_append: num_kv_heads * head_dim too large");
+        kyro::KvAppendArgs a{};
+        a.key = key;
+        a.value = value;
+        a.q_start = q_start_loc;
+        a.table = block_table;
+        a.ctx_lens = context_lens;
+        a.kc = key_cache;
+        a.vc = value_cache;
+        a.B = p->batch_size;
+        a.Hkv = p->num_kv_heads;
+        a.D = p->head_dim;
+        a.bs = p->block_size;
+        a.max_blocks = p->max_blocks_per_seq;
+        a.num_blocks = p->num_blocks;
+        a.total_q = p->total_q;
+        a.max_q_len = p->max_q_len > 0 ? p->max_q_len : (q_start_loc ? p->total_q : 1);
+        if (!q_start_loc) a.max_q_len = 1;
+        a.src_bf16 = p->src_dtype == KYRO_BF16;
+        a.cache_bf16 = p->cache_dtype == KYRO_BF16;
+        a.vecs_per_row = (int)row_vecs;
+        if ((long long)a.max_q_len * a.vecs_per_row > (long long)INT32_MAX - 256)
+            return fail(KYRO_EUNSUPPORTED, "kv_append: max_q_len * num_kv_heads * head_dim too large");
+        const uintptr_t align = reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value) |
+                                reinterpret_cast<uintptr_t>(key_cache) | reinterpret_cast<uintptr_t>(value_cache);
+        if (align % 16 != 0) return fail(KYRO_EINVAL, "kv_append: tensors must be 16-byte aligned");
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        a.err = ctx->err;
+        KYRO_HIP(kyro::launch_kv_append(a, ctx->stream));
         return KYRO_OK;
     });
 }

@@ -64,6 +64,8 @@ def _lib(precision: str = "f64"):
         lib.oracle_sample_token.argtypes = [p, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
                                             ctypes.c_int32, ctypes.c_double]
         lib.oracle_sample_token.restype = ctypes.c_int
+        lib.oracle_kv_append.argtypes = [ctypes.c_int32] * 9 + [p] * 7
+        lib.oracle_kv_append.restype = ctypes.c_int
         _libs[path] = lib
     return _libs[path]
 
@@ -135,3 +137,24 @@ def sample_token(logits, temperature, top_p=1.0, top_k=None, u=0.5, precision="f
     return int(_lib(precision).oracle_sample_token(
         _ptr(logits), int(logits.shape[0]), float(temperature), float(top_p),
         int(top_k) if top_k else 0, float(u)))
+
+
+def kv_append(key, value, key_cache, value_cache, block_table, context_lens, *, block_size,
+              q_start_loc=None):
+    """Oracle paged KV append (src/model/kv_cache.rs:49-75 for a block-table cache). ``key`` /
+    ``value`` are [total_q, Hkv, D] float32 or uint16 (bf16 bits); the caches (float32 or uint16)
+    are updated in place. Returns 0, or 1 if some sequence was rejected (its rows not written)."""
+    key = np.ascontiguousarray(key)
+    value = np.ascontiguousarray(value)
+    assert key_cache.flags.c_contiguous and value_cache.flags.c_contiguous
+    block_table = np.ascontiguousarray(block_table, dtype=np.int64)
+    context_lens = np.ascontiguousarray(context_lens, dtype=np.int64)
+    if q_start_loc is not None:
+        q_start_loc = np.ascontiguousarray(q_start_loc, dtype=np.int32)
+    B = int(context_lens.shape[0])
+    total_q, Hkv, D = key.shape
+    return int(_lib().oracle_kv_append(
+        B, Hkv, D, block_size, int(block_table.shape[1]), int(key_cache.shape[0]), total_q,
+        1 if key.dtype == np.uint16 else 0, 1 if key_cache.dtype == np.uint16 else 0,
+        _ptr(key), _ptr(value), _ptr(q_start_loc), _ptr(block_table), _ptr(context_lens),
+        _ptr(key_cache), _ptr(value_cache)))

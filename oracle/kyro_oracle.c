@@ -27,14 +27,24 @@
  *       max, and a draw is the inverse-CDF walk in index order `r -= p; if r <= 0 -> id`.
  *   oracle_sample_token  src/worker.rs:267-362 with the uniform passed in (the reference draws it
  *       from an unseeded rand::rng()).
+ *   oracle_kv_append  src/model/kv_cache.rs:49-75 (append_kv: a request's new [seq_len, Hkv, D]
+ *       rows go after its cached ones and num_cached_tokens grows by seq_len) for a block-table
+ *       cache, as called before attention at src/model/llama.rs:80-84: new row j of a sequence
+ *       with q_len new rows and context length ctx (after the append) is token ctx - q_len + j,
+ *       slot (p % bs) of block table[b][p / bs]. f32 rows stored into a bf16 cache round to
+ *       nearest even; NaN becomes 0x7FC0.
  *
- * Pinning (tests/test_oracle.py): attention against torch-CPU scaled_dot_product_attention on
+ * Pinning (tests/test_oracle.py, tests/test_kv_append_oracle.py): attention against torch-CPU scaled_dot_product_attention on
  * the gathered contiguous KV, and the closed forms all-ones -> 1, ctx 0 -> 0, single key -> V,
  * equal keys -> mean(V), block-permutation invariance, GQA == MHA with repeated KV, causal row j
  * == non-causal over ctx - q_len + j + 1 keys. Sampler against the argmax/sampling known-answer
  * tests of src/worker.rs:395-449, numpy searchsorted for the inverse-CDF walk, q == p accepting
  * everything, and a chi-square test that the first emitted token follows p_0 whatever q is
  * (Leviathan et al. 2023, Theorem 1) — a residual with a wrong sign or a dropped max(.,0) fails it.
+ * KV append against the reference's append_kv tests (context 2 then 5; ones in, ones cached),
+ * torch's float32 -> bfloat16 conversion, a gather of the written positions through the block
+ * table that returns the new rows with every other slot unchanged, and attention after the
+ * append equal to attention over the contiguous old + new K/V.
  */
 #include <math.h>
 #include <pthread.h>
@@ -425,4 +435,59 @@ int oracle_sample_token(const float* logits, int32_t V, float temperature, float
     free(ids);
     free(pr);
     return result;
+}
+
+/* ------------------------------------------------------------------------- paged KV append */
+
+static uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+/* Returns ORACLE_EINVAL (and writes nothing for that sequence) for a bad q_start_loc, context
+ * length or block id, like the device's latched errors. Other sequences are still written. */
+int oracle_kv_append(int32_t B, int32_t Hkv, int32_t D, int32_t bs, int32_t max_blocks,
+                     int32_t num_blocks, int32_t total_q, int32_t src_bf16, int32_t cache_bf16,
+                     const void* key, const void* value, const int32_t* q_start,
+                     const int64_t* table, const int64_t* ctx_lens, void* kc, void* vc) {
+    int rc = ORACLE_OK;
+    for (int b = 0; b < B; ++b) {
+        const int r0 = q_start ? q_start[b] : b, r1 = q_start ? q_start[b + 1] : b + 1;
+        const int64_t ctx = ctx_lens[b];
+        const int q_len = r1 - r0;
+        if (r0 < 0 || r1 < r0 || r1 > total_q || ctx < q_len || ctx > (int64_t)max_blocks * bs) {
+            rc = ORACLE_EINVAL;
+            continue;
+        }
+        for (int j = 0; j < q_len; ++j) {
+            const int64_t pos = ctx - q_len + j;
+            const int64_t blk = table[(size_t)b * max_blocks + (size_t)(pos / bs)];
+            if (blk < 0 || blk >= num_blocks) {
+                rc = ORACLE_EINVAL;
+                continue;
+            }
+            const int slot = (int)(pos % bs);
+            for (int h = 0; h < Hkv; ++h) {
+                const size_t src = ((size_t)(r0 + j) * Hkv + h) * D;
+                const size_t dst = (((size_t)blk * Hkv + h) * bs + slot) * D;
+                for (int d = 0; d < D; ++d) {
+                    for (int which = 0; which < 2; ++which) {
+                        const void* in = which ? value : key;
+                        void* out = which ? vc : kc;
+                        if (src_bf16 && cache_bf16) {
+                            ((uint16_t*)out)[dst + d] = ((const uint16_t*)in)[src + d];
+                        } else {
+                            const float x = src_bf16 ? bf16_to_f32(((const uint16_t*)in)[src + d])
+                                                     : ((const float*)in)[src + d];
+                            if (cache_bf16) ((uint16_t*)out)[dst + d] = f32_to_bf16_rne(x);
+                            else ((float*)out)[dst + d] = x;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    return rc;
 }
