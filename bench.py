@@ -173,6 +173,47 @@ def kv_append_workload(warmup, steps):
     print(json.dumps(res), flush=True)
 
 
+def block_tables_workload(warmup, steps):
+    """One JSON line for the block-table producer: host allocation of 64 requests with 4096-token
+    prompts sharing a 1000-token prefix (the prefix cache warmed by one finished request, so each
+    allocation shares 62 blocks and copies one partially matched block), the device table write
+    for the verify batch (64 x 256 int64 + context lengths), and the copy-on-write of 64 blocks."""
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(0)
+    prefix = rng.integers(0, 128256, size=1000).astype(np.uint32)
+    prompts = [np.concatenate([prefix, rng.integers(0, 128256, size=CTX - 1000).astype(np.uint32)]) for _ in range(B)]
+    times, copies = [], []
+    for rep_i in range(max(3, warmup)):
+        bm = kyro_amd.BlockManager(BS, 32768, 0)
+        bm.allocate_with_prefix(10_000, prompts[0])
+        bm.free(10_000)
+        t0 = time.perf_counter()
+        for b in range(B):
+            bm.allocate_with_prefix(b, prompts[b])
+        times.append((time.perf_counter() - t0) / B * 1e6)
+        copies = bm.take_copies()
+    table = torch.zeros((B, CTX // BS + 1), dtype=torch.int64, device=dev)
+    lens = torch.zeros((B,), dtype=torch.int64, device=dev)
+    write_us = _median_us(lambda: bm.write_tables(list(range(B)), table, lens), warmup, steps)
+    kc = torch.zeros((32768, HKV, BS, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    copy_us = _median_us(lambda: kyro_amd.copy_blocks(kc, vc, copies), warmup, steps)
+    slab = HKV * BS * D * 2
+    print(json.dumps({
+        "workload": "block-tables",
+        "allocate_with_prefix_host_us_per_request": float(np.median(times)),
+        "cached_tokens_per_request": 1000,
+        "write_tables": {"us": write_us, "bytes": int(table.numel() * 8 + B * 8)},
+        "copy_blocks": {"us": copy_us, "pairs": len(copies), "bytes": 2 * 2 * slab * len(copies),
+                        "GB_s": 2 * 2 * slab * len(copies) / copy_us / 1e3},
+    }), flush=True)
+
+
 def other_workload(name, warmup, steps):
     """One JSON line for a non-default workload: the attention kernel (when the workload has one)
     and the sampler (when it has one), each on its algorithmic bytes. Inputs come from
@@ -252,16 +293,18 @@ def main():
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
-                             "mixed-llama3-70b", "kv-append", "others"],
+                             "mixed-llama3-70b", "kv-append", "block-tables", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
-        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append"]
+        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables"]
                  if args.workload == "others" else [args.workload])
         for n in names:
             if n == "kv-append":
                 kv_append_workload(args.warmup, args.steps)
+            elif n == "block-tables":
+                block_tables_workload(args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
         return

@@ -43,14 +43,15 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 3
+#define KYRO_ABI_VERSION 4
 
 typedef enum kyro_status {
     KYRO_OK = 0,
     KYRO_EINVAL = 1,       /* bad argument, shape, or (latched) bad block id / context length */
     KYRO_EOOM = 2,         /* device allocation failed */
     KYRO_EHIP = 3,         /* a HIP runtime call failed */
-    KYRO_EUNSUPPORTED = 4  /* valid request this build has no kernel for (e.g. head_dim 96) */
+    KYRO_EUNSUPPORTED = 4, /* valid request this build has no kernel for (e.g. head_dim 96) */
+    KYRO_ENOSPACE = 5      /* not enough free KV blocks, even after evicting the prefix cache */
 } kyro_status;
 
 typedef enum kyro_dtype {

@@ -9,13 +9,17 @@ acceptance, and the paged KV write. This package is the Python host mirror of th
     verify_drafts(...)  (src/speculative.rs:286-339, extended to p/q rejection sampling)
     PagedKVCache(block_size, num_kv_heads, head_dim).append_kv(...)
         (src/model/kv_cache.rs:49-75, for the block-table cache the attention reads)
+    BlockManager(block_size, num_gpu_blocks, num_cpu_blocks), RadixCache(max_capacity)
+        (src/scheduler/block_manager.rs, src/scheduler/radix_cache.rs) and the device tables
 """
 from ._lib import Context, KyroError, context, lib
 from .attention import PagedAttention
+from .block_manager import BlockManager, RadixCache, copy_blocks
 from .kv_cache import PagedKVCache
 from .speculative import VerifyResult, verify_drafts, verify_drafts_async
 
-__all__ = ["Context", "KyroError", "PagedAttention", "PagedKVCache", "VerifyResult", "context", "lib",
+__all__ = ["BlockManager", "Context", "KyroError", "PagedAttention", "PagedKVCache", "RadixCache",
+           "VerifyResult", "context", "copy_blocks", "lib",
            "sync", "verify_drafts", "verify_drafts_async"]
 
 

@@ -12,11 +12,12 @@ import threading
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkyro_verify.so")
 
-KYRO_OK, KYRO_EINVAL, KYRO_EOOM, KYRO_EHIP, KYRO_EUNSUPPORTED = 0, 1, 2, 3, 4
+KYRO_OK, KYRO_EINVAL, KYRO_EOOM, KYRO_EHIP, KYRO_EUNSUPPORTED, KYRO_ENOSPACE = 0, 1, 2, 3, 4, 5
 KYRO_F32, KYRO_BF16 = 0, 1
 KYRO_ATTN_AUTO, KYRO_ATTN_VECTOR, KYRO_ATTN_MFMA = 0, 1, 2
 
-_STATUS_NAMES = {0: "KYRO_OK", 1: "KYRO_EINVAL", 2: "KYRO_EOOM", 3: "KYRO_EHIP", 4: "KYRO_EUNSUPPORTED"}
+_STATUS_NAMES = {0: "KYRO_OK", 1: "KYRO_EINVAL", 2: "KYRO_EOOM", 3: "KYRO_EHIP", 4: "KYRO_EUNSUPPORTED",
+                 5: "KYRO_ENOSPACE"}
 
 
 class KyroError(RuntimeError):
@@ -54,7 +55,11 @@ class KvAppendParams(ctypes.Structure):
         "num_blocks", "src_dtype", "cache_dtype", "max_q_len")]
 
 
-ABI_VERSION = 3  # KYRO_ABI_VERSION of include/kyro_verify.h
+class CopyBlocksParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("block_size", "num_kv_heads", "head_dim", "num_blocks", "dtype")]
+
+
+ABI_VERSION = 4  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -78,6 +83,28 @@ _SIGNATURES = {
     "kyro_paged_attention_mq": ([_P, ctypes.POINTER(PagedAttentionParams)] + [_P] * 7, ctypes.c_int),
     "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
     "kyro_paged_kv_append": ([_P, ctypes.POINTER(KvAppendParams)] + [_P] * 7, ctypes.c_int),
+    # include/kyro_blocks.h
+    "kyro_radix_create": ([ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(_P)], ctypes.c_int),
+    "kyro_radix_destroy": ([_P], ctypes.c_int),
+    "kyro_radix_match_prefix": ([_P, _P, ctypes.c_int64, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
+    "kyro_radix_insert": ([_P, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
+    "kyro_radix_evict_lru": ([_P, _P, ctypes.c_int64, _P], ctypes.c_int),
+    "kyro_radix_num_cached_blocks": ([_P], ctypes.c_int64),
+    "kyro_bm_create": ([ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(_P)], ctypes.c_int),
+    "kyro_bm_destroy": ([_P], ctypes.c_int),
+    "kyro_bm_allocate_with_prefix": ([_P, ctypes.c_uint64, _P, ctypes.c_int64, _P], ctypes.c_int),
+    "kyro_bm_allocate": ([_P, ctypes.c_uint64, ctypes.c_int64], ctypes.c_int),
+    "kyro_bm_append_slots": ([_P, ctypes.c_uint64, ctypes.c_int64], ctypes.c_int),
+    "kyro_bm_truncate": ([_P, ctypes.c_uint64, ctypes.c_int64], ctypes.c_int),
+    "kyro_bm_free": ([_P, ctypes.c_uint64, ctypes.c_int32], ctypes.c_int),
+    "kyro_bm_request_blocks": ([_P, ctypes.c_uint64, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
+    "kyro_bm_take_copies": ([_P, _P, _P, ctypes.c_int64, _P], ctypes.c_int),
+    "kyro_bm_num_free_blocks": ([_P], ctypes.c_int64),
+    "kyro_bm_check": ([_P], ctypes.c_int),
+    "kyro_bm_num_cached_blocks": ([_P], ctypes.c_int64),
+    "kyro_bm_match_prefix": ([_P, _P, ctypes.c_int64, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
+    "kyro_bm_write_tables": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P], ctypes.c_int),
+    "kyro_copy_blocks": ([_P, ctypes.POINTER(CopyBlocksParams), _P, _P, _P, _P, ctypes.c_int64], ctypes.c_int),
 }
 
 

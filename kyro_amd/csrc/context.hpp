@@ -1,0 +1,85 @@
+// Shared host-runtime pieces of the C ABI: the context object, error reporting, device scoping,
+// the scratch arena and small host-to-device uploads.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <exception>
+#include <new>
+#include <string>
+
+#include "kyro_verify.h"
+
+struct kyro_ctx_s {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    void* arena = nullptr;  // per-call scratch, stream-ordered
+    size_t arena_bytes = 0;
+    int* err = nullptr;     // device error word
+    void* pinned = nullptr;            // host staging for small uploads (hipHostMalloc)
+    size_t pinned_bytes = 0;
+    hipEvent_t pinned_done = nullptr;  // recorded after the last copy out of `pinned`
+};
+
+namespace kyro {
+namespace rt {
+
+// Records the message as the calling thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Makes `dev` current for the scope and restores the caller's device afterwards.
+struct DeviceGuard {
+    int prev = -1;
+    hipError_t status = hipSuccess;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) status = hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+int check_ctx(kyro_ctx ctx);
+int ensure_arena(kyro_ctx ctx, size_t bytes);
+
+// One host-to-device copy of an upload.
+struct Upload {
+    void* dst;        // device
+    const void* src;  // host
+    size_t bytes;
+};
+
+// Queues the copies on the context's stream through its pinned staging buffer. The host data
+// is copied into staging before this returns, so the caller may reuse it at once; staging is
+// reused only after the previous upload's copies have executed.
+int stage_uploads(kyro_ctx ctx, const Upload* ups, int n);
+
+template <typename F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return fail(KYRO_EOOM, "host allocation failed");
+    } catch (const std::exception& e) {
+        return fail(KYRO_EHIP, "internal error: %s", e.what());
+    } catch (...) {
+        return fail(KYRO_EHIP, "internal error");
+    }
+}
+
+}  // namespace rt
+}  // namespace kyro
+
+#define KYRO_HIP(expr)                                                                          \
+    do {                                                                                        \
+        hipError_t e_ = (expr);                                                                 \
+        if (e_ != hipSuccess)                                                                   \
+            return ::kyro::rt::fail(e_ == hipErrorOutOfMemory ? KYRO_EOOM : KYRO_EHIP,          \
+                                    "%s failed: %s", #expr, hipGetErrorString(e_));             \
+    } while (0)

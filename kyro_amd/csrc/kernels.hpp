@@ -105,6 +105,17 @@ struct KvAppendArgs {
 
 hipError_t launch_kv_append(const KvAppendArgs& a, hipStream_t stream);
 
+// Whole-block copies within a cache pair (copy-on-write of a prefix block).
+struct CopyBlocksArgs {
+    const int64_t* pairs;  // [2, n]: sources then destinations
+    int64_t n;
+    int64_t slab_vecs;     // 16-byte vectors in one block of one cache
+    uint4* kc;
+    uint4* vc;
+};
+
+hipError_t launch_copy_blocks(const CopyBlocksArgs& a, hipStream_t stream);
+
 #ifndef KYRO_SPEC_CHUNK
 #define KYRO_SPEC_CHUNK 4096
 #endif

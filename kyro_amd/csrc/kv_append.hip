@@ -119,7 +119,25 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvAppendArgs a) {
     store_row8<SRC_BF16, CACHE_BF16>(a.vc, dst, rv, raw_v);
 }
 
+// One workgroup column per pair: consecutive threads copy consecutive 16-byte vectors of the
+// block's [Hkv, bs, D] slab in both caches.
+__global__ __launch_bounds__(kThreads) void copy_blocks_kernel(CopyBlocksArgs a) {
+    const int64_t pair = blockIdx.y;
+    const int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (v >= a.slab_vecs) return;
+    const int64_t src = a.pairs[pair], dst = a.pairs[a.n + pair];
+    a.kc[dst * a.slab_vecs + v] = a.kc[src * a.slab_vecs + v];
+    a.vc[dst * a.slab_vecs + v] = a.vc[src * a.slab_vecs + v];
+}
+
 }  // namespace
+
+hipError_t launch_copy_blocks(const CopyBlocksArgs& a, hipStream_t stream) {
+    if (a.n == 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.slab_vecs + kThreads - 1) / kThreads), (unsigned)a.n);
+    copy_blocks_kernel<<<grid, kThreads, 0, stream>>>(a);
+    return hipGetLastError();
+}
 
 hipError_t launch_kv_append(const KvAppendArgs& a, hipStream_t stream) {
     if (a.B == 0 || a.max_q_len == 0) return hipSuccess;

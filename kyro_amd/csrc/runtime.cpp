@@ -12,12 +12,22 @@
 #include <new>
 #include <string>
 
+#include "context.hpp"
 #include "kernels.hpp"
 #include "kyro_verify.h"
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+struct kyro_buf_s {
+    int device = 0;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+namespace kyro {
+namespace rt {
 
 int fail(int code, const char* fmt, ...) {
     char buf[512];
@@ -29,48 +39,10 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-#define KYRO_HIP(expr)                                                                        \
-    do {                                                                                      \
-        hipError_t e_ = (expr);                                                               \
-        if (e_ != hipSuccess)                                                                 \
-            return fail(e_ == hipErrorOutOfMemory ? KYRO_EOOM : KYRO_EHIP, "%s failed: %s", \
-                        #expr, hipGetErrorString(e_));                                        \
-    } while (0)
-
-// Makes `dev` current for the scope and restores the caller's device afterwards.
-struct DeviceGuard {
-    int prev = -1;
-    hipError_t status = hipSuccess;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) status = hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
-
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-}  // namespace
-
-struct kyro_ctx_s {
-    int device = 0;
-    hipStream_t own_stream = nullptr;
-    hipStream_t stream = nullptr;
-    void* arena = nullptr;  // per-call scratch, stream-ordered
-    size_t arena_bytes = 0;
-    int* err = nullptr;  // device error word
-};
-
-struct kyro_buf_s {
-    int device = 0;
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-
-namespace {
+int check_ctx(kyro_ctx ctx) {
+    if (!ctx) return fail(KYRO_EINVAL, "null kyro_ctx");
+    return KYRO_OK;
+}
 
 int ensure_arena(kyro_ctx ctx, size_t bytes) {
     if (bytes <= ctx->arena_bytes) return KYRO_OK;
@@ -84,10 +56,37 @@ int ensure_arena(kyro_ctx ctx, size_t bytes) {
     return KYRO_OK;
 }
 
-int check_ctx(kyro_ctx ctx) {
-    if (!ctx) return fail(KYRO_EINVAL, "null kyro_ctx");
+int stage_uploads(kyro_ctx ctx, const Upload* ups, int n) {
+    size_t total = 0;
+    for (int i = 0; i < n; ++i) total += align_up(ups[i].bytes, 256);
+    if (total == 0) return KYRO_OK;
+    if (!ctx->pinned_done) KYRO_HIP(hipEventCreateWithFlags(&ctx->pinned_done, hipEventDisableTiming));
+    else KYRO_HIP(hipEventSynchronize(ctx->pinned_done));  // the last upload has left staging
+    if (total > ctx->pinned_bytes) {
+        const size_t want = align_up(std::max(total, ctx->pinned_bytes * 3 / 2), size_t(1) << 16);
+        if (ctx->pinned) KYRO_HIP(hipHostFree(ctx->pinned));
+        ctx->pinned = nullptr;
+        ctx->pinned_bytes = 0;
+        KYRO_HIP(hipHostMalloc(&ctx->pinned, want, hipHostMallocDefault));
+        ctx->pinned_bytes = want;
+    }
+    char* p = static_cast<char*>(ctx->pinned);
+    for (int i = 0; i < n; ++i) {
+        if (ups[i].bytes == 0) continue;
+        std::memcpy(p, ups[i].src, ups[i].bytes);
+        KYRO_HIP(hipMemcpyAsync(ups[i].dst, p, ups[i].bytes, hipMemcpyHostToDevice, ctx->stream));
+        p += align_up(ups[i].bytes, 256);
+    }
+    KYRO_HIP(hipEventRecord(ctx->pinned_done, ctx->stream));
     return KYRO_OK;
 }
+
+}  // namespace rt
+}  // namespace kyro
+
+using namespace kyro::rt;
+
+namespace {
 
 int sync_and_report(kyro_ctx ctx) {
     KYRO_HIP(hipStreamSynchronize(ctx->stream));
@@ -104,19 +103,6 @@ int sync_and_report(kyro_ctx ctx) {
     if (err & kyro::ERR_NUM_DRAFT) msg += " num_draft outside [0, max_draft];";
     if (err & kyro::ERR_NO_DRAFT) msg += " draft_logits is NULL but a sampled sequence has drafts;";
     return fail(KYRO_EINVAL, "%s", msg.c_str());
-}
-
-template <typename F>
-int guarded(F&& f) {
-    try {
-        return f();
-    } catch (const std::bad_alloc&) {
-        return fail(KYRO_EOOM, "host allocation failed");
-    } catch (const std::exception& e) {
-        return fail(KYRO_EHIP, "internal error: %s", e.what());
-    } catch (...) {
-        return fail(KYRO_EHIP, "internal error");
-    }
 }
 
 }  // namespace
@@ -162,6 +148,9 @@ int kyro_ctx_destroy(kyro_ctx ctx) {
         if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
         if (ctx->arena) (void)hipFree(ctx->arena);
         if (ctx->err) (void)hipFree(ctx->err);
+        if (ctx->pinned_done) (void)hipEventSynchronize(ctx->pinned_done);
+        if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+        if (ctx->pinned_done) (void)hipEventDestroy(ctx->pinned_done);
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
         return KYRO_OK;
