@@ -214,6 +214,49 @@ def block_tables_workload(warmup, steps):
     }), flush=True)
 
 
+def decode_sample_workload(warmup, steps):
+    """One JSON line for the plain-decode sampler (kyro_sample_tokens): 64 rows of V 128256 f32
+    logits ~ N(0, 3), T 0.8, for each filter setting, plus one with every logit processor (bias,
+    penalties from 256 generated tokens, a grammar mask on half the rows). Bytes: the logit rows
+    read once (33 MB); the kernels re-read them from cache, so GB/s on these bytes is the rate at
+    which a batch's rows are turned into tokens."""
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(0)
+    b, v = B, VOCAB
+    x = (torch.randn((b, v), generator=g, device=dev) * 3).contiguous()
+    u = torch.rand((b,), generator=g, device=dev)
+    T = torch.full((b,), TEMP, device=dev)
+    nbytes = b * v * 4
+    res = {"workload": "decode-sample", "rows": b, "vocab": v, "logit_bytes": nbytes}
+    rng = np.random.default_rng(0)
+    settings = {
+        "greedy": dict(temperature=torch.zeros((b,), device=dev)),
+        "plain": {},
+        "top_k_50": dict(top_k=np.full(b, 50, np.int32)),
+        "top_p_0.9": dict(top_p=np.full(b, 0.9, np.float32)),
+        "top_k_50_top_p_0.9": dict(top_k=np.full(b, 50, np.int32), top_p=np.full(b, 0.9, np.float32)),
+        "processors_plain": dict(
+            bias=[{int(t): 1.0 for t in rng.integers(0, v, size=8)} for _ in range(b)],
+            penalty=[kyro_amd.penalty_adds(rng.integers(0, v, size=256), 0.5, 0.2, v) for _ in range(b)],
+            masks=np.stack([kyro_amd.grammar_mask(rng.choice(v, size=20000, replace=False), v)]),
+            mask_row=np.where(np.arange(b) % 2 == 0, 0, -1).astype(np.int32)),
+    }
+    for name, kw in settings.items():
+        kw = dict(kw)
+        temp = kw.pop("temperature", T)
+        if "bias" in kw:  # device tensors built once, outside the timed calls
+            kw = {"processors": kyro_amd.sampling.Processors(b, v, dev, **kw)}
+        out = torch.empty(b, dtype=torch.int32, device=dev)
+        us = _median_us(lambda: kyro_amd.sample_tokens_async(x, temp, u, out=out, **kw), warmup, steps)
+        res[name] = {"us": us, "GB_s": nbytes / us / 1e3}
+    print(json.dumps(res), flush=True)
+
+
 def other_workload(name, warmup, steps):
     """One JSON line for a non-default workload: the attention kernel (when the workload has one)
     and the sampler (when it has one), each on its algorithmic bytes. Inputs come from
@@ -293,18 +336,20 @@ def main():
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
-                             "mixed-llama3-70b", "kv-append", "block-tables", "others"],
+                             "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
-        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables"]
-                 if args.workload == "others" else [args.workload])
+        names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables",
+                  "decode-sample"] if args.workload == "others" else [args.workload])
         for n in names:
             if n == "kv-append":
                 kv_append_workload(args.warmup, args.steps)
             elif n == "block-tables":
                 block_tables_workload(args.warmup, args.steps)
+            elif n == "decode-sample":
+                decode_sample_workload(args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
         return

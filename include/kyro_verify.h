@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 4
+#define KYRO_ABI_VERSION 5
 
 typedef enum kyro_status {
     KYRO_OK = 0,

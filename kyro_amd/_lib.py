@@ -59,7 +59,11 @@ class CopyBlocksParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("block_size", "num_kv_heads", "head_dim", "num_blocks", "dtype")]
 
 
-ABI_VERSION = 4  # KYRO_ABI_VERSION of include/kyro_verify.h
+class SampleParams(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("batch_size", "vocab_size", "logits_dtype", "num_masks")]
+
+
+ABI_VERSION = 5  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -105,6 +109,10 @@ _SIGNATURES = {
     "kyro_bm_match_prefix": ([_P, _P, ctypes.c_int64, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
     "kyro_bm_write_tables": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P], ctypes.c_int),
     "kyro_copy_blocks": ([_P, ctypes.POINTER(CopyBlocksParams), _P, _P, _P, _P, ctypes.c_int64], ctypes.c_int),
+    # include/kyro_sample.h
+    "kyro_sample_tokens": ([_P, ctypes.POINTER(SampleParams)] + [_P] * 14, ctypes.c_int),
+    "kyro_penalty_adds": ([_P, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_int32, _P, _P,
+                           ctypes.c_int64, _P], ctypes.c_int),
 }
 
 

@@ -116,6 +116,30 @@ struct CopyBlocksArgs {
 
 hipError_t launch_copy_blocks(const CopyBlocksArgs& a, hipStream_t stream);
 
+// Plain-decode sampling with logit processors.
+struct SampleArgs {
+    const float* logits;        // [B, V]
+    float* ws;                  // [B, V] processed rows (rows that have a processor)
+    const float* temperature;   // [B]
+    const float* top_p;         // [B] or nullptr (1.0)
+    const int32_t* top_k;       // [B] or nullptr (off)
+    const float* u;             // [B]
+    const int32_t* bias_off;    // [B+1] or nullptr
+    const uint32_t* bias_tok;
+    const float* bias_val;
+    const int32_t* pen_off;     // [B+1] or nullptr
+    const uint32_t* pen_tok;
+    const float* pen_val;
+    const uint32_t* mask;       // [num_masks, mask_words]
+    const int32_t* mask_row;    // [B] (-1: no mask) or nullptr
+    uint32_t* out;              // [B]
+    int* err;
+    int B, V, num_masks, mask_words;
+    int vec4;                   // rows (logits and workspace) are 16-byte aligned
+};
+
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
+
 #ifndef KYRO_SPEC_CHUNK
 #define KYRO_SPEC_CHUNK 4096
 #endif

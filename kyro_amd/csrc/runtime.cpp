@@ -99,7 +99,7 @@ int sync_and_report(kyro_ctx ctx) {
     if (err & kyro::ERR_CTX_LEN)
         msg += " context length < 0 or > max_blocks_per_seq * block_size (or, for kv_append, below the new rows);";
     if (err & kyro::ERR_Q_LAYOUT) msg += " q_start_loc not monotone / out of range, or q_len > max_q_len;";
-    if (err & kyro::ERR_TOKEN) msg += " draft token id >= vocab_size;";
+    if (err & kyro::ERR_TOKEN) msg += " a draft, bias or penalty token id >= vocab_size, or a mask_row >= num_masks;";
     if (err & kyro::ERR_NUM_DRAFT) msg += " num_draft outside [0, max_draft];";
     if (err & kyro::ERR_NO_DRAFT) msg += " draft_logits is NULL but a sampled sequence has drafts;";
     return fail(KYRO_EINVAL, "%s", msg.c_str());

@@ -64,6 +64,8 @@ def _lib(precision: str = "f64"):
         lib.oracle_sample_token.argtypes = [p, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
                                             ctypes.c_int32, ctypes.c_double]
         lib.oracle_sample_token.restype = ctypes.c_int
+        lib.oracle_sample_decode.argtypes = [ctypes.c_int32, ctypes.c_int32] + [p] * 15
+        lib.oracle_sample_decode.restype = ctypes.c_int
         lib.oracle_kv_append.argtypes = [ctypes.c_int32] * 9 + [p] * 7
         lib.oracle_kv_append.restype = ctypes.c_int
         _libs[path] = lib
@@ -158,3 +160,44 @@ def kv_append(key, value, key_cache, value_cache, block_table, context_lens, *, 
         1 if key.dtype == np.uint16 else 0, 1 if key_cache.dtype == np.uint16 else 0,
         _ptr(key), _ptr(value), _ptr(q_start_loc), _ptr(block_table), _ptr(context_lens),
         _ptr(key_cache), _ptr(value_cache)))
+
+
+def _csr(rows, B):
+    """Per-row {token: value} dicts (or None) -> (offsets int32 [B+1], tokens uint32, values f32)."""
+    if rows is None:
+        return None, None, None
+    off = np.zeros(B + 1, np.int32)
+    toks, vals = [], []
+    for b in range(B):
+        d = rows[b] or {}
+        for t in sorted(d):
+            toks.append(t)
+            vals.append(d[t])
+        off[b + 1] = len(toks)
+    return (off, np.asarray(toks, np.uint32).reshape(-1), np.asarray(vals, np.float32).reshape(-1))
+
+
+def sample_decode(logits, temperature, u, *, top_p=None, top_k=None, bias=None, penalty=None,
+                  masks=None, mask_row=None, precision="f64"):
+    """Oracle of the worker's decode step (src/worker.rs:141-197 then sample_token :267-362) for a
+    batch. ``bias`` / ``penalty``: per-row {token: value} dicts (or None); ``masks``: uint32
+    [num_masks, ceil(V/32)] allowed-token bits, ``mask_row`` int32 [B] (-1: no mask).
+    Returns (tokens uint32 [B], margins float64 [B])."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    B, V = logits.shape
+    t = np.ascontiguousarray(temperature, dtype=np.float32).reshape(B)
+    uu = np.ascontiguousarray(u, dtype=np.float32).reshape(B)
+    tp = None if top_p is None else np.ascontiguousarray(top_p, dtype=np.float32).reshape(B)
+    tk = None if top_k is None else np.ascontiguousarray(top_k, dtype=np.int32).reshape(B)
+    bo, bt, bv = _csr(bias, B)
+    po, pt, pv = _csr(penalty, B)
+    mk = None if masks is None else np.ascontiguousarray(masks, dtype=np.uint32)
+    mr = None if mask_row is None else np.ascontiguousarray(mask_row, dtype=np.int32).reshape(B)
+    out = np.zeros(B, np.uint32)
+    mg = np.zeros(B, np.float64)
+    rc = _lib(precision).oracle_sample_decode(
+        B, V, _ptr(logits), _ptr(t), _ptr(tp), _ptr(tk), _ptr(uu), _ptr(bo), _ptr(bt), _ptr(bv),
+        _ptr(po), _ptr(pt), _ptr(pv), _ptr(mk), _ptr(mr), _ptr(out), _ptr(mg))
+    if rc != 0:
+        raise ValueError("oracle_sample_decode: a bias or penalty token is out of range")
+    return out, mg

@@ -27,6 +27,8 @@
  *       max, and a draw is the inverse-CDF walk in index order `r -= p; if r <= 0 -> id`.
  *   oracle_sample_token  src/worker.rs:267-362 with the uniform passed in (the reference draws it
  *       from an unseeded rand::rng()).
+ *   oracle_sample_decode  src/worker.rs:141-197 (logit bias, frequency / presence penalty as a
+ *       sparse additive list, grammar mask as bits) followed by sample_token, for a batch.
  *   oracle_kv_append  src/model/kv_cache.rs:49-75 (append_kv: a request's new [seq_len, Hkv, D]
  *       rows go after its cached ones and num_cached_tokens grows by seq_len) for a block-table
  *       cache, as called before attention at src/model/llama.rs:80-84: new row j of a sequence
@@ -345,13 +347,15 @@ int oracle_spec_verify(int32_t B, int32_t kmax, int32_t V, const float* target, 
 }
 
 /*
- * sample_token (src/worker.rs:267-362) with the uniform `u` passed in. T <= 0 -> argmax
- * (:290-296); else logits / T (:298), optional top-k keeping the k largest (:306-311), softmax
- * with the max subtracted (:314-323), optional top-p over the probabilities sorted descending,
- * cut after the first index whose running sum exceeds top_p (:325-338), then the walk
- * `r -= p; if r <= 0` with r = u * (kept mass) for top-p (:340-350) or r = u otherwise
- * (:352-360), falling back to the first sorted id (top-p) or the last id (otherwise).
- * Returns the token id, or -1 for V <= 0 (the reference returns a random id below 100 there).
+ * sample_token (src/worker.rs:267-362) on scaled logits z, with the uniform `u` passed in:
+ * optional top-k keeping the k largest z (:306-311; ties go to the lower index), softmax with the
+ * max subtracted (:314-323), optional top-p over the probabilities sorted descending (ties: lower
+ * index), cut after the first entry whose running sum exceeds top_p (:325-338), then the walk
+ * `r -= p; if r <= 0` (:340-360) with r = u * (mass of the cut) after top-p and r = u otherwise.
+ * The walk runs in index order without filters and in the descending order after top-k alone
+ * (the reference leaves that order to select_nth_unstable). Fallbacks: the most probable kept
+ * token after top-p, the last one walked otherwise. *margin (if given) receives the distance of
+ * r (and of top_p) from the nearest running sum that would change the decision.
  */
 static const acc_t* g_sort_keys;
 static int cmp_desc(const void* a, const void* b) {
@@ -361,80 +365,147 @@ static int cmp_desc(const void* a, const void* b) {
     return (*(const int*)a) - (*(const int*)b);
 }
 
-int oracle_sample_token(const float* logits, int32_t V, float temperature, float top_p, int32_t top_k,
-                        double u) {
-    if (V <= 0) return -1;
-    if (temperature <= 0) return argmax_f32(logits, V);
-    acc_t* y = (acc_t*)malloc(sizeof(acc_t) * (size_t)V);
+static int sample_core(const float* z, int32_t V, float top_p, int32_t top_k, double u, double* margin) {
+    acc_t* zz = (acc_t*)malloc(sizeof(acc_t) * (size_t)V);
     int* ids = (int*)malloc(sizeof(int) * (size_t)V);
+    acc_t* pr = (acc_t*)malloc(sizeof(acc_t) * (size_t)V);
     for (int v = 0; v < V; ++v) {
-        y[v] = (acc_t)logits[v] / (acc_t)temperature;
+        zz[v] = (acc_t)z[v];
         ids[v] = v;
     }
     int n = V;
-    if (top_k > 0 && top_k < V) {
-        g_sort_keys = y;
+    const int filtered = (top_k > 0 && top_k < V) || top_p < 1.0f;
+    if (filtered) {  /* descending z, ties by index (a strictly monotone exp keeps the order of p) */
+        g_sort_keys = zz;
         qsort(ids, (size_t)V, sizeof(int), cmp_desc);
-        n = top_k;
+        if (top_k > 0 && top_k < V) n = top_k;
     }
     acc_t m = -INFINITY;
     for (int i = 0; i < n; ++i)
-        if (y[ids[i]] > m) m = y[ids[i]];
-    acc_t* pr = (acc_t*)malloc(sizeof(acc_t) * (size_t)V);
-    acc_t z = 0;
+        if (zz[ids[i]] > m) m = zz[ids[i]];
+    acc_t zsum = 0;
     for (int i = 0; i < n; ++i) {
-        pr[i] = ACC_EXP(y[ids[i]] - m);
-        z += pr[i];
+        pr[i] = ACC_EXP(zz[ids[i]] - m);
+        zsum += pr[i];
     }
-    for (int i = 0; i < n; ++i) pr[i] /= z;
-    int result;
+    for (int i = 0; i < n; ++i) pr[i] /= zsum;
+    double mg = INFINITY;
+    int cut = n;
+    acc_t r = (acc_t)u;
     if (top_p < 1.0f) {
-        /* sort kept entries by probability, descending */
-        acc_t* pv = (acc_t*)malloc(sizeof(acc_t) * (size_t)V);
-        int* order = (int*)malloc(sizeof(int) * (size_t)n);
+        acc_t cum = 0, prev = 0;
         for (int i = 0; i < n; ++i) {
-            pv[i] = pr[i];
-            order[i] = i;
-        }
-        g_sort_keys = pv;
-        qsort(order, (size_t)n, sizeof(int), cmp_desc);
-        acc_t cum = 0;
-        int cut = n;
-        for (int i = 0; i < n; ++i) {
-            cum += pv[order[i]];
+            prev = cum;
+            cum += pr[i];
             if (cum > (acc_t)top_p) {
                 cut = i + 1;
                 break;
             }
         }
-        acc_t kept = 0;
-        for (int i = 0; i < cut; ++i) kept += pv[order[i]];
-        acc_t r = (acc_t)u * kept;
-        result = ids[order[0]];
-        for (int i = 0; i < cut; ++i) {
-            r -= pv[order[i]];
-            if (r <= 0) {
-                result = ids[order[i]];
-                break;
-            }
+        if (cut < n || cum > (acc_t)top_p) {
+            const double a = (double)cum - (double)top_p, b = (double)top_p - (double)prev;
+            mg = a < b ? a : b;
         }
-        free(pv);
-        free(order);
-    } else {
-        acc_t r = (acc_t)u;
-        result = ids[n - 1];
-        for (int i = 0; i < n; ++i) {
-            r -= pr[i];
-            if (r <= 0) {
-                result = ids[i];
-                break;
-            }
+        acc_t kept = 0;
+        for (int i = 0; i < cut; ++i) kept += pr[i];
+        r = (acc_t)u * kept;
+    }
+    int result = -1;
+    acc_t cum = 0;
+    for (int i = 0; i < cut; ++i) {
+        const acc_t before = cum;
+        cum += pr[i];
+        if (r - cum <= 0) {
+            result = ids[i];
+            const double a = (double)cum - (double)r, b = (double)r - (double)before;
+            const double d = a < b ? a : b;
+            if (d < mg) mg = d;
+            break;
         }
     }
-    free(y);
+    if (result < 0) {
+        result = top_p < 1.0f ? ids[0] : ids[cut - 1];
+        const double d = (double)r - (double)cum;
+        if (d < mg) mg = d;
+    }
+    if (margin) *margin = mg;
+    free(zz);
     free(ids);
     free(pr);
     return result;
+}
+
+/* candle's `logits / T` on f32 data: x * (float)(1 / T) + 0 (worker.rs:298). */
+static void scale_row(const float* x, int32_t V, float temperature, float* z) {
+    const float s = (float)(1.0 / (double)temperature);
+    for (int v = 0; v < V; ++v) z[v] = x[v] * s + 0.0f;
+}
+
+int oracle_sample_token(const float* logits, int32_t V, float temperature, float top_p, int32_t top_k,
+                        double u) {
+    if (V <= 0) return -1;
+    if (temperature <= 0) return argmax_f32(logits, V);
+    float* z = (float*)malloc(sizeof(float) * (size_t)V);
+    scale_row(logits, V, temperature, z);
+    const int t = sample_core(z, V, top_p, top_k, u, NULL);
+    free(z);
+    return t;
+}
+
+/*
+ * The worker's decode step for a batch of rows (src/worker.rs:141-197 then sample_token):
+ * y = ((logits + bias) + penalty) + mask in f32, the bias and penalty entries given per row as
+ * sparse lists (CSR offsets, tokens, values; NULL offsets: none) and the mask as bit rows
+ * (-inf where bit v of masks[mask_row[b]] is clear; mask_row NULL or -1: none). A row whose
+ * tokens are all masked gets V - 1. margins (optional) as for sample_core; +inf for argmax rows.
+ */
+int oracle_sample_decode(int32_t B, int32_t V, const float* logits, const float* temperature,
+                         const float* top_p, const int32_t* top_k, const float* u,
+                         const int32_t* bias_off, const uint32_t* bias_tok, const float* bias_val,
+                         const int32_t* pen_off, const uint32_t* pen_tok, const float* pen_val,
+                         const uint32_t* masks, const int32_t* mask_row, uint32_t* out,
+                         double* margins) {
+    float* y = (float*)malloc(sizeof(float) * (size_t)V);
+    float* z = (float*)malloc(sizeof(float) * (size_t)V);
+    const int words = (V + 31) / 32;
+    int rc = ORACLE_OK;
+    for (int b = 0; b < B; ++b) {
+        memcpy(y, logits + (size_t)b * V, sizeof(float) * (size_t)V);
+        if (bias_off)
+            for (int i = bias_off[b]; i < bias_off[b + 1]; ++i) {
+                if (bias_tok[i] < (uint32_t)V) y[bias_tok[i]] = y[bias_tok[i]] + bias_val[i];
+                else rc = ORACLE_EINVAL;
+            }
+        if (pen_off)
+            for (int i = pen_off[b]; i < pen_off[b + 1]; ++i) {
+                if (pen_tok[i] < (uint32_t)V) y[pen_tok[i]] = y[pen_tok[i]] + pen_val[i];
+                else rc = ORACLE_EINVAL;
+            }
+        if (mask_row && mask_row[b] >= 0) {
+            const uint32_t* mk = masks + (size_t)mask_row[b] * words;
+            for (int v = 0; v < V; ++v) y[v] = y[v] + (((mk[v >> 5] >> (v & 31)) & 1u) ? 0.0f : -INFINITY);
+        }
+        double mg = INFINITY;
+        const float T = temperature[b];
+        int tok;
+        if (!(T > 0)) {
+            tok = argmax_f32(y, V);
+        } else {
+            int any = 0;
+            for (int v = 0; v < V && !any; ++v) any = y[v] != -INFINITY;
+            if (!any) {
+                tok = V - 1;
+            } else {
+                scale_row(y, V, T, z);
+                tok = sample_core(z, V, top_p ? top_p[b] : 1.0f, top_k ? top_k[b] : 0, (double)u[b], &mg);
+            }
+        }
+        out[b] = (uint32_t)tok;
+        if (margins) margins[b] = mg;
+    }
+    free(y);
+    free(z);
+    return rc;
 }
 
 /* ------------------------------------------------------------------------- paged KV append */

@@ -1,0 +1,132 @@
+"""Plain-decode sampling on the GPU against the oracle, through the C ABI (kyro_sample_tokens).
+
+Tokens must match bit for bit, except rows whose decision the oracle places within 1e-5 of a
+boundary (|r - running sum| or |top_p - running sum|; f32 sums in another order may land on the
+other side). Covers argmax, index-order draws, top-k, top-p, both, ties, the logit processors
+(bias, penalties, grammar masks), a fully masked row and bad token ids.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kyro_amd
+import oracle
+from tests import helpers as h
+
+pytestmark = pytest.mark.gpu
+
+
+def run_both(x, T, u, gpu, max_exempt=1, **kw):
+    got = kyro_amd.sample_tokens(torch.from_numpy(x).to(gpu), T, u, **kw).cpu().numpy().astype(np.uint32)
+    exp, margin = oracle.sample_decode(x, T, u, **kw)
+    bad = np.nonzero(got != exp)[0]
+    for b in bad:
+        assert margin[b] < h.MARGIN, f"row {b}: gpu {got[b]} vs oracle {exp[b]}, margin {margin[b]:.3g}"
+    assert len(bad) <= max_exempt, f"{len(bad)} margin exemptions"
+    return got
+
+
+def test_reference_sample_token_kats(gpu):
+    rows = [[0.1, 0.2, 0.3, 0.4, 0.5, 10.0, 0.1, 0.2], [1.0, 2.0, 3.0, 0.5, 0.1, 0, 0, 0],
+            [0.1, 0.2, 5.0, 0.4, 0, 0, 0, 0]]
+    x = np.array(rows, np.float32)
+    assert kyro_amd.sample_tokens(torch.from_numpy(x).to(gpu), [0, 0, 0], [0.5] * 3).tolist() == [5, 2, 2]
+    assert kyro_amd.sample_token(torch.tensor([100.0, 0, 0, 0, 0], device=gpu), 2.0, 1.0, None, 0.9) == 0
+    assert kyro_amd.sample_token(torch.tensor([100.0, 0, 0, 0, 0], device=gpu), 1.0, 0.5, None, 0.9) == 0
+    for u in (0.01, 0.5, 0.99):
+        assert kyro_amd.sample_token(torch.tensor([1.0, 2.0, 10.0, 0.5, 0.1], device=gpu), 1.0, 1.0, 2, u) in (1, 2)
+
+
+@pytest.mark.parametrize("V", [37, 1000, 32000, 128256])
+@pytest.mark.parametrize("mode", ["greedy", "plain", "top_k", "top_p", "top_k_top_p"])
+def test_matches_oracle(gpu, V, mode):
+    rng = np.random.default_rng(V + len(mode))
+    B = 24
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    T = np.full(B, 0.0 if mode == "greedy" else 0.8, np.float32)
+    T[::5] = 1.7 if mode != "greedy" else 0.0
+    u = rng.random(B).astype(np.float32)
+    kw = {}
+    if "top_k" in mode:
+        kw["top_k"] = rng.choice([1, 2, 7, 50, V - 1, 0], size=B).astype(np.int32)
+    if "top_p" in mode:
+        kw["top_p"] = rng.choice([0.0, 0.3, 0.9, 0.95, 1.0], size=B).astype(np.float32)
+    run_both(x, T, u, gpu, **kw)
+
+
+def test_ties_follow_the_index(gpu):
+    """Small integer logits: many equal values, so top-k boundaries and the descending order
+    depend on the tie rule (lower index first)."""
+    rng = np.random.default_rng(7)
+    B, V = 40, 500
+    x = rng.integers(-3, 4, size=(B, V)).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    T = np.ones(B, np.float32)
+    run_both(x, T, u, gpu, top_k=rng.integers(1, 60, size=B).astype(np.int32))
+    run_both(x, T, u, gpu, top_p=rng.choice([0.2, 0.5, 0.8], size=B).astype(np.float32))
+    run_both(x, np.zeros(B, np.float32), u, gpu)
+
+
+def test_processors(gpu):
+    rng = np.random.default_rng(8)
+    B, V = 16, 5000
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    bias = [{int(t): float(rng.normal(0, 3)) for t in rng.integers(0, V, size=int(rng.integers(0, 40)))} if b % 3 else None
+            for b in range(B)]
+    penalty = [kyro_amd.penalty_adds(rng.integers(0, V, size=int(rng.integers(0, 300))), float(rng.choice([0, 0.5, -0.7])),
+                                     float(rng.choice([0, 0.3, -0.2])), V) for b in range(B)]
+    masks = np.stack([kyro_amd.grammar_mask(None, V), kyro_amd.grammar_mask(kyro_amd.sampling.JSON_TOKENS, V),
+                      kyro_amd.grammar_mask(rng.choice(V, size=700, replace=False), V)])
+    mask_row = rng.integers(-1, 3, size=B).astype(np.int32)
+    T = rng.choice([0.0, 0.6, 1.0], size=B).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    kw = dict(bias=bias, penalty=penalty, masks=masks, mask_row=mask_row)
+    got = run_both(x, T, u, gpu, **kw)
+    for b in range(B):
+        if mask_row[b] == 1:
+            assert got[b] in kyro_amd.sampling.JSON_TOKENS
+    run_both(x, T, u, gpu, top_k=np.full(B, 20, np.int32), top_p=np.full(B, 0.9, np.float32), **kw)
+    # the input logits are untouched (processing happens in the workspace)
+    xt = torch.from_numpy(x).to(gpu)
+    kyro_amd.sample_tokens(xt, T, u, **kw)
+    assert torch.equal(xt.cpu(), torch.from_numpy(x))
+
+
+def test_fully_masked_row_gets_the_last_index(gpu):
+    x = np.zeros((2, 64), np.float32)
+    masks = np.stack([kyro_amd.grammar_mask([], 64)])
+    got = kyro_amd.sample_tokens(torch.from_numpy(x).to(gpu), [1.0, 0.5], [0.3, 0.6], masks=masks, mask_row=[0, 0])
+    assert got.tolist() == [63, 63]
+
+
+def test_bad_token_ids_raise_and_recover(gpu):
+    x = torch.zeros((2, 10), device=gpu)
+    with pytest.raises(kyro_amd.KyroError, match="vocab_size"):
+        kyro_amd.sample_tokens(x, [1.0, 1.0], [0.5, 0.5], bias=[{10: 1.0}, None])
+    assert kyro_amd.sample_tokens(x, [0.0, 0.0], [0.5, 0.5], bias=[{7: 1.0}, {2: 1.0}]).tolist() == [7, 2]
+
+
+def test_token_law_on_the_gpu(gpu):
+    """Chi-square over 60k rows: plain and top-p draws follow the renormalised distributions."""
+    rng = np.random.default_rng(9)
+    V, N = 10, 60000
+    x = (rng.standard_normal(V) * 0.7).astype(np.float32)
+    z = (x * np.float32(1 / 0.9)).astype(np.float64)
+    u = rng.random(N).astype(np.float32)
+    xs = torch.from_numpy(np.broadcast_to(x, (N, V)).copy()).to(gpu)
+    import scipy.stats
+    for tp in (1.0, 0.75):
+        got = kyro_amd.sample_tokens(xs, np.full(N, 0.9, np.float32), u, top_p=np.full(N, tp, np.float32)).cpu().numpy()
+        order = np.argsort(-z, kind="stable")
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        if tp < 1:
+            cs = np.cumsum(p[order])
+            cut = int(np.argmax(cs > tp)) + 1
+            q = np.zeros(V)
+            q[order[:cut]] = p[order[:cut]]
+            p = q / q.sum()
+        counts = np.bincount(got, minlength=V)
+        nz = p > 0
+        assert counts[~nz].sum() == 0
+        assert scipy.stats.chisquare(counts[nz], p[nz] * N).pvalue > 1e-4

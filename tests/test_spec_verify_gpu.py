@@ -150,7 +150,7 @@ def test_bad_inputs_raise_and_recover(gpu):
         kyro_amd.verify_drafts(**bad)
     bad = dict(t)
     bad["draft_tokens"] = torch.tensor([[5, 100], [1, 2]], dtype=torch.int32, device=gpu)
-    with pytest.raises(kyro_amd.KyroError, match="draft token"):
+    with pytest.raises(kyro_amd.KyroError, match="draft, bias or penalty token"):
         kyro_amd.verify_drafts(**bad)
     h.assert_verify_parity(kyro_amd.verify_drafts(**t, return_probs=True), case, h.oracle_verify(case))
 
