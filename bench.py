@@ -257,6 +257,31 @@ def decode_sample_workload(warmup, steps):
     print(json.dumps(res), flush=True)
 
 
+def ngram_draft_workload(warmup, steps):
+    """One JSON line for n-gram drafting: a table of order 3 built on the host from a 1M-token
+    corpus (vocabulary 128256, drawn so that prefixes repeat), then drafts of up to 7 tokens for
+    the 64 sequences of the verify batch on the GPU."""
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(0)
+    corpus = [rng.integers(0, 2000, size=1 << 14).astype(np.uint32) for _ in range(64)]
+    t0 = time.perf_counter()
+    table = kyro_amd.NgramTable(corpus, 3)
+    build_s = time.perf_counter() - t0
+    contexts = [c[: int(rng.integers(100, 4000))] for c in corpus]
+    tail, lens = kyro_amd.context_tails(contexts, 3, dev)
+    toks = torch.empty((B, K_DRAFT), dtype=torch.int32, device=dev)
+    nd = torch.empty((B,), dtype=torch.int32, device=dev)
+    us = _median_us(lambda: table.draft(tail, lens, K_DRAFT, out=(toks, nd)), warmup, steps)
+    print(json.dumps({"workload": "ngram-draft", "corpus_tokens": int(sum(c.size for c in corpus)),
+                      "table_entries": len(table), "host_build_ms": build_s * 1e3, "draft_us": us,
+                      "mean_drafts": float(nd.float().mean().item())}), flush=True)
+
+
 def other_workload(name, warmup, steps):
     """One JSON line for a non-default workload: the attention kernel (when the workload has one)
     and the sampler (when it has one), each on its algorithmic bytes. Inputs come from
@@ -336,13 +361,14 @@ def main():
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
-                             "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "others"],
+                             "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "ngram-draft",
+                             "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
         names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables",
-                  "decode-sample"] if args.workload == "others" else [args.workload])
+                  "decode-sample", "ngram-draft"] if args.workload == "others" else [args.workload])
         for n in names:
             if n == "kv-append":
                 kv_append_workload(args.warmup, args.steps)
@@ -350,6 +376,8 @@ def main():
                 block_tables_workload(args.warmup, args.steps)
             elif n == "decode-sample":
                 decode_sample_workload(args.warmup, args.steps)
+            elif n == "ngram-draft":
+                ngram_draft_workload(args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
         return

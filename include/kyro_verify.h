@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 5
+#define KYRO_ABI_VERSION 6
 
 typedef enum kyro_status {
     KYRO_OK = 0,

@@ -63,7 +63,7 @@ class SampleParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("batch_size", "vocab_size", "logits_dtype", "num_masks")]
 
 
-ABI_VERSION = 5  # KYRO_ABI_VERSION of include/kyro_verify.h
+ABI_VERSION = 6  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -113,6 +113,13 @@ _SIGNATURES = {
     "kyro_sample_tokens": ([_P, ctypes.POINTER(SampleParams)] + [_P] * 14, ctypes.c_int),
     "kyro_penalty_adds": ([_P, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_int32, _P, _P,
                            ctypes.c_int64, _P], ctypes.c_int),
+    # include/kyro_draft.h
+    "kyro_ngram_build": ([_P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.POINTER(_P)], ctypes.c_int),
+    "kyro_ngram_destroy": ([_P], ctypes.c_int),
+    "kyro_ngram_lookup": ([_P, _P, _P], ctypes.c_int),
+    "kyro_ngram_size": ([_P], ctypes.c_int64),
+    "kyro_ngram_upload": ([_P, _P], ctypes.c_int),
+    "kyro_ngram_draft": ([_P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
 }
 
 

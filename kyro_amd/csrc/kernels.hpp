@@ -140,6 +140,31 @@ struct SampleArgs {
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 
+// N-gram drafting against an open-addressing table of (order-1)-token keys.
+struct NgramArgs {
+    const uint32_t* slots;  // [capacity, order]: key tokens then the next token
+    const uint8_t* used;    // [capacity]
+    uint64_t mask;          // capacity - 1 (a power of two)
+    int order;
+    const uint32_t* ctx_tail;  // [B, order-1]
+    const int64_t* ctx_len;    // [B]
+    uint32_t* draft;           // [B, kmax]
+    int32_t* num_draft;        // [B]
+    int B, kmax;
+};
+
+// FNV-1a over the key tokens: the host table and the device lookups must agree.
+__host__ __device__ inline uint64_t ngram_hash(const uint32_t* key, int n) {
+    uint64_t h = 1469598103934665603ull;
+    for (int i = 0; i < n; ++i) {
+        h ^= key[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+hipError_t launch_ngram_draft(const NgramArgs& a, hipStream_t stream);
+
 #ifndef KYRO_SPEC_CHUNK
 #define KYRO_SPEC_CHUNK 4096
 #endif

@@ -201,3 +201,30 @@ def sample_decode(logits, temperature, u, *, top_p=None, top_k=None, bias=None, 
     if rc != 0:
         raise ValueError("oracle_sample_decode: a bias or penalty token is out of range")
     return out, mg
+
+
+def ngram_build(corpus, order):
+    """build_ngram_table (src/speculative.rs:196-208): {prefix tuple: next}, later windows win."""
+    table = {}
+    for seq in corpus:
+        seq = [int(t) for t in seq]
+        if len(seq) < order:
+            continue
+        for i in range(len(seq) - order + 1):
+            table[tuple(seq[i:i + order - 1])] = seq[i + order - 1]
+    return table
+
+
+def ngram_draft(table, context, order, lookahead):
+    """generate_drafts' Ngram arm (src/speculative.rs:239-256) for one context."""
+    ctx = [int(t) for t in context]
+    drafts = []
+    for _ in range(lookahead):
+        if len(ctx) < order:
+            break
+        nxt = table.get(tuple(ctx[len(ctx) - (order - 1):]))
+        if nxt is None:
+            break
+        drafts.append(nxt)
+        ctx.append(nxt)
+    return drafts

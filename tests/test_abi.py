@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().kyro_abi_version() == 5
+    assert _lib.lib().kyro_abi_version() == 6
 
 
 def test_null_context_is_einval():
