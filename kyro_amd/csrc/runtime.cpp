@@ -343,9 +343,11 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
             // one CU streaming it alone; more splits only when the workgroups cannot cover the
             // chip's 256 CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
+            // With four or more workgroups per CU already, splitting only adds per-workgroup
+            // set-up and a combine pass (one workgroup fills a CU, so nothing hides them).
             constexpr int kTargetChunk = 256, kCUs = 256, kMinChunk = 16;
             const int per_split = a.units * a.row_groups;
-            splits = (mb + kTargetChunk - 1) / kTargetChunk;
+            splits = per_split >= 4 * kCUs ? 1 : (mb + kTargetChunk - 1) / kTargetChunk;
             if (per_split * splits < kCUs)
                 splits = std::min((kCUs + per_split - 1) / per_split, std::max(1, mb / kMinChunk));
         }
