@@ -33,34 +33,27 @@ B, HQ, HKV, D, BS, CTX, K_DRAFT, VOCAB, TEMP = 64, 32, 8, 128, 16, 4096, 7, 1282
 
 
 def make_inputs(dev, seed=0):
+    """The Llama-3-8B verify-step inputs of kyro_amd.workloads: counter-based Philox-4x32-10
+    streams of `seed` (one stream per tensor), normals by Box-Muller, bf16 by round-to-nearest-
+    even, draft tokens drawn from softmax(draft / T) by inverse CDF. Built on the host (a few
+    seconds) and uploaded before any timing."""
+    import numpy as np
     import torch
 
-    g = torch.Generator(device=dev).manual_seed(seed)
-    q_len = K_DRAFT + 1
-    nb_seq = CTX // BS
-    num_blocks = B * nb_seq
-    kc = torch.randn((num_blocks, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
-    vc = torch.randn((num_blocks, HKV, BS, D), generator=g, device=dev).to(torch.bfloat16)
-    table = torch.randperm(num_blocks, generator=g, device=dev).view(B, nb_seq).contiguous()
-    ctx = torch.full((B,), CTX, dtype=torch.int64, device=dev)
-    q_start = (torch.arange(B + 1, device=dev) * q_len).to(torch.int32)
-    q = torch.randn((B * q_len, HQ, D), generator=g, device=dev).to(torch.bfloat16)
+    from kyro_amd import workloads as wl
 
-    target = torch.randn((B, K_DRAFT + 1, VOCAB), generator=g, device=dev) * 3.0
-    draft = (target[:, :K_DRAFT] + torch.randn((B, K_DRAFT, VOCAB), generator=g, device=dev)).contiguous()
-    eps = 2.0 ** -24
-    probs = torch.softmax(draft.double() / TEMP, dim=-1)
-    cdf = probs.cumsum(-1)
-    u_draw = torch.rand((B, K_DRAFT, 1), generator=g, device=dev, dtype=torch.float64)
-    tokens = torch.searchsorted(cdf, u_draw * cdf[..., -1:]).clamp_(max=VOCAB - 1)
-    tokens = tokens.squeeze(-1).to(torch.int32).contiguous()
-    del probs, cdf
-    u_acc = torch.rand((B, K_DRAFT), generator=g, device=dev).clamp_(eps, 1 - eps)
-    u_res = torch.rand((B,), generator=g, device=dev).clamp_(eps, 1 - eps)
-    nd = torch.full((B,), K_DRAFT, dtype=torch.int32, device=dev)
-    temp = torch.full((B,), TEMP, dtype=torch.float32, device=dev)
-    return dict(q=q, kc=kc, vc=vc, table=table, ctx=ctx, q_start=q_start, target=target,
-                draft=draft, tokens=tokens, u_acc=u_acc, u_res=u_res, nd=nd, temp=temp)
+    a = wl.gqa_llama3_8b(batch=B, ctx=CTX, seed=seed)
+    v = wl.verify_llama3_8b(batch=B, vocab=VOCAB, seed=seed)
+
+    def up(x, bf16=False):
+        t = torch.from_numpy(np.ascontiguousarray(x))
+        return (t.view(torch.bfloat16) if bf16 else t).to(dev)
+
+    return dict(q=up(a.query, True), kc=up(a.key_cache, True), vc=up(a.value_cache, True),
+                table=up(a.block_table), ctx=up(a.context_lens), q_start=up(a.q_start_loc.astype(np.int32)),
+                target=up(v.target), draft=up(v.draft), tokens=up(v.draft_tokens.astype(np.int32)),
+                u_acc=up(v.u_accept), u_res=up(v.u_resample), nd=up(v.num_draft.astype(np.int32)),
+                temp=up(v.temperature.astype(np.float32)))
 
 
 def attention_bytes():
@@ -500,8 +493,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: torch generator seed 0 on the GPU (KV, Q ~ N(0,1); target logits ~ N(0,3); "
-                "draft = target + N(0,1); draft tokens drawn from softmax(draft/T))",
+        "data": "synthetic, Philox-4x32-10 streams of seed 0 (kyro_amd.workloads): KV, Q ~ N(0,1) bf16; "
+                "target logits ~ N(0,3); draft = target + N(0,1); draft tokens ~ softmax(draft/T) by inverse "
+                "CDF; tables: one shuffled pool of 16384 blocks",
         "config": {
             "workload": "Llama-3-8B verify step: paged attention (1 layer) + acceptance sampling",
             "batch": B, "draft_k": K_DRAFT, "context": CTX, "q_heads": HQ, "kv_heads": HKV,

@@ -161,17 +161,22 @@ __device__ __forceinline__ const float* stats_row_base(const SpecArgs& a, int b,
     return row <= a.kmax ? target_row(a, b, row) : draft_row(a, b, row - a.kmax - 1);
 }
 
+// The draft token whose logit a statistics row captures: sampled rows below k only.
+__device__ __forceinline__ uint32_t row_token(const SpecArgs& a, int b, int row, int k, float T) {
+    const int pos = row <= a.kmax ? row : row - a.kmax - 1;
+    return (T > 0.f && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
+}
+
 // Reduces chunk c of statistics row `row` (already loaded into x in the strided layout) to
 // {max, sum exp2((x - max) log2e / T)}, or {max, first argmax} for a greedy sequence, and keeps
-// the logit at the row's draft token (sampled rows below k) for the acceptance scan.
+// the logit at the row's draft token `tok` (row_token, loaded by the caller with x) for the
+// acceptance scan.
 template <bool VEC>
-__device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, int c, int k, float T,
+__device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, int c, uint32_t tok, float T,
                                             const float (&x)[kPer], float* shv, int* shi) {
     const bool greedy = !(T > 0.f);
     const int v0 = c * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
-    const int pos = row <= a.kmax ? row : row - a.kmax - 1;
-    const uint32_t tok = (!greedy && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
     if (tok >= (uint32_t)v0 && tok < (uint32_t)v1) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
@@ -225,9 +230,10 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
         if (!(T > 0.f) || i >= k || a.draft == nullptr) return;
         row = a.kmax + 1 + i;
     }
+    const uint32_t tok = row_token(a, b, row, k, T);
     float x[kPer];
     load_strided<VEC>(stats_row_base(a, b, row), c * a.chunk, min(a.V, c * a.chunk + a.chunk), x);
-    chunk_stats<VEC>(a, b, row, c, k, T, x, shv, shi);
+    chunk_stats<VEC>(a, b, row, c, tok, T, x, shv, shi);
 }
 
 // ------------------------------------------------------------------------- pass 2: acceptance
@@ -617,10 +623,16 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
     struct Item {
         int b, row, c, k;
         bool greedy;
+        uint32_t tok;
+        float T;
     };
+    // Every load an item needs (its chunk, draft token and temperature) is issued here, so the
+    // prefetched item never waits behind a later load of the item being reduced.
     auto load_item = [&](int item, Item& m, float (&x)[kPer]) {
         locate(item, m.row, m.c, m.k, m.greedy);
         m.b = b;
+        m.T = m.greedy ? 0.f : a.temperature[b];
+        m.tok = m.greedy ? 0xFFFFFFFFu : row_token(a, b, m.row, m.k, 1.f);
         const int v0 = m.c * a.chunk;
         load_strided<VEC>(stats_row_base(a, b, m.row), v0, min(a.V, v0 + a.chunk), x);
     };
@@ -631,12 +643,12 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
     while (true) {
         int nx = it + step;
         if (nx < total) load_item(nx, mb, xb);
-        chunk_stats<VEC>(a, ma.b, ma.row, ma.c, ma.k, ma.greedy ? 0.f : a.temperature[ma.b], xa, shv, shi);
+        chunk_stats<VEC>(a, ma.b, ma.row, ma.c, ma.tok, ma.T, xa, shv, shi);
         if (nx >= total) break;
         it = nx;
         nx = it + step;
         if (nx < total) load_item(nx, ma, xa);
-        chunk_stats<VEC>(a, mb.b, mb.row, mb.c, mb.k, mb.greedy ? 0.f : a.temperature[mb.b], xb, shv, shi);
+        chunk_stats<VEC>(a, mb.b, mb.row, mb.c, mb.tok, mb.T, xb, shv, shi);
         if (nx >= total) break;
         it = nx;
     }
