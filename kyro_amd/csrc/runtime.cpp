@@ -427,7 +427,10 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         a.win = p->window > 0 ? std::min(p->window, a.kmax + 1) : std::max(1, kyro::kSpecWindow);
         if (a.B > kyro::kMaxLazyBatch) a.win = a.kmax + 1;
         const long long tail_items = a.kmax >= a.win ? (long long)a.B * (2 * (a.kmax - a.win) + 1) * a.C : 1;
-        a.tail_wgs = (int)std::max(1LL, std::min((long long)kyro::kSpecTailWgs, tail_items));
+        // Up to kSpecTailWgs workgroups, more when that would give one workgroup more than 64
+        // items (the tail pass keeps one item's location per lane of a wave).
+        a.tail_wgs = (int)std::min<long long>(
+            INT32_MAX, std::max({1LL, std::min((long long)kyro::kSpecTailWgs, tail_items), (tail_items + 63) / 64}));
         const size_t stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
         const size_t plan_b = 2 * align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
         const size_t csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);

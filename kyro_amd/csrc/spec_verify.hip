@@ -95,25 +95,59 @@ __device__ __forceinline__ int strided_index(int v0, int i) {
 
 __device__ __forceinline__ int contig_index(int v0, int i) { return v0 + (int)threadIdx.x * kPer + i; }
 
+// Every load is issued unconditionally: a position past v1 reads the chunk's last vector (or
+// float) instead and is replaced by -inf afterwards (v0 < v1, and v1 is a multiple of 4 on the
+// vector path). Without branches around the loads the compiler can count the loads still in
+// flight exactly, so a prefetch issued before a reduction is not waited for by it.
 template <bool VEC>
 __device__ __forceinline__ void load_strided(const float* row, int v0, int v1, float (&x)[kPer]) {
     if constexpr (VEC) {
 #pragma unroll
         for (int it = 0; it < kPer / 4; ++it) {
             const int v = v0 + (it * kT + (int)threadIdx.x) * 4;
-            float4 f = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
-            if (v < v1) f = *reinterpret_cast<const float4*>(row + v);
-            x[it * 4 + 0] = f.x;
-            x[it * 4 + 1] = f.y;
-            x[it * 4 + 2] = f.z;
-            x[it * 4 + 3] = f.w;
+            const float4 f = *reinterpret_cast<const float4*>(row + min(v, v1 - 4));
+            const bool in = v < v1;
+            x[it * 4 + 0] = in ? f.x : kNegInf;
+            x[it * 4 + 1] = in ? f.y : kNegInf;
+            x[it * 4 + 2] = in ? f.z : kNegInf;
+            x[it * 4 + 3] = in ? f.w : kNegInf;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int v = strided_index<false>(v0, i);
-            x[i] = v < v1 ? row[v] : kNegInf;
+            const float f = row[min(v, v1 - 1)];
+            x[i] = v < v1 ? f : kNegInf;
         }
+    }
+}
+
+// Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data format, no swizzle, no
+// thread-id addressing. With stride 0 the hardware checks each access against num_records
+// (bytes) and returns zeros past it instead of faulting.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// The strided-layout load of a chunk through a buffer resource over its `bytes` bytes at
+// `chunk`: the per-thread offsets do not depend on the chunk, so a loop can issue one chunk
+// after another without vector address arithmetic, and positions past the chunk's end read as
+// zeros (the consumer masks them, strided_index >= v1).
+template <bool VEC>
+__device__ __forceinline__ void load_buffer(const float* chunk, int bytes, float (&x)[kPer]) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(chunk), (short)0, bytes, kRawBufferWord3);
+    if constexpr (VEC) {
+#pragma unroll
+        for (int it = 0; it < kPer / 4; ++it) {
+            const auto f = __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16, it * kT * 16, 0);
+            x[it * 4 + 0] = __uint_as_float(f[0]);
+            x[it * 4 + 1] = __uint_as_float(f[1]);
+            x[it * 4 + 2] = __uint_as_float(f[2]);
+            x[it * 4 + 3] = __uint_as_float(f[3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            x[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, i * kT * 4, 0));
     }
 }
 
@@ -123,18 +157,19 @@ __device__ __forceinline__ void load_contig(const float* row, int v0, int v1, fl
 #pragma unroll
         for (int it = 0; it < kPer / 4; ++it) {
             const int v = contig_index(v0, it * 4);
-            float4 f = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
-            if (v < v1) f = *reinterpret_cast<const float4*>(row + v);
-            x[it * 4 + 0] = f.x;
-            x[it * 4 + 1] = f.y;
-            x[it * 4 + 2] = f.z;
-            x[it * 4 + 3] = f.w;
+            const float4 f = *reinterpret_cast<const float4*>(row + min(v, v1 - 4));
+            const bool in = v < v1;
+            x[it * 4 + 0] = in ? f.x : kNegInf;
+            x[it * 4 + 1] = in ? f.y : kNegInf;
+            x[it * 4 + 2] = in ? f.z : kNegInf;
+            x[it * 4 + 3] = in ? f.w : kNegInf;
         }
     } else {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int v = contig_index(v0, i);
-            x[i] = v < v1 ? row[v] : kNegInf;
+            const float f = row[min(v, v1 - 1)];
+            x[i] = v < v1 ? f : kNegInf;
         }
     }
 }
@@ -167,23 +202,13 @@ __device__ __forceinline__ uint32_t row_token(const SpecArgs& a, int b, int row,
     return (T > 0.f && pos < k) ? a.draft_tokens[(size_t)b * a.kmax + pos] : 0xFFFFFFFFu;
 }
 
-// Reduces chunk c of statistics row `row` (already loaded into x in the strided layout) to
-// {max, sum exp2((x - max) log2e / T)}, or {max, first argmax} for a greedy sequence, and keeps
-// the logit at the row's draft token `tok` (row_token, loaded by the caller with x) for the
-// acceptance scan.
+// Reduces one chunk [v0, v1) of a statistics row (loaded into x in the strided layout) to
+// {max, sum exp2((x - max) log2e / T)}, or {max, first argmax as int bits} for a greedy row
+// (T <= 0). Every thread returns the result; nothing is stored.
 template <bool VEC>
-__device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, int c, uint32_t tok, float T,
-                                            const float (&x)[kPer], float* shv, int* shi) {
-    const bool greedy = !(T > 0.f);
-    const int v0 = c * a.chunk;
-    const int v1 = min(a.V, v0 + a.chunk);
-    if (tok >= (uint32_t)v0 && tok < (uint32_t)v1) {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            if (strided_index<VEC>(v0, i) == (int)tok) a.gath[(size_t)b * (2 * a.kmax + 1) + row] = x[i];
-    }
-    float2* out = a.stats + ((size_t)b * (2 * a.kmax + 1) + row) * a.C + c;
-    if (greedy) {
+__device__ __forceinline__ float2 chunk_reduce(int v0, int v1, float T, const float (&x)[kPer], float* shv,
+                                               int* shi) {
+    if (!(T > 0.f)) {
         ArgMax best = {kNegInf, 0x7fffffff};
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -191,8 +216,7 @@ __device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, i
             if (v < v1) best = argmax_pick(best, ArgMax{x[i], v});
         }
         best = block_argmax(best, shv, shi);
-        if (threadIdx.x == 0) *out = make_float2(best.v, __int_as_float(best.i));
-        return;
+        return make_float2(best.v, __int_as_float(best.i));
     }
     float m = kNegInf;
 #pragma unroll
@@ -205,7 +229,30 @@ __device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, i
         for (int i = 0; i < kPer; ++i) s += fast_exp2((x[i] - m) * c2);
     }
     s = block_sum(s, shv);
-    if (threadIdx.x == 0) *out = make_float2(m, s);
+    return make_float2(m, s);
+}
+
+// Whether the draft token `tok` lies in the chunk [v0, v1) (the same answer on every thread);
+// the thread holding its logit writes the logit to *dst.
+template <bool VEC>
+__device__ __forceinline__ bool token_logit(int v0, int v1, uint32_t tok, const float (&x)[kPer], float* dst) {
+    if (!(tok >= (uint32_t)v0 && tok < (uint32_t)v1)) return false;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (strided_index<VEC>(v0, i) == (int)tok) *dst = x[i];
+    return true;
+}
+
+// Statistics of chunk c of statistics row `row` of sequence b, stored in place, and the logit at
+// the row's draft token `tok` (row_token, loaded by the caller with x) for the acceptance scan.
+template <bool VEC>
+__device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, int c, uint32_t tok, float T,
+                                            const float (&x)[kPer], float* shv, int* shi) {
+    const int v0 = c * a.chunk;
+    const int v1 = min(a.V, v0 + a.chunk);
+    token_logit<VEC>(v0, v1, tok, x, a.gath + (size_t)b * (2 * a.kmax + 1) + row);
+    const float2 st = chunk_reduce<VEC>(v0, v1, T, x, shv, shi);
+    if (threadIdx.x == 0) a.stats[((size_t)b * (2 * a.kmax + 1) + row) * a.C + c] = st;
 }
 
 // Pass 1a: the rows of the first `win` draft positions (target rows 0 .. win - 1, draft rows
@@ -566,6 +613,7 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
     __shared__ int s_wsum[4];
     __shared__ float shv[4];
     __shared__ int shi[4];
+    __shared__ float s_tok[2];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int kTiles = kMaxLazyBatch / kT;
     int2 ti[kTiles];
@@ -598,60 +646,119 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
     if (threadIdx.x == 0) s_pre[0] = 0;
     __syncthreads();
     const int total = s_pre[a.B];
-    int it = blockIdx.x;
-    if (it >= total) return;
-
-    // Item -> (sequence, statistics row, chunk): the last sequence whose prefix is <= item, by
-    // binary search from the previous item's sequence (items only grow).
-    int b = 0;
-    auto locate = [&](int item, int& row, int& c, int& k, bool& greedy) {
-        int hi = a.B - 1;
-        while (b < hi) {
-            const int mid = (b + hi + 1) >> 1;
-            if (s_pre[mid] <= item) b = mid;
+    const int step = gridDim.x;
+    if ((int)blockIdx.x >= total) return;
+    // This workgroup's items are blockIdx.x + j * step, j < n_items <= 64 (the host sizes the
+    // grid for that). Lane j of every wave locates item j here: the sequence is the last one
+    // whose prefix is <= the item (binary search), then the row and chunk within it. The loop
+    // reads an item's location from lane j with readlane into scalar registers, so it needs no
+    // vector temporaries that could alias a load still in flight.
+    const int n_items = (total - 1 - (int)blockIdx.x) / step + 1;
+    uint32_t lptr_lo, lptr_hi;  // address of the item's chunk
+    int lrow, lc, lflags, ltok;
+    float lT;
+    {
+        const int item = (int)blockIdx.x + min(lane, n_items - 1) * step;
+        int lo = 0, hi = a.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_pre[mid] <= item) lo = mid;
             else hi = mid - 1;
         }
-        const int local = item - s_pre[b];
-        const int info = s_info[b];
-        const int nt = info & 0xffff;
-        greedy = (info >> 16) != 0;
-        k = nt + a.win - 1;
+        const int local = item - s_pre[lo];
+        const int info = s_info[lo];
+        const int nt = info & 0xffff;  // target rows left
+        const bool greedy = (info >> 16) != 0;
+        const int k = nt + a.win - 1;
         const int ri = local / a.C;
-        c = local - ri * a.C;
-        row = ri < nt ? a.win + ri : a.kmax + 1 + a.win + (ri - nt);
-    };
+        const int row = ri < nt ? a.win + ri : a.kmax + 1 + a.win + (ri - nt);
+        const int pos = row <= a.kmax ? row : row - a.kmax - 1;
+        const int c = local - ri * a.C;
+        const int v0 = c * a.chunk;
+        const uint64_t ptr = reinterpret_cast<uint64_t>(stats_row_base(a, lo, row) + v0);
+        lptr_lo = (uint32_t)ptr;
+        lptr_hi = (uint32_t)(ptr >> 32);
+        lrow = lo * (2 * a.kmax + 1) + row;
+        lc = c;
+        // The row's temperature and draft token, raw: they are selected on (greedy rows take
+        // T = 0, and only sampled rows below k capture a token) when the item is reduced, so the
+        // first chunk loads do not wait for these two.
+        lT = a.temperature[lo];
+        ltok = (int)a.draft_tokens[(size_t)lo * a.kmax + min(pos, a.kmax - 1)];
+        lflags = (int)!greedy | ((int)(pos < k) << 1);
+    }
     struct Item {
-        int b, row, c, k;
-        bool greedy;
-        uint32_t tok;
-        float T;
+        int j;     // index of the item within this workgroup's items (its lane)
+        int r, c;  // statistics row (sequence * (2 kmax + 1) + row) and chunk
     };
-    // Every load an item needs (its chunk, draft token and temperature) is issued here, so the
-    // prefetched item never waits behind a later load of the item being reduced.
-    auto load_item = [&](int item, Item& m, float (&x)[kPer]) {
-        locate(item, m.row, m.c, m.k, m.greedy);
-        m.b = b;
-        m.T = m.greedy ? 0.f : a.temperature[b];
-        m.tok = m.greedy ? 0xFFFFFFFFu : row_token(a, b, m.row, m.k, 1.f);
+    // The loop issues nothing but an item's chunk loads, unconditionally (the prefetch past the
+    // last item re-loads the last one, and is dropped), from scalar addresses and fixed
+    // per-thread offsets, into registers that stay raw until the item is reduced: with no branch
+    // around a load, no vector address arithmetic and no select on loaded values, the wait
+    // before an item's reduction leaves the next item's loads in flight.
+    auto load_item = [&](int j, Item& m, float (&x)[kPer]) {
+        j = min(j, n_items - 1);
+        const uint64_t ptr = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)lptr_lo, j) |
+                             ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)lptr_hi, j) << 32);
+        m.j = j;
+        m.r = __builtin_amdgcn_readlane(lrow, j);
+        m.c = __builtin_amdgcn_readlane(lc, j);
         const int v0 = m.c * a.chunk;
-        load_strided<VEC>(stats_row_base(a, b, m.row), v0, min(a.V, v0 + a.chunk), x);
+        load_buffer<VEC>(reinterpret_cast<const float*>(ptr), (min(a.V, v0 + a.chunk) - v0) * 4, x);
     };
-    const int step = gridDim.x;
+    // Results are not stored inside the loop: a store there is counted with the loads, and a wait
+    // for it (before its data registers are reused) would also wait for the prefetch issued
+    // before it. Thread `held` (= the item's j < 64) keeps the item's statistics (and draft-token
+    // logit) in registers instead; they are stored after the loop.
+    float2 res = make_float2(0.f, 0.f);
+    size_t res_at = 0;
+    int g_at = -1;
+    float gval = 0.f;
+    int held = 0, parity = 0;
+    auto flush = [&]() {
+        if ((int)threadIdx.x < held) {
+            a.stats[res_at] = res;
+            if (g_at >= 0) a.gath[g_at] = gval;
+        }
+        held = 0;
+    };
+    auto reduce_item = [&](const Item& m, float (&x)[kPer]) {
+        const int v0 = m.c * a.chunk;
+        const int v1 = min(a.V, v0 + a.chunk);
+        if (v1 - v0 < a.chunk) {  // the row's last chunk, partial: its tail read as zeros
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                if (strided_index<VEC>(v0, i) >= v1) x[i] = kNegInf;
+        }
+        const int fl = __builtin_amdgcn_readlane(lflags, m.j);
+        const float T = (fl & 1) ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lT), m.j)) : 0.f;
+        const uint32_t tok = fl == 3 ? (uint32_t)__builtin_amdgcn_readlane(ltok, m.j) : 0xFFFFFFFFu;
+        // s_tok alternates between two slots: the barriers inside the next item's reduction
+        // separate this item's read from the write two items later.
+        const bool has_tok = token_logit<VEC>(v0, v1, tok, x, &s_tok[parity]);
+        const float2 st = chunk_reduce<VEC>(v0, v1, T, x, shv, shi);  // its barriers publish s_tok
+        if ((int)threadIdx.x == held) {
+            res = st;
+            res_at = (size_t)m.r * a.C + m.c;
+            g_at = has_tok ? m.r : -1;
+            gval = has_tok ? s_tok[parity] : 0.f;
+        }
+        parity ^= 1;
+        ++held;
+    };
     float xa[kPer], xb[kPer];
     Item ma, mb;
-    load_item(it, ma, xa);
+    int j = 0;
+    load_item(0, ma, xa);
     while (true) {
-        int nx = it + step;
-        if (nx < total) load_item(nx, mb, xb);
-        chunk_stats<VEC>(a, ma.b, ma.row, ma.c, ma.tok, ma.T, xa, shv, shi);
-        if (nx >= total) break;
-        it = nx;
-        nx = it + step;
-        if (nx < total) load_item(nx, ma, xa);
-        chunk_stats<VEC>(a, mb.b, mb.row, mb.c, mb.tok, mb.T, xb, shv, shi);
-        if (nx >= total) break;
-        it = nx;
+        load_item(j + 1, mb, xb);
+        reduce_item(ma, xa);
+        if (++j >= n_items) break;
+        load_item(j + 1, ma, xa);
+        reduce_item(mb, xb);
+        if (++j >= n_items) break;
     }
+    flush();
 }
 
 // Residual (and p) mass of one chunk of the row to resample. The plan comes from the window's
