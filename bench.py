@@ -4,14 +4,16 @@
 Workload: the Llama-3-8B verify step — batch 64, k = 7 drafts (8 query rows per sequence), every
 context 4096 tokens, GQA 32 query / 8 kv heads, head_dim 128, bf16 KV in 16-token blocks through
 a shuffled block table, then acceptance over a 128256-entry vocabulary at temperature 0.8 with
-target logits ~ N(0, 3) and draft logits = target + N(0, 1). Synthetic data from torch's seeded
-generator, resident in HBM before timing starts.
+target logits ~ N(0, 3) and draft logits = target + N(0, 1). Synthetic data from the
+Philox-4x32-10 streams of seed 0 (kyro_amd.workloads), resident in HBM before timing starts.
 
 One step = kyro_paged_attention_mq + kyro_spec_verify on the same stream. W warm-up steps, then
 K timed steps between two synchronisations. ``value`` is verified tokens per second,
-sum_b (accepted_b + 1) / seconds per step. HIP events on the launch stream time the attention
-kernel for the roofline entry; the CPU oracle (f32 build) is timed on a bounded sample of the same
-workload for the cpu_baseline entry.
+sum_b (accepted_b + 1) / seconds per step. The same K steps are then run again with HIP events
+on the launch stream around each part; those time the attention kernel for the roofline entry
+and the per-part figures (event records cost the stream time of their own, so they stay out of
+the steps ``value`` is computed from). The CPU oracle (f32 build) is timed on a bounded sample of
+the same workload for the cpu_baseline entry.
 """
 from __future__ import annotations
 
@@ -339,8 +341,10 @@ def other_workload(name, warmup, steps):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # 200 steps (about 55 ms): with 50, the launch of the first step and the final
+    # synchronisation added about 4 us to every step's share.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--path", default="auto", choices=["auto", "vector", "mfma"])
     ap.add_argument("--splits", type=int, default=0, help="context splits (0 = automatic)")
     ap.add_argument("--window", type=int, default=0,
@@ -423,16 +427,29 @@ def main():
     kyro_amd.sync(0)
     torch.cuda.synchronize()
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    # `value`: K steps back to back, nothing else on the stream.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
+    for _ in range(args.steps):
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     kyro_amd.sync(0)
-
     sec_per_step = (t1 - t0) / args.steps
+
+    # Per-part times and the attention launch duration behind `roofline`: the same K steps again,
+    # with HIP events recorded on the launch stream before the attention kernel, between it and the
+    # sampler, and after the sampler. Each record costs the stream a few microseconds (about 10 us
+    # per step for the three), so these steps are timed apart from the ones `value` comes from.
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    kyro_amd.sync(0)
+    instrumented_sec_per_step = (t3 - t2) / args.steps
 
     # Cold-cache timing: a 512 MiB read between steps evicts the L2s and the 256 MiB MALL; the
     # events bracket the step only (the back-to-back loop above is what `value` reports). A
@@ -466,6 +483,9 @@ def main():
     a_bytes, s_bytes = attention_bytes(), sampler_bytes(acc)
     achieved = a_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = (a_bytes + s_bytes) / sec_per_step / 1e9
+    # The step's bytes as a sampler that reads every logit row would move them (KV, Q, out, all
+    # target and draft rows): 1,574,633,472 B on this workload.
+    all_rows_gbs = (a_bytes + sampler_bytes()) / sec_per_step / 1e9
 
     traffic = None
     # HBM bytes per attention launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded
@@ -519,6 +539,10 @@ def main():
             "algorithmic_bytes": a_bytes + s_bytes,
             "GB_s": step_gbs,
             "frac_of_peak": step_gbs / PEAK_HBM_GBS,
+            "all_rows_bytes": a_bytes + sampler_bytes(),
+            "all_rows_GB_s": all_rows_gbs,
+            "all_rows_frac_of_peak": all_rows_gbs / PEAK_HBM_GBS,
+            "instrumented_ms_per_step": instrumented_sec_per_step * 1e3,
             "attention_us": attn_ms * 1e3,
             "sampler_us": samp_ms * 1e3,
             "sampler_GB_s": s_bytes / (samp_ms * 1e-3) / 1e9,
