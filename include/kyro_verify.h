@@ -160,7 +160,7 @@ typedef struct kyro_spec_verify_params {
     int32_t logits_dtype; /* kyro_dtype of both logits tensors (KYRO_F32) */
     int32_t window;       /* draft positions whose logit rows are read before the first
                              acceptance scan; rows after it are read only for sequences that
-                             accept all of them. 0 = default (2); >= max_draft reads every row
+                             accept all of them. 0 = default (3); >= max_draft reads every row
                              in one pass. Outputs do not depend on it. */
 } kyro_spec_verify_params;
 

@@ -170,10 +170,13 @@ hipError_t launch_ngram_draft(const NgramArgs& a, hipStream_t stream);
 #endif
 constexpr int kSpecChunk = KYRO_SPEC_CHUNK;  // vocabulary entries per workgroup in the streaming passes
 constexpr int kMaxDraft = 63;                // one wave holds the acceptance decisions of a sequence
+// Draft positions read before the first acceptance scan. With per-position acceptance rate a
+// and k drafts, a sequence's rows read are about 2W + a^W (2 (k - W) + 1) (window rows, plus the
+// rest when the window is all accepted); W = 3 is the smallest for a between 0.5 and 0.8 at k = 7.
 #ifndef KYRO_SPEC_WINDOW
-#define KYRO_SPEC_WINDOW 2
+#define KYRO_SPEC_WINDOW 3
 #endif
-constexpr int kSpecWindow = KYRO_SPEC_WINDOW;  // draft positions read before the first acceptance scan
+constexpr int kSpecWindow = KYRO_SPEC_WINDOW;
 constexpr int kMaxLazyBatch = 2048;  // larger batches read every row in the first pass
 #ifndef KYRO_SPEC_TAIL_WGS
 #define KYRO_SPEC_TAIL_WGS 2048
