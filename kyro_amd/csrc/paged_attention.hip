@@ -202,6 +202,9 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
 
 constexpr int kMfmaD = 128;
 constexpr int kMfmaBS = 16;
+// One (block, kv head) slab of zeros, read in place of a missing block (static device memory is
+// zero-initialised when the code object loads, and nothing writes it).
+__device__ uint16_t kZeroSlab[kMfmaBS * kMfmaD];
 
 // K and V of one pair of 16-token blocks, already in MFMA operand layout (K) or ready for the
 // in-register transpose (V). 64 VGPRs.
@@ -211,26 +214,36 @@ struct KVPair {
 };
 
 // Issues the 16 loads of one block pair. A negative block id reads as zeros (never dereferenced).
+// Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// Loads the K and V operands of a pair of blocks (block ids uniform across the wave; -1 for a
+// missing block: past the split, or a bad id). Each (block, kv head) slab is read through a
+// buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
+// addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
+// a prefetched pair in flight.
 __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t block_stride, size_t kv_off, int r, int g) {
+    constexpr int kSlabBytes = kMfmaBS * kMfmaD * 2;
+    const int koff = (r * kMfmaD + 8 * g) * 2;        // bytes; + 64 s for head-dim slot s
+    const int voff = (4 * g * kMfmaD + 8 * r) * 2;    // bytes; + 256 e for token 4 g + e
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
         const int blk = bi ? blk1 : blk0;
-        if (blk >= 0) {
-            const size_t base = (size_t)blk * block_stride + kv_off;
-            const uint16_t* kb = kp + base + (size_t)r * kMfmaD + 8 * g;
-            const uint16_t* vb = vp + base + (size_t)(4 * g) * kMfmaD + 8 * r;
+        const size_t base = (size_t)(blk >= 0 ? blk : 0) * block_stride + kv_off;
+        const uint16_t* kslab = blk >= 0 ? kp + base : kZeroSlab;
+        const uint16_t* vslab = blk >= 0 ? vp + base : kZeroSlab;
+        const __amdgpu_buffer_rsrc_t kr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), (short)0, kSlabBytes, kRawBufferWord3);
+        const __amdgpu_buffer_rsrc_t vr =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), (short)0, kSlabBytes, kRawBufferWord3);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, load16(kb + 32 * s));
+        for (int s = 0; s < 4; ++s)
+            p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * s, 0));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p.v[bi][e] = load16(vb + (size_t)e * kMfmaD);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p.v[bi][e] = make_uint4(0, 0, 0, 0);
-        }
+        for (int e = 0; e < 4; ++e)
+            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 256 * e, 0));
     }
 }
 
@@ -265,7 +278,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     if (row0 > 0 && row0 >= si.rows) return;  // this row group is past the sequence's rows
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int r = lane & 15;  // MFMA row/column within a 16-tile
     const int g = lane >> 4;  // 16-lane group
     const int blk_begin = split * a.chunk_blocks;
@@ -281,9 +294,6 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
 
     stage_block_ids(a, si, blk_begin, blk_end, s_blk);
-    auto blk_at = [&](int i) -> int {
-        return i < blk_end ? __builtin_amdgcn_readfirstlane(s_blk[i - blk_begin]) : -1;
-    };
 
     {
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
@@ -318,7 +328,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         }
 
         // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
-        auto compute = [&](const KVPair& kv, int pb, int blk0, int blk1) {
+        auto compute = [&](KVPair& kv, int pb, int blk0, int blk1) {
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
             f32x4 S[2][NTW];
 #pragma unroll
@@ -332,6 +342,15 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                     S[bi][nt] = acc;
                 }
             const bool full = blk0 >= 0 && blk1 >= 0 && (pb + 2) * kMfmaBS <= full_vis;
+            if (!full) {
+                // Tokens past the context (the unused tail of the last block) get V = 0, so that
+                // whatever those cache slots hold cannot reach O through a zero probability.
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx) kv.v[bi][e] = make_uint4(0, 0, 0, 0);
+            }
             bf16x8 pB[NTW];
 #pragma unroll
             for (int nt = 0; nt < NTW; ++nt) {
@@ -400,32 +419,50 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         // pair are issued before the current pair is computed (two register buffers, unrolled).
         constexpr int step = 2 * kWaves;
         {
-            KVPair bufA, bufB;
-            int pb = blk_begin + 2 * wave;
-            int a0 = -1, a1 = -1, b0 = -1, b1 = -1;
-            if (pb < blk_end) {
-                a0 = blk_at(pb);
-                a1 = blk_at(pb + 1);
-                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+            // Pair j of this wave covers blocks pb0 + j step and pb0 + j step + 1. Lane j % 64 holds
+            // the ids of pair j in slot j / 64 (a split has at most kMaxChunkBlocks blocks, so at
+            // most kPairSlots * 64 pairs per wave); the loop reads them with readlane into scalar
+            // registers and needs no vector temporaries for addressing.
+            constexpr int kPairSlots = kMaxChunkBlocks / (2 * kWaves * 64);
+            static_assert(kPairSlots * 64 * 2 * kWaves >= kMaxChunkBlocks, "pair table too small");
+            const int pb0 = blk_begin + 2 * wave;
+            int pid0[kPairSlots], pid1[kPairSlots];
+#pragma unroll
+            for (int t = 0; t < kPairSlots; ++t) {
+                const int pbj = pb0 + (t * 64 + lane) * step;
+                pid0[t] = pbj < blk_end ? s_blk[pbj - blk_begin] : -1;
+                pid1[t] = pbj + 1 < blk_end ? s_blk[pbj + 1 - blk_begin] : -1;
             }
-            while (pb < blk_end) {
-                int pn = pb + step;
-                if (pn < blk_end) {
-                    b0 = blk_at(pn);
-                    b1 = blk_at(pn + 1);
+            auto pair_ids = [&](int j, int& b0, int& b1) {
+                b0 = __builtin_amdgcn_readlane(pid0[0], j & 63);
+                b1 = __builtin_amdgcn_readlane(pid1[0], j & 63);
+#pragma unroll
+                for (int t = 1; t < kPairSlots; ++t) {
+                    const int x0 = __builtin_amdgcn_readlane(pid0[t], j & 63);
+                    const int x1 = __builtin_amdgcn_readlane(pid1[t], j & 63);
+                    b0 = (j >> 6) == t ? x0 : b0;
+                    b1 = (j >> 6) == t ? x1 : b1;
+                }
+            };
+            const int npairs = pb0 < blk_end ? (blk_end - 1 - pb0) / step + 1 : 0;
+            KVPair bufA, bufB;
+            if (npairs > 0) {
+                // The next pair's loads are issued unconditionally: past the last pair they load
+                // the current pair again (L2-hot, and dropped), so no branch separates a prefetch
+                // from the wait that precedes the computation of the pair before it.
+                int j = 0, a0, a1, b0, b1;
+                pair_ids(0, a0, a1);
+                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                while (true) {
+                    pair_ids(min(j + 1, npairs - 1), b0, b1);
                     load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
-                }
-                compute(bufA, pb, a0, a1);
-                pb = pn;
-                if (pb >= blk_end) break;
-                pn = pb + step;
-                if (pn < blk_end) {
-                    a0 = blk_at(pn);
-                    a1 = blk_at(pn + 1);
+                    compute(bufA, pb0 + j * step, a0, a1);
+                    if (++j >= npairs) break;
+                    pair_ids(min(j + 1, npairs - 1), a0, a1);
                     load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    compute(bufB, pb0 + j * step, b0, b1);
+                    if (++j >= npairs) break;
                 }
-                compute(bufB, pb, b0, b1);
-                pb = pn;
             }
         }
 
