@@ -121,6 +121,36 @@ def test_repeat_calls_are_bitwise_identical(gpu):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_cache_slots_past_the_context_are_never_used(gpu, dtype):
+    """The slots after a sequence's last token in its last block, and every block no table
+    references, may hold anything (here NaN in K and V): the rows must still equal the oracle's,
+    which reads positions below the context length only (attention_kernel.rs:91-93,119-120)."""
+    ctx = [17, 40, 33, 100, 1, 48]
+    case = wl.make_attention_case(context_lens=ctx, q_lens=[1, 5, 8, 3, 1, 4], num_heads=8,
+                                  num_kv_heads=2, dtype=dtype, seed=13, num_blocks=64)
+    nan = np.uint16(0x7FC0) if dtype == "bf16" else np.float32(np.nan)
+    used = set()
+    for b, c in enumerate(ctx):
+        nb = -(-c // case.block_size)
+        used.update(int(x) for x in case.block_table[b, :nb])
+        last, tail = int(case.block_table[b, nb - 1]), c - (nb - 1) * case.block_size
+        case.key_cache[last, :, tail:, :] = nan
+        case.value_cache[last, :, tail:, :] = nan
+    unused = [i for i in range(case.key_cache.shape[0]) if i not in used]
+    case.key_cache[unused] = nan
+    case.value_cache[unused] = nan
+    t = h.attention_tensors(case, gpu)
+    exp = h.oracle_attention(case)
+    attn = make_attention(16, 8, 128, 2)
+    for path in (("vector", "mfma") if dtype == "bf16" else ("vector",)):
+        for splits in (1, 2):
+            out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                               t["context_lens"], q_start_loc=t["q_start_loc"], path=path,
+                               num_splits=splits)
+            h.assert_attention_close(out, case, exp, h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
+
+
 # ---------------------------------------------------------------- full-size workloads
 
 
