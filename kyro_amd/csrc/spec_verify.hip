@@ -256,8 +256,10 @@ __device__ __forceinline__ void chunk_stats(const SpecArgs& a, int b, int row, i
 }
 
 // Pass 1a: the rows of the first `win` draft positions (target rows 0 .. win - 1, draft rows
-// 0 .. win - 1), grid (sequence x vocab chunk, row). Rows past a sequence's k, and draft rows
-// of greedy sequences, are never read.
+// 0 .. win - 1), grid (sequence x vocab chunk, row). The chunk is loaded together with the
+// sequence's k and temperature and the row's draft token, so a workgroup makes one round trip;
+// rows past a sequence's k, and draft rows of greedy sequences, are then dropped unreduced (at
+// most 2 win rows of a sequence with k < win are read for nothing).
 template <bool VEC>
 __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     __shared__ float shv[4];
@@ -265,21 +267,25 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     const int c = blockIdx.x % a.C, b = blockIdx.x / a.C;
     const int wt = min(a.win, a.kmax + 1);  // target rows in the window
     const int y = blockIdx.y;
-    const int k = a.num_draft[b];
-    if (k < 0 || k > a.kmax) return;  // reported by the acceptance pass
-    const float T = a.temperature[b];
-    int row;
-    if (y < wt) {
-        if (y > k) return;
-        row = y;
-    } else {
-        const int i = y - wt;
-        if (!(T > 0.f) || i >= k || a.draft == nullptr) return;
-        row = a.kmax + 1 + i;
-    }
-    const uint32_t tok = row_token(a, b, row, k, T);
+    const bool target = y < wt;
+    if (!target && a.draft == nullptr) return;
+    const int pos = target ? y : y - wt;  // draft position of the row
+    const int row = target ? y : a.kmax + 1 + pos;
+    const int v0 = c * a.chunk;
+    const int v1 = min(a.V, v0 + a.chunk);
     float x[kPer];
-    load_strided<VEC>(stats_row_base(a, b, row), c * a.chunk, min(a.V, c * a.chunk + a.chunk), x);
+    load_buffer<VEC>(stats_row_base(a, b, row) + v0, (v1 - v0) * 4, x);
+    const int k = a.num_draft[b];
+    const float T = a.temperature[b];
+    const uint32_t tk = a.kmax > 0 ? a.draft_tokens[(size_t)b * a.kmax + min(pos, a.kmax - 1)] : 0u;
+    if (k < 0 || k > a.kmax) return;  // reported by the acceptance pass
+    if (target ? pos > k : (!(T > 0.f) || pos >= k)) return;
+    const uint32_t tok = (T > 0.f && pos < k) ? tk : 0xFFFFFFFFu;
+    if (v1 - v0 < a.chunk) {  // the row's last chunk, partial: its tail read as zeros
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            if (strided_index<VEC>(v0, i) >= v1) x[i] = kNegInf;
+    }
     chunk_stats<VEC>(a, b, row, c, tok, T, x, shv, shi);
 }
 
