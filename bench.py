@@ -232,9 +232,12 @@ def decode_sample_workload(warmup, steps):
     settings = {
         "greedy": dict(temperature=torch.zeros((b,), device=dev)),
         "plain": {},
-        "top_k_50": dict(top_k=np.full(b, 50, np.int32)),
-        "top_p_0.9": dict(top_p=np.full(b, 0.9, np.float32)),
-        "top_k_50_top_p_0.9": dict(top_k=np.full(b, 50, np.int32), top_p=np.full(b, 0.9, np.float32)),
+        # per-row settings as device tensors, built once: a host array would be copied (and the
+        # host held) inside every timed call
+        "top_k_50": dict(top_k=torch.full((b,), 50, dtype=torch.int32, device=dev)),
+        "top_p_0.9": dict(top_p=torch.full((b,), 0.9, dtype=torch.float32, device=dev)),
+        "top_k_50_top_p_0.9": dict(top_k=torch.full((b,), 50, dtype=torch.int32, device=dev),
+                                   top_p=torch.full((b,), 0.9, dtype=torch.float32, device=dev)),
         "processors_plain": dict(
             bias=[{int(t): 1.0 for t in rng.integers(0, v, size=8)} for _ in range(b)],
             penalty=[kyro_amd.penalty_adds(rng.integers(0, v, size=256), 0.5, 0.2, v) for _ in range(b)],

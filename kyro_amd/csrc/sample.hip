@@ -17,16 +17,24 @@
 //               after top-p, the least probable kept token after top-k alone, the last index
 //               otherwise (worker.rs:340-360).
 //
-// Two kernels:
-//   sample_prepare_kernel  (rows with a processor) copies the row into the workspace with the
-//                          mask applied; many workgroups per row.
-//   sample_row_kernel      one 1024-thread workgroup per row: adds the sparse bias and penalty
-//                          entries, then samples with passes over the row (it stays in L2 / the
-//                          MALL after the first). Top-k and top-p are exact selects in the
-//                          descending order: three radix passes (11 + 11 + 10 bits) over an
-//                          order-preserving key of z build mass histograms in LDS (64-bit fixed
-//                          point, 2^-52 resolution, so the sums do not depend on thread order),
-//                          then a pass in index order settles ties between equal keys.
+// The row is split into 4096-entry chunks so that a batch of a few rows still fills the chip:
+//   sample_prepare_kernel  (rows with a processor; grid chunk x row) copies the row into the
+//                          workspace with the mask, then the bias, then the penalty applied.
+//   sample_stats_kernel    (grid chunk x row) per chunk: {max z, sum exp(z - max z)}, or the first
+//                          maximum at T <= 0; with top-k / top-p also the chunk's non-empty bins
+//                          of the top 11 bits of an order-preserving key of z (counts, and for
+//                          top-p alone exp(z - top of the bin) sums in 2^-20 units).
+//   sample_select_kernel   (one workgroup per row) settles greedy and plain rows: the first
+//                          maximum, or Z, the chunk where the running mass reaches u Z and the
+//                          walk inside it. Top-k / top-p rows get the candidate bins: down to the
+//                          bin holding the k-th token, or the bin holding the top-p crossing.
+//   sample_gather_kernel   (grid chunk x row) appends the candidates to the row's list.
+//   sample_final_kernel    (one workgroup per row) sorts the candidates (key descending, index
+//                          ascending) in LDS, cuts and walks them. Rows whose candidates did not
+//                          fit (or did not settle the cut) run exact radix selects over the whole
+//                          row instead: three passes (11 + 11 + 10 bits) of mass histograms in LDS
+//                          (64-bit fixed point, 2^-52 resolution, so the sums do not depend on
+//                          thread order), then a pass in index order for ties between equal keys.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -36,9 +44,11 @@ namespace {
 constexpr int kRT = 1024;  // threads of the row kernel
 constexpr int kRW = kRT / 64;
 constexpr int kBins = 2048;
-constexpr int kCap = 8192;                   // candidates sorted in LDS
+constexpr int kCap = kSampleCand;            // candidates sorted in LDS
+constexpr int kListCap = kSampleListCap;
 constexpr double kFix = 4503599627370496.0;  // 2^52: fixed-point unit of probability mass
-constexpr double kFixE = 1099511627776.0;    // 2^40: unit of exp(z - max) in the candidate histogram
+constexpr double kFixE = 1099511627776.0;    // 2^40: unit of exp(z - max) in a row's bin masses
+constexpr float kFixC = 1048576.0f;          // 2^20: unit of exp(z - top of the bin) in a chunk's bins
 constexpr float kLog2e = 1.4426950408889634f;
 using u64 = unsigned long long;
 
@@ -334,22 +344,38 @@ __device__ int desc_bin_search(const H* h, u64 theta, bool strict, RowShared& sh
     return d;
 }
 
-// Sorts a[0, n) (n a power of two, at most kCap) into descending order. Whole block.
+// Sorts a[0, n) (n a power of two, at most kCap) into descending order. Whole block. Stages
+// whose pairs lie inside one wave's segment of n / kRW entries run without a block barrier (a
+// wave's LDS accesses are processed in order; the wavefront fence only keeps the compiler from
+// moving them), so only strides of a segment or more pay for __syncthreads.
 __device__ void bitonic_desc(u64* a, int n) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int seg = max(2, n / kRW);  // entries per wave segment (a power of two)
+    auto cswap = [&](int lo, int hi, int size) {
+        const bool desc = (lo & size) == 0;
+        const u64 x = a[lo], y = a[hi];
+        if (desc ? x < y : x > y) {
+            a[lo] = y;
+            a[hi] = x;
+        }
+    };
     for (int size = 2; size <= n; size <<= 1) {
         for (int sb = __builtin_ctz((unsigned)size) - 1; sb >= 0; --sb) {  // stride = 2^sb
             const int stride = 1 << sb;
-            for (int i = threadIdx.x; i < (n >> 1); i += kRT) {
-                const int lo = ((i >> sb) << (sb + 1)) + (i & (stride - 1)), hi = lo + stride;
-                const bool desc = (lo & size) == 0;
-                const u64 x = a[lo], y = a[hi];
-                if (desc ? x < y : x > y) {
-                    a[lo] = y;
-                    a[hi] = x;
-                }
+            if (2 * stride <= seg) {  // wave w: pairs [w seg / 2, (w + 1) seg / 2) = its segment
+                if (wave * seg < n)
+                    for (int p = lane; p < seg / 2; p += 64) {
+                        const int i = wave * (seg / 2) + p;
+                        cswap(((i >> sb) << (sb + 1)) + (i & (stride - 1)), ((i >> sb) << (sb + 1)) + (i & (stride - 1)) + stride, size);
+                    }
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            } else {
+                for (int i = threadIdx.x; i < (n >> 1); i += kRT)
+                    cswap(((i >> sb) << (sb + 1)) + (i & (stride - 1)), ((i >> sb) << (sb + 1)) + (i & (stride - 1)) + stride, size);
+                __syncthreads();
             }
-            __syncthreads();
         }
+        if (2 * size > seg) __syncthreads();  // the next size starts with a block-wide stage
     }
 }
 
@@ -395,71 +421,451 @@ __device__ __forceinline__ bool row_has_proc(const SampleArgs& a, int b) {
            (a.mask_row && a.mask_row[b] >= 0);
 }
 
-// Copies rows that have a processor into the workspace, adding -inf where the mask disallows.
-__global__ __launch_bounds__(256) void sample_prepare_kernel(SampleArgs a) {
-    const int b = blockIdx.y;
+__device__ __forceinline__ const float* row_ptr(const SampleArgs& a, int b) {
+    return (row_has_proc(a, b) ? a.ws : a.logits) + (size_t)b * a.V;
+}
+
+// ------------------------------------------------------------------ chunked passes (kCT threads)
+
+constexpr int kChunk = kSampleChunk;  // vocabulary entries per workgroup of a chunked pass
+constexpr int kCT = 256;             // threads of a chunked pass
+constexpr int kCW = kCT / 64;
+constexpr int kCPer = kChunk / kCT;  // entries per thread
+
+// Index of entry i of this thread in chunk [v0, v0 + kChunk), strided layout: consecutive threads
+// take consecutive 16-byte vectors (floats when the row is not 16-byte aligned).
+__device__ __forceinline__ int chunk_index(int v0, int i, bool vec4) {
+    return vec4 ? v0 + ((i >> 2) * kCT + (int)threadIdx.x) * 4 + (i & 3) : v0 + i * kCT + (int)threadIdx.x;
+}
+
+// Loads chunk [v0, v1) of row y in the strided layout; positions past v1 get -inf.
+__device__ __forceinline__ void load_chunk(const float* y, int v0, int v1, bool vec4, float (&x)[kCPer]) {
+    const float ninf = -__builtin_huge_valf();
+    if (vec4) {
+#pragma unroll
+        for (int it = 0; it < kCPer / 4; ++it) {
+            const int v = chunk_index(v0, it * 4, true);
+            float4 f = make_float4(ninf, ninf, ninf, ninf);
+            if (v < v1) f = *reinterpret_cast<const float4*>(y + v);
+            x[it * 4 + 0] = f.x;
+            x[it * 4 + 1] = f.y;
+            x[it * 4 + 2] = f.z;
+            x[it * 4 + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i) {
+            const int v = chunk_index(v0, i, false);
+            x[i] = v < v1 ? y[v] : ninf;
+        }
+    }
+}
+
+__device__ __forceinline__ float cblock_max(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int w = 1; w < kCW; ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float cblock_sum(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int w = 0; w < kCW; ++w) r += red[w];
+    __syncthreads();
+    return r;
+}
+
+// Largest float value whose order_key falls in histogram bin `bin` (the top 11 key bits).
+__device__ __forceinline__ float bin_top(int bin) { return key_value(((uint32_t)bin << 21) | 0x1FFFFFu); }
+
+// Copies rows that have a processor into the workspace: the mask (-inf where disallowed), then
+// the bias entries, then the penalty entries (worker.rs:142-181; the entries of one list name
+// distinct tokens). Grid (chunk, row).
+__global__ __launch_bounds__(kCT) void sample_prepare_kernel(SampleArgs a) {
+    __shared__ float s_row[kChunk];
+    const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     if (!row_has_proc(a, b)) return;
     const float* x = a.logits + (size_t)b * a.V;
     float* y = a.ws + (size_t)b * a.V;
     const int mr = a.mask_row ? a.mask_row[b] : -1;
     const uint32_t* mask = (mr >= 0 && mr < a.num_masks) ? a.mask + (size_t)mr * a.mask_words : nullptr;
-    if (a.mask_row && mr >= a.num_masks) {
-        if (blockIdx.x == 0 && threadIdx.x == 0) latch_error(a.err, ERR_TOKEN);
-    }
-    const int v0 = blockIdx.x * 4096;
-    for (int v = v0 + threadIdx.x; v < min(a.V, v0 + 4096); v += 256) {
+    if (a.mask_row && mr >= a.num_masks && c == 0 && tid == 0) latch_error(a.err, ERR_TOKEN);
+    const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
+    for (int v = v0 + tid; v < v1; v += kCT) {
         float g = 0.0f;
         if (mask && !((mask[v >> 5] >> (v & 31)) & 1u)) g = -__builtin_huge_valf();
-        y[v] = x[v] + g;
+        s_row[v - v0] = x[v] + g;
+    }
+    __syncthreads();
+    auto apply = [&](const int32_t* off, const uint32_t* tok, const float* val) {
+        for (int i = off[b] + tid; i < off[b + 1]; i += kCT) {
+            const uint32_t t = tok[i];
+            if (t >= (uint32_t)v0 && t < (uint32_t)v1) s_row[t - v0] = s_row[t - v0] + val[i];
+            else if (t >= (uint32_t)a.V && c == 0) latch_error(a.err, ERR_TOKEN);
+        }
+        __syncthreads();
+    };
+    if (a.bias_off) apply(a.bias_off, a.bias_tok, a.bias_val);
+    if (a.pen_off) apply(a.pen_off, a.pen_tok, a.pen_val);
+    for (int v = v0 + tid; v < v1; v += kCT) y[v] = s_row[v - v0];
+}
+
+// Pass 1, grid (chunk, row): per chunk of the processed row, {max z, sum exp(z - max z)} with
+// z = y * f32(1 / T) + 0, or {max y, its first index} for T <= 0. Rows with top-k or top-p also
+// report the chunk's non-empty bins of the top 11 bits of order_key(z): a count and, for top-p
+// alone, the sum of exp(z - bin_top) in 2^-20 units (relative to a fixed value of the bin, so
+// chunks add up without knowing the row's max; 32-bit sums keep the pass at 16 KiB of LDS).
+// These masses only choose the candidate bins: the cut itself is taken on the candidates.
+__global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
+    __shared__ uint32_t s_cnt[kBins];
+    __shared__ uint32_t s_mass[kBins];
+    __shared__ float s_red[kCW];
+    __shared__ int s_ired[kCW];
+    __shared__ uint32_t s_wn[kCW];
+    const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* y = row_ptr(a, b);
+    const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
+    const bool vec4 = a.vec4;
+    float x[kCPer];
+    load_chunk(y, v0, v1, vec4, x);
+    const float T = a.temperature[b];
+    const int k = a.top_k ? a.top_k[b] : 0;  // issued with the chunk's loads
+    const float tp = a.top_p ? a.top_p[b] : 1.0f;
+    float2* out = a.cstat + (size_t)b * a.C + c;
+    if (!(T > 0.f)) {  // first maximum of y (entries of a thread ascend in index)
+        float bv = -__builtin_huge_valf();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i) {
+            const int v = chunk_index(v0, i, vec4);
+            if (v < v1 && x[i] > bv) {
+                bv = x[i];
+                bi = v;
+            }
+        }
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            s_red[wave] = bv;
+            s_ired[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < kCW; ++w)
+                if (s_red[w] > bv || (s_red[w] == bv && s_ired[w] < bi)) {
+                    bv = s_red[w];
+                    bi = s_ired[w];
+                }
+            *out = make_float2(bv, __int_as_float(bi));
+        }
+        return;
+    }
+    const float sc = (float)(1.0 / (double)T);
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < kCPer; ++i) {
+        x[i] = x[i] * sc + 0.0f;
+        m = fmaxf(m, x[i]);
+    }
+    m = cblock_max(m, s_red);
+    float sum = 0.f;
+    if (m != -__builtin_huge_valf()) {
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i) sum += fast_exp2((x[i] - m) * kLog2e);
+    }
+    sum = cblock_sum(sum, s_red);
+    if (tid == 0) *out = make_float2(m, sum);
+
+    const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
+    if (!use_k && !use_p) return;
+    const bool mass = !use_k;  // top-p alone locates its cut by mass, top-k by count
+    for (int i = tid; i < kBins; i += kCT) {
+        s_cnt[i] = 0;
+        s_mass[i] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kCPer; ++i) {
+        if (chunk_index(v0, i, vec4) >= v1) continue;
+        const int bin = (int)(order_key(x[i]) >> 21);
+        atomicAdd(&s_cnt[bin], 1u);
+        if (mass) {
+            const float e = fast_exp2((x[i] - bin_top(bin)) * kLog2e);
+            if (e > 0.f && e <= 1.f) {  // at most 4096 * 2^20 per bin: fits 32 bits
+                const uint32_t f = (uint32_t)__float2uint_rn(e * kFixC);
+                if (f) atomicAdd(&s_mass[bin], f);
+            }
+        }
+    }
+    __syncthreads();
+    // The non-empty bins in bin order: thread t owns bins 8t .. 8t+7.
+    constexpr int kPerT = kBins / kCT;
+    uint32_t nz = 0;
+#pragma unroll
+    for (int j = 0; j < kPerT; ++j) nz += s_cnt[tid * kPerT + j] ? 1u : 0u;
+    uint32_t incl = nz;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) s_wn[wave] = incl;
+    __syncthreads();
+    uint32_t pos = incl - nz, total = 0;
+    for (int w = 0; w < kCW; ++w) {
+        if (w < wave) pos += s_wn[w];
+        total += s_wn[w];
+    }
+    int* n_out = a.clist_n + (size_t)b * a.C + c;
+    if (total > (uint32_t)kListCap) {  // more distinct bins than a chunk may report
+        if (tid == 0) *n_out = -1;
+        return;
+    }
+    SampleBin* list = a.clist + ((size_t)b * a.C + c) * kListCap;
+#pragma unroll
+    for (int j = 0; j < kPerT; ++j) {
+        const int bin = tid * kPerT + j;
+        if (s_cnt[bin]) {
+            list[pos] = SampleBin{(uint32_t)bin, s_cnt[bin], s_mass[bin]};
+            ++pos;
+        }
+    }
+    if (tid == 0) *n_out = (int)total;
+}
+
+// Pass 2, one workgroup per row: merges the chunk statistics. T <= 0: the first maximum. Plain
+// sampling: Z, the chunk where the running mass in index order reaches u Z, and the walk inside
+// it (worker.rs:352-360). Top-k / top-p: the row histogram, the candidate bins (down to the bin
+// holding the k-th token, or the bin holding the top-p crossing), and the row's plan for the
+// gather and final passes.
+__global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
+    __shared__ RowShared sh;
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int C = a.C;
+    const float T = a.temperature[b];
+    SamplePlan* plan = a.plan + b;
+    const float2 st = tid < C ? a.cstat[(size_t)b * C + tid] : make_float2(-__builtin_huge_valf(), 0.f);
+    // Bin-list lengths, loaded with the statistics (used by top-k / top-p rows only).
+    const int listn = (a.clist_n && tid < C) ? a.clist_n[(size_t)b * C + tid] : 0;
+    if (!(T > 0.f)) {
+        const int best = block_argmax(st.x, tid < C ? __float_as_int(st.y) : 0x7fffffff, sh);
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(best == 0x7fffffff ? 0 : best);
+            plan->mode = SAMPLE_DONE;
+        }
+        return;
+    }
+    const float M = block_max_f(st.x, sh);
+    if (M == -__builtin_huge_valf()) {  // every token disallowed
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(a.V - 1);
+            plan->mode = SAMPLE_DONE;
+        }
+        return;
+    }
+    // Chunk masses exp(z - M) in chunk order: thread t holds chunk t; inclusive scan gives Z.
+    const float w = (tid < C && st.x != -__builtin_huge_valf()) ? st.y * fast_exp2((st.x - M) * kLog2e) : 0.f;
+    const float winc = wave_incl_scan_f(w);
+    if (lane == 63) sh.fred[wave] = winc;
+    __syncthreads();
+    float cbase = 0.f, Z = 0.f;
+    for (int q = 0; q < kRW; ++q) {
+        if (q < wave) cbase += sh.fred[q];
+        Z += sh.fred[q];
+    }
+    const float cum = cbase + winc;  // running mass through chunk tid
+    __syncthreads();
+    const int k = a.top_k ? a.top_k[b] : 0;
+    const float tp = a.top_p ? a.top_p[b] : 1.0f;
+    const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
+    const float sc = (float)(1.0 / (double)T);
+    if (!use_k && !use_p) {
+        const float rr = a.u[b] * Z;
+        if (tid == 0) sh.found = 0x7fffffff;
+        __syncthreads();
+        if (tid < C && cum >= rr && (tid == 0 || cum - w < rr)) atomicMin(&sh.found, tid);
+        __syncthreads();
+        const int cs = sh.found == 0x7fffffff ? C - 1 : sh.found;
+        __syncthreads();
+        if (tid == cs) sh.fred[0] = cum - w;  // mass before the crossing chunk
+        __syncthreads();
+        const float rem = rr - sh.fred[0];
+        // Walk chunk cs in index order: thread t owns the 4 consecutive entries 4t .. 4t+3.
+        const float* y = row_ptr(a, b);
+        const int v0 = cs * kChunk, v1 = min(a.V, v0 + kChunk);
+        const int v = v0 + 4 * tid;
+        float e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = v + j < v1 ? fast_exp2((y[v + j] * sc + 0.0f - M) * kLog2e) : 0.f;
+        const float mine = (e[0] + e[1]) + (e[2] + e[3]);
+        const float inc = wave_incl_scan_f(mine);
+        if (lane == 63) sh.fred[wave] = inc;
+        __syncthreads();
+        float base = inc - mine;
+        for (int q = 0; q < wave; ++q) base += sh.fred[q];
+        if (tid == 0) sh.found = 0x7fffffff;
+        __syncthreads();
+        if (v < v1 && base < rem && base + mine >= rem) {  // this thread's four hold the crossing
+            float run = base;
+            int pick = -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                run += e[j];
+                if (pick < 0 && v + j < v1 && run >= rem) pick = v + j;
+            }
+            atomicMin(&sh.found, pick >= 0 ? pick : min(v + 3, v1 - 1));  // rounding can make two threads claim it
+        } else if (tid == 0 && rem <= 0.f) {
+            atomicMin(&sh.found, v0);
+        }
+        __syncthreads();
+        if (tid == 0 && sh.found == 0x7fffffff) sh.found = -1;
+        __syncthreads();
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(sh.found >= 0 ? sh.found : a.V - 1);
+            plan->mode = SAMPLE_DONE;
+        }
+        return;
+    }
+    // Row histogram from the chunks' bin lists; masses are converted to exp(z - M) units per bin.
+    for (int i = tid; i < kBins; i += kRT) {
+        sh.cnt[i] = 0;
+        sh.hist[i] = 0;
+    }
+    if (tid == 0) sh.count = 0;
+    // Wave w merges the lists of chunks w, w + 16, ...
+    int* s_n = reinterpret_cast<int*>(sh.cum);
+    if (tid < C) {
+        s_n[tid] = listn;
+        if (listn < 0) sh.count = 1;  // a chunk overflowed its list
+    }
+    __syncthreads();
+    for (int c = wave; c < C; c += kRW) {
+        const int n = s_n[c];
+        const SampleBin* list = a.clist + ((size_t)b * C + c) * kListCap;
+        for (int j = lane; j < n; j += 64) {
+            const SampleBin e = list[j];
+            atomicAdd(&sh.cnt[e.bin], e.count);
+            if (e.mass) atomicAdd(&sh.hist[e.bin], (u64)e.mass);
+        }
+    }
+    __syncthreads();
+    const bool overflow = sh.count != 0;
+    const bool mass = !use_k;
+    if (mass) {  // to exp(z - M) in 2^-40 units
+        for (int i = tid; i < kBins; i += kRT)
+            if (sh.hist[i]) {
+                const float f = fast_exp2((bin_top(i) - M) * kLog2e);
+                sh.hist[i] = (u64)llrint((double)sh.hist[i] * (double)f * (kFixE / (double)kFixC));
+            }
+        __syncthreads();
+    }
+    int tb;
+    if (use_k) {
+        tb = desc_bin_search(sh.cnt, (u64)k, false, sh);
+    } else {
+        u64 tot = 0;
+        for (int i = lane; i < kBins; i += 64) tot += sh.hist[i];
+        tot = wave_sum_u64(tot);
+        // The bin holding the crossing. Its mass is rounded differently from the candidates'
+        // own sums: should the exact cut fall below it, the final pass finds no cut among the
+        // candidates and runs the radix path.
+        tb = desc_bin_search(sh.hist, (u64)llrint((double)tp * (double)tot), true, sh);
+    }
+    u64 ncand = ~0ull;
+    if (tb >= 0) {
+        u64 cn = 0;
+        for (int i = tb + lane; i < kBins; i += 64) cn += sh.cnt[i];
+        ncand = wave_sum_u64(cn);
+    }
+    if (tid == 0) {
+        SamplePlan pl;
+        pl.mode = (overflow || tb < 0 || ncand > (u64)kCap) ? SAMPLE_RADIX : SAMPLE_CAND;
+        pl.tb = tb;
+        pl.m = M;
+        pl.z = Z;
+        pl.ncand = (int)(ncand > (u64)kCap ? kCap + 1 : ncand);
+        pl.count = 0;
+        *plan = pl;
     }
 }
 
-__global__ __launch_bounds__(kRT) void sample_row_kernel(SampleArgs a) {
+// Pass 3, grid (chunk, row): rows on the candidate path append their tokens in the candidate
+// bins to the row's list (one atomic per workgroup; the list's order is settled by the sort).
+__global__ __launch_bounds__(kCT) void sample_gather_kernel(SampleArgs a) {
+    __shared__ uint32_t s_wn[kCW];
+    __shared__ int s_base;
+    const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float* y = row_ptr(a, b);
+    const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
+    const bool vec4 = a.vec4;
+    float x[kCPer];
+    load_chunk(y, v0, v1, vec4, x);  // issued with the plan's load; dropped when not needed
+    SamplePlan* plan = a.plan + b;
+    if (plan->mode != SAMPLE_CAND) return;
+    const uint32_t tb = (uint32_t)plan->tb;
+    const float sc = (float)(1.0 / (double)a.temperature[b]);
+    uint32_t keys[kCPer];
+    uint32_t hits = 0;  // bit i: entry i is a candidate
+#pragma unroll
+    for (int i = 0; i < kCPer; ++i) {
+        keys[i] = order_key(x[i] * sc + 0.0f);
+        if (chunk_index(v0, i, vec4) < v1 && (keys[i] >> 21) >= tb) hits |= 1u << i;
+    }
+    // One atomic per workgroup: a block scan of the per-thread counts places every candidate.
+    const uint32_t mine = (uint32_t)__popc(hits);
+    uint32_t incl = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    if (lane == 63) s_wn[wave] = incl;
+    __syncthreads();
+    uint32_t off = incl - mine, total = 0;
+    for (int w = 0; w < kCW; ++w) {
+        if (w < wave) off += s_wn[w];
+        total += s_wn[w];
+    }
+    if (total == 0) return;
+    if (threadIdx.x == 0) s_base = atomicAdd(&plan->count, (int)total);
+    __syncthreads();
+    u64* cand = a.cand + (size_t)b * kCap;
+    int slot = s_base + (int)off;
+#pragma unroll
+    for (int i = 0; i < kCPer; ++i)
+        if (hits & (1u << i)) {
+            if (slot < kCap) cand[slot] = ((u64)keys[i] << 32) | (uint32_t)~(uint32_t)chunk_index(v0, i, vec4);
+            ++slot;
+        }
+}
+
+// Pass 4, one workgroup per row on the candidate or radix path: sorts the candidates (key
+// descending, index ascending), applies top-k / top-p in that order and walks the kept set; rows
+// whose candidates do not settle the cut run exact radix selects over the whole row.
+__global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
     __shared__ RowShared sh;
     const int b = blockIdx.x, tid = threadIdx.x;
+    const SamplePlan pl = a.plan[b];
+    if (pl.mode == SAMPLE_DONE) return;
     const int V = a.V;
-    const bool proc = row_has_proc(a, b);
-    const float* y = proc ? a.ws + (size_t)b * V : a.logits + (size_t)b * V;
-    if (proc) {
-        // Bias first, then penalty (worker.rs:142-181). Entries of one list have distinct tokens.
-        float* w = a.ws + (size_t)b * V;
-        if (a.bias_off) {
-            for (int i = a.bias_off[b] + tid; i < a.bias_off[b + 1]; i += kRT) {
-                const uint32_t t = a.bias_tok[i];
-                if (t < (uint32_t)V) w[t] = w[t] + a.bias_val[i];
-                else latch_error(a.err, ERR_TOKEN);
-            }
-            __syncthreads();
-        }
-        if (a.pen_off) {
-            for (int i = a.pen_off[b] + tid; i < a.pen_off[b + 1]; i += kRT) {
-                const uint32_t t = a.pen_tok[i];
-                if (t < (uint32_t)V) w[t] = w[t] + a.pen_val[i];
-                else latch_error(a.err, ERR_TOKEN);
-            }
-        }
-        __syncthreads();
-    }
     const float T = a.temperature[b];
-    const bool vec4 = a.vec4;
-    if (!(T > 0.f)) {  // argmax of the processed logits
-        float bv = -__builtin_huge_valf();
-        int bi = 0x7fffffff;
-        row_for_each(y, V, vec4, [&](int v, float x) {
-            if (x > bv) {
-                bv = x;
-                bi = v;
-            }
-        });
-        const int best = block_argmax(bv, bi, sh);
-        if (tid == 0) a.out[b] = (uint32_t)(best == 0x7fffffff ? 0 : best);
-        return;
-    }
     Row r;
-    r.y = y;
+    r.y = row_ptr(a, b);
     r.V = V;
-    r.vec4 = vec4;
+    r.vec4 = a.vec4;
     r.s = (float)(1.0 / (double)T);
+    r.m = pl.m;
+    r.z_sum = pl.z;
     r.kk = 0;
     r.ki = V;
     r.ck = 0;
@@ -469,143 +875,12 @@ __global__ __launch_bounds__(kRT) void sample_row_kernel(SampleArgs a) {
     const bool use_k = k > 0 && k < V;
     const bool use_p = tp < 1.0f;
     const float u = a.u[b];
-    const int lane = tid & 63, wave = tid >> 6;
-    if (!use_k && !use_p) {
-        float mx = -__builtin_huge_valf();
-        row_for_each(y, V, vec4, [&](int, float yv) { mx = fmaxf(mx, yv * r.s + 0.0f); });
-        r.m = block_max_f(mx, sh);
-        if (r.m == -__builtin_huge_valf()) {  // every token disallowed
-            if (tid == 0) a.out[b] = (uint32_t)(V - 1);
-            return;
-        }
-        // Index order: wave w owns the contiguous chunk [w L, w L + L) (L a multiple of 256).
-        // The chunk sums of exp(z - max) give the total and the crossing chunk; that wave then
-        // walks its chunk 256 entries at a time (4 consecutive per lane).
-        const int L = ((V + kRW - 1) / kRW + 255) & ~255;
-        const int c0 = min(V, wave * L), c1 = min(V, c0 + L);
-        auto ev = [&](int v) { return v < c1 ? r.e(y[v] * r.s + 0.0f) : 0.f; };
-        // Four consecutive entries of lane l in tile t0: one 16-byte load when the row allows.
-        auto ev4 = [&](int v, float& e0, float& e1, float& e2, float& e3) {
-            if (vec4 && v + 3 < c1) {
-                const float4 q = *reinterpret_cast<const float4*>(y + v);
-                e0 = r.e(q.x * r.s + 0.0f);
-                e1 = r.e(q.y * r.s + 0.0f);
-                e2 = r.e(q.z * r.s + 0.0f);
-                e3 = r.e(q.w * r.s + 0.0f);
-            } else {
-                e0 = ev(v);
-                e1 = ev(v + 1);
-                e2 = ev(v + 2);
-                e3 = ev(v + 3);
-            }
-        };
-        float part = 0.f;
-#pragma unroll 4
-        for (int t0 = c0; t0 < c1; t0 += 256) {
-            float e0, e1, e2, e3;
-            ev4(t0 + 4 * lane, e0, e1, e2, e3);
-            part += (e0 + e1) + (e2 + e3);
-        }
-        part = wave_sum(part);
-        if (lane == 0) sh.fred[wave] = part;
-        if (tid == 0) sh.found = -1;
-        __syncthreads();
-        float zsum = 0.f, wb = 0.f;
-        for (int w = 0; w < kRW; ++w) {
-            if (w == wave) wb = zsum;
-            zsum += sh.fred[w];
-        }
-        const float rr = u * zsum;  // r = u in probability; compare running sums of exp(z - max)
-        const bool my_wave = (wave == 0 && rr <= 0.f) ||
-                             (wb < rr && (wb + sh.fred[wave] >= rr || wave == kRW - 1));
-        if (my_wave) {
-            for (int t0 = c0; t0 < c1; t0 += 256) {
-                const int v = t0 + 4 * lane;
-                float e0, e1, e2, e3;
-                ev4(v, e0, e1, e2, e3);
-                const float mine = (e0 + e1) + (e2 + e3);
-                const float in = wb + wave_incl_scan_f(mine);
-                const unsigned long long bal = __ballot(in >= rr);
-                if (bal) {
-                    const int l = __ffsll((long long)bal) - 1;
-                    if (lane == l) {  // the lane's four entries in order
-                        const float c0r = in - mine + e0, c1r = c0r + e1, c2r = c1r + e2;
-                        int pick = min(v + 3, c1 - 1);
-                        if (c2r >= rr) pick = v + 2;
-                        if (c1r >= rr) pick = v + 1;
-                        if (c0r >= rr) pick = v;
-                        sh.found = pick;
-                    }
-                    break;
-                }
-                wb = __shfl(in, 63, 64);
-            }
-        }
-        __syncthreads();
-        if (tid == 0) a.out[b] = (uint32_t)(sh.found >= 0 ? sh.found : V - 1);
-        return;
-    }
-
-    // Filtered: max and the histogram of the top 11 key bits.
-    for (int i = tid; i < kBins; i += kRT) {
-        sh.cnt[i] = 0;
-        sh.hist[i] = 0;
-    }
-    __syncthreads();
-    {
-        float mx = -__builtin_huge_valf();
-        row_for_each(y, V, vec4, [&](int, float yv) {
-            const float zv = yv * r.s + 0.0f;
-            mx = fmaxf(mx, zv);
-            atomicAdd(&sh.cnt[order_key(zv) >> 21], 1u);
-        });
-        r.m = block_max_f(mx, sh);
-    }
-    if (r.m == -__builtin_huge_valf()) {
-        if (tid == 0) a.out[b] = (uint32_t)(V - 1);
-        return;
-    }
-    // Candidate bins: from the top down to the bin holding the k-th token (top-k), or one bin
-    // below the bin where the running mass of exp(z - max) passes top_p (top-p alone).
-    int tb;
-    if (use_k) {
-        tb = desc_bin_search(sh.cnt, (u64)k, false, sh);
-    } else {
-        float zs = 0.f;
-        row_for_each(y, V, vec4, [&](int, float yv) {
-            const float zv = yv * r.s + 0.0f;
-            const float e = r.e(zv);
-            zs += e;
-            atomicAdd(&sh.hist[order_key(zv) >> 21], (u64)llrint((double)e * kFixE));
-        });
-        r.z_sum = block_sum_f(zs, sh);
-        u64 tot = 0;
-        for (int i = lane; i < kBins; i += 64) tot += sh.hist[i];
-        tot = wave_sum_u64(tot);
-        tb = desc_bin_search(sh.hist, (u64)llrint((double)tp * (double)tot), true, sh);
-        tb = tb > 0 ? tb - 1 : 0;
-    }
-    uint32_t ncand = 0xffffffffu;  // candidates: tokens in bins tb and above (every wave sums all bins)
-    if (tb >= 0) {
-        u64 c = 0;
-        for (int i = tb + lane; i < kBins; i += 64) c += sh.cnt[i];
-        ncand = (uint32_t)wave_sum_u64(c);
-    }
-    if (tb >= 0 && ncand <= (uint32_t)kCap) {
-        if (tid == 0) sh.count = 0;
-        __syncthreads();
-        row_for_each(y, V, vec4, [&](int v, float yv) {
-            const uint32_t key = order_key(yv * r.s + 0.0f);
-            if ((int)(key >> 21) >= tb) {
-                const int slot = atomicAdd(&sh.count, 1);
-                sh.cand[slot] = ((u64)key << 32) | (uint32_t)~(uint32_t)v;
-            }
-        });
-        __syncthreads();
-        const int n = sh.count;
+    if (pl.mode == SAMPLE_CAND) {
+        const int n = min(pl.count, kCap);
         int np2 = 2;
         while (np2 < n) np2 <<= 1;
-        for (int i = n + tid; i < np2; i += kRT) sh.cand[i] = 0;
+        const u64* cand = a.cand + (size_t)b * kCap;
+        for (int i = tid; i < np2; i += kRT) sh.cand[i] = i < n ? cand[i] : 0;
         __syncthreads();
         bitonic_desc(sh.cand, np2);
         const int ns = use_k ? min(k, n) : n;
@@ -635,7 +910,7 @@ __global__ __launch_bounds__(kRT) void sample_row_kernel(SampleArgs a) {
             return;
         }
     }
-    // Radix selects over the whole row (candidates did not fit in LDS).
+    // Radix selects over the whole row (candidates did not fit in LDS, or did not settle the cut).
     auto all = [](uint32_t, int) { return true; };
     auto one = [](float) -> u64 { return 1; };
     if (use_k) {  // the k-th token in descending order bounds the kept set
@@ -648,7 +923,7 @@ __global__ __launch_bounds__(kRT) void sample_row_kernel(SampleArgs a) {
     }
     {
         float zs = 0.f;
-        row_for_each(y, V, vec4, [&](int v, float yv) {
+        row_for_each(r.y, V, r.vec4, [&](int v, float yv) {
             const float zv = yv * r.s + 0.0f;
             if (r.kept(order_key(zv), v)) zs += r.e(zv);
         });
@@ -694,11 +969,14 @@ __global__ __launch_bounds__(kRT) void sample_row_kernel(SampleArgs a) {
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
-    if (a.bias_off || a.pen_off || a.mask_row) {
-        const dim3 grid((unsigned)((a.V + 4095) / 4096), (unsigned)a.B);
-        sample_prepare_kernel<<<grid, 256, 0, stream>>>(a);
+    const dim3 grid((unsigned)a.C, (unsigned)a.B);
+    if (a.bias_off || a.pen_off || a.mask_row) sample_prepare_kernel<<<grid, kCT, 0, stream>>>(a);
+    sample_stats_kernel<<<grid, kCT, 0, stream>>>(a);
+    sample_select_kernel<<<dim3((unsigned)a.B), kRT, 0, stream>>>(a);
+    if (a.top_k || a.top_p) {
+        sample_gather_kernel<<<grid, kCT, 0, stream>>>(a);
+        sample_final_kernel<<<dim3((unsigned)a.B), kRT, 0, stream>>>(a);
     }
-    sample_row_kernel<<<dim3((unsigned)a.B), kRT, 0, stream>>>(a);
     return hipGetLastError();
 }
 

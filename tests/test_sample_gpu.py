@@ -67,6 +67,19 @@ def test_ties_follow_the_index(gpu):
     run_both(x, np.zeros(B, np.float32), u, gpu)
 
 
+def test_wide_dynamic_range(gpu):
+    """Logits spread over 2^-60 .. 2^60 in magnitude: a 4096-entry chunk then spans more distinct
+    key bins than its list holds, so top-k and top-p rows take the exact radix path."""
+    rng = np.random.default_rng(17)
+    B, V = 12, 32000
+    x = (rng.choice([-1.0, 1.0], size=(B, V)) * np.exp2(rng.uniform(-60, 60, size=(B, V)))).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    T = np.full(B, 1.0, np.float32)
+    run_both(x, T, u, gpu, top_k=rng.choice([1, 5, 300], size=B).astype(np.int32))
+    run_both(x, T, u, gpu, top_p=rng.choice([0.3, 0.9], size=B).astype(np.float32))
+    run_both(x, T, u, gpu)
+
+
 def test_processors(gpu):
     rng = np.random.default_rng(8)
     B, V = 16, 5000
