@@ -136,6 +136,24 @@ def _median_us(fn, warmup, steps):
     return float(np.median([e0.elapsed_time(e1) for e0, e1 in ev])) * 1e3
 
 
+def _roofline(nbytes, us, bound="hbm"):
+    """Roofline entry for one kernel chain on its algorithmic bytes (bound "hbm": 8 TB/s peak)."""
+    achieved = nbytes / us / 1e3
+    return {"bound": bound, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBS}
+
+
+def _cpu_seconds(fn, min_seconds=0.5):
+    """Seconds per call of fn() on the host, repeated until min_seconds have passed."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        t = time.perf_counter() - t0
+        if t >= min_seconds:
+            return t / n
+
+
 def kv_append_workload(warmup, steps):
     """One JSON line for the paged KV write (kyro_paged_kv_append): the verify step's 8 new rows per
     sequence of the Llama-3-8B workload, and a prefill of 4 x 2048 f32 rows into a bf16 cache.
@@ -164,8 +182,33 @@ def kv_append_workload(warmup, steps):
         us = _median_us(lambda: kv.append_kv_async(k, v, kc, vc, table, ctx_t, q_start_loc=qs, max_q_len=q),
                         warmup, steps)
         nbytes = 2 * b * q * HKV * D * (k.element_size() + 2)
-        res[label] = {"us": us, "algorithmic_bytes": nbytes, "GB_s": nbytes / us / 1e3, "rows": b * q}
+        res[label] = {"us": us, "algorithmic_bytes": nbytes, "GB_s": nbytes / us / 1e3, "rows": b * q,
+                      "roofline": _roofline(nbytes, us)}
+    res["cpu_baseline"] = _kv_append_cpu()
     print(json.dumps(res), flush=True)
+
+
+def _kv_append_cpu():
+    """The oracle's KV append (C, one thread) on 8 of the verify batch's sequences: 8 new bf16
+    rows each into a bf16 cache of their own blocks."""
+    import numpy as np
+
+    import oracle
+
+    n, q, ctx = 8, K_DRAFT + 1, CTX
+    mb = (ctx + BS - 1) // BS
+    rng = np.random.default_rng(0)
+    kc = np.zeros((n * mb, HKV, BS, D), np.uint16)
+    vc = np.zeros_like(kc)
+    table = rng.permutation(n * mb).reshape(n, mb).astype(np.int64)
+    k = rng.integers(0, 1 << 15, size=(n * q, HKV, D)).astype(np.uint16)
+    v = rng.integers(0, 1 << 15, size=(n * q, HKV, D)).astype(np.uint16)
+    ctx_a = np.full(n, ctx, np.int64)
+    qs = np.arange(0, (n + 1) * q, q).astype(np.int32)
+    sec = _cpu_seconds(lambda: oracle.kv_append(k, v, kc, vc, table, ctx_a, block_size=BS, q_start_loc=qs))
+    nbytes = 2 * n * q * HKV * D * 4
+    return {"value": nbytes / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} sequences x {q} bf16 rows of the verify step, oracle_kv_append"}
 
 
 def block_tables_workload(warmup, steps):
@@ -205,7 +248,11 @@ def block_tables_workload(warmup, steps):
         "cached_tokens_per_request": 1000,
         "write_tables": {"us": write_us, "bytes": int(table.numel() * 8 + B * 8)},
         "copy_blocks": {"us": copy_us, "pairs": len(copies), "bytes": 2 * 2 * slab * len(copies),
-                        "GB_s": 2 * 2 * slab * len(copies) / copy_us / 1e3},
+                        "GB_s": 2 * 2 * slab * len(copies) / copy_us / 1e3,
+                        "roofline": _roofline(2 * 2 * slab * len(copies) * 2, copy_us)},
+        "cpu_baseline": {"value": float(np.median(times)), "unit": "us per request", "cores": 1,
+                         "kind": "port", "sample": "allocate_with_prefix is host code in the "
+                         "reference and here alike; this is its time per request"},
     }), flush=True)
 
 
@@ -251,7 +298,19 @@ def decode_sample_workload(warmup, steps):
             kw = {"processors": kyro_amd.sampling.Processors(b, v, dev, **kw)}
         out = torch.empty(b, dtype=torch.int32, device=dev)
         us = _median_us(lambda: kyro_amd.sample_tokens_async(x, temp, u, out=out, **kw), warmup, steps)
-        res[name] = {"us": us, "GB_s": nbytes / us / 1e3}
+        res[name] = {"us": us, "GB_s": nbytes / us / 1e3, "roofline": _roofline(nbytes, us)}
+    # CPU: the oracle's decode step (C, f32 build, one thread) on 4 of the rows
+    import oracle
+
+    xs = x[:4].cpu().numpy()
+    us_np, T_np = u[:4].cpu().numpy(), T[:4].cpu().numpy()
+    cpu = {}
+    for name, kw in (("plain", {}), ("top_p_0.9", {"top_p": np.full(4, 0.9, np.float32)})):
+        sec = _cpu_seconds(lambda: oracle.sample_decode(xs, T_np, us_np, precision="f32", **kw))
+        cpu[name] = {"value": 4 / sec, "unit": "tok/s"}
+    res["cpu_baseline"] = {"value": cpu["plain"]["value"], "unit": "tok/s", "cores": 1, "kind": "port",
+                           "sample": "4 rows of V 128256, oracle_sample_decode (f32), plain; top-p 0.9: "
+                                     f"{cpu['top_p_0.9']['value']:.0f} tok/s"}
     print(json.dumps(res), flush=True)
 
 
@@ -275,9 +334,19 @@ def ngram_draft_workload(warmup, steps):
     toks = torch.empty((B, K_DRAFT), dtype=torch.int32, device=dev)
     nd = torch.empty((B,), dtype=torch.int32, device=dev)
     us = _median_us(lambda: table.draft(tail, lens, K_DRAFT, out=(toks, nd)), warmup, steps)
+    # CPU: the oracle's dict table (built outside the timing) drafting for the same 64 contexts
+    import oracle
+
+    ref = oracle.ngram_build(corpus, 3)
+    sec = _cpu_seconds(lambda: [oracle.ngram_draft(ref, c, 3, K_DRAFT) for c in contexts])
     print(json.dumps({"workload": "ngram-draft", "corpus_tokens": int(sum(c.size for c in corpus)),
                       "table_entries": len(table), "host_build_ms": build_s * 1e3, "draft_us": us,
-                      "mean_drafts": float(nd.float().mean().item())}), flush=True)
+                      "mean_drafts": float(nd.float().mean().item()),
+                      "roofline": {"bound": "latency", "note": "one lane per sequence, 7 dependent "
+                                   "table probes of a few bytes each"},
+                      "cpu_baseline": {"value": sec * 1e6, "unit": "us per batch", "cores": 1,
+                                       "kind": "port", "sample": "the same 64 contexts, Python dict "
+                                       "table of the oracle"}}), flush=True)
 
 
 def other_workload(name, warmup, steps):
@@ -324,6 +393,21 @@ def other_workload(name, warmup, steps):
                 max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
             res[path] = {"us": us, "GB_s_unique": unique / us / 1e3, "frac_unique": unique / us / 1e3 / PEAK_HBM_GBS,
                          "GB_s_logical": logical / us / 1e3}
+        res["roofline"] = _roofline(unique, res["auto"]["us"])
+        # CPU: the oracle's attention (f32 build, 16 threads) on the first two sequences
+        import oracle
+
+        n2 = min(2, acase.batch)
+        nb2 = int(((acase.context_lens[:n2] + acase.block_size - 1) // acase.block_size).max())
+        q2 = int(acase.q_start_loc[n2])
+        sec = _cpu_seconds(lambda: oracle.paged_attention_mq(
+            acase.query[:q2], acase.key_cache, acase.value_cache, acase.block_table[:n2, :nb2],
+            acase.context_lens[:n2], num_heads=acase.num_heads, num_kv_heads=acase.num_kv_heads,
+            head_dim=acase.head_dim, block_size=acase.block_size, q_start_loc=acase.q_start_loc[:n2 + 1],
+            threads=16, precision="f32"), min_seconds=1.0)
+        kv2 = int(acase.context_lens[:n2].sum()) * acase.num_kv_heads * acase.head_dim * 2 * 2
+        res["cpu_baseline"] = {"value": kv2 / sec / 1e9, "unit": "GB/s of KV", "cores": 16, "kind": "port",
+                               "sample": f"the first {n2} sequences, oracle paged attention (f32)"}
         line["attention"] = res
         total_us += res["auto"]["us"]
     if vcase is not None:
@@ -335,7 +419,21 @@ def other_workload(name, warmup, steps):
         emitted = int((r.accepted.cpu() + 1).sum().item())
         s_bytes = vcase.logit_bytes(r.accepted.cpu().numpy())
         line["sampler"] = {"us": us, "algorithmic_bytes": s_bytes, "GB_s": s_bytes / us / 1e3,
-                           "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1}
+                           "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1,
+                           "roofline": _roofline(s_bytes, us)}
+        # CPU: the oracle's acceptance (f32 build, one thread) on up to 8 sequences
+        import oracle
+
+        n8 = min(8, vcase.batch)
+        sec = _cpu_seconds(lambda: oracle.spec_verify(
+            vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8], vcase.num_draft[:n8],
+            vcase.temperature[:n8], vcase.u_accept[:n8], vcase.u_resample[:n8], precision="f32"), min_seconds=1.0)
+        r8 = oracle.spec_verify(vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8],
+                                vcase.num_draft[:n8], vcase.temperature[:n8], vcase.u_accept[:n8],
+                                vcase.u_resample[:n8], precision="f32")
+        line["sampler"]["cpu_baseline"] = {"value": float((r8["accepted"] + 1).sum()) / sec, "unit": "tok/s",
+                                           "cores": 1, "kind": "port",
+                                           "sample": f"the first {n8} sequences, oracle acceptance (f32)"}
         total_us += us
         line["verified_tok_s_at_measured_parts"] = emitted / (total_us * 1e-6)
     print(json.dumps(line), flush=True)
