@@ -151,6 +151,21 @@ def test_cache_slots_past_the_context_are_never_used(gpu, dtype):
             h.assert_attention_close(out, case, exp, h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
 
 
+def test_long_context_in_one_split(gpu):
+    """Contexts of 16384 and 16000 tokens in a single split: 1024 blocks, 128 block pairs per
+    wave, so the block ids of a wave's pairs fill both slots of its lane-held table."""
+    case = wl.make_attention_case(context_lens=[16384, 16000], q_lens=[3, 1], num_heads=8,
+                                  num_kv_heads=2, dtype="bf16", seed=31)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 8, 128, 2)
+    exp = h.oracle_attention(case)
+    for splits in (1, 0):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                           t["context_lens"], q_start_loc=t["q_start_loc"], path="mfma",
+                           num_splits=splits)
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16)
+
+
 # ---------------------------------------------------------------- full-size workloads
 
 

@@ -97,6 +97,27 @@ def test_window_does_not_change_outputs(gpu, window):
     assert torch.equal(torch.nan_to_num(res.p_draft, -1.0), torch.nan_to_num(ref.p_draft, -1.0))
 
 
+def test_tail_pass_with_more_items_than_the_default_grid_holds(gpu):
+    """600 sequences that accept every draft (draft logits equal the target's): after a window of
+    1 there are 600 x 29 rows x 8 chunks = 139,200 tail items, more than 2048 workgroups x 64 items,
+    so the grid grows and every workgroup keeps at most 64. Outputs must equal a single pass over
+    all rows bit for bit."""
+    g = torch.Generator(device=gpu).manual_seed(3)
+    B, kmax, V = 600, 15, 32000
+    target = torch.randn((B, kmax + 1, V), generator=g, device=gpu) * 2
+    t = dict(target_logits=target, draft_logits=target[:, :kmax].contiguous(),
+             draft_tokens=torch.randint(0, V, (B, kmax), generator=g, device=gpu, dtype=torch.int32),
+             num_draft=torch.full((B,), kmax, dtype=torch.int32, device=gpu),
+             temperature=torch.ones(B, device=gpu),
+             u_accept=torch.rand((B, kmax), generator=g, device=gpu),
+             u_resample=torch.rand((B,), generator=g, device=gpu))
+    res = kyro_amd.verify_drafts(**t, return_probs=True, window=1)
+    ref = kyro_amd.verify_drafts(**t, return_probs=True, window=64)
+    assert res.accepted.min().item() == kmax
+    assert torch.equal(res.accepted, ref.accepted) and torch.equal(res.tokens, ref.tokens)
+    assert torch.equal(res.p_draft, ref.p_draft) and torch.equal(res.q_draft, ref.q_draft)
+
+
 def test_window_all_accepted_reads_bonus_row(gpu):
     """Identical draft and target: every sequence passes the window and its bonus row comes from
     the pass over the remaining rows."""
