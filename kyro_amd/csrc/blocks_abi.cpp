@@ -261,12 +261,20 @@ int kyro_copy_blocks(kyro_ctx ctx, const kyro_copy_blocks_params* p, void* key_c
                                                     (long long)dst[i]);
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        const size_t pair_bytes = pairs.size() * sizeof(int64_t);
-        if (int rc = ensure_arena(ctx, pair_bytes)) return rc;
-        Upload up = {ctx->arena, pairs.data(), pair_bytes};
-        if (int rc = stage_uploads(ctx, &up, 1)) return rc;
-        kyro::CopyBlocksArgs a;
-        a.pairs = static_cast<const int64_t*>(ctx->arena);
+        kyro::CopyBlocksArgs a{};
+        if (n <= kyro::kCopyInline) {  // the pairs travel in the kernel arguments: no upload
+            a.pairs = nullptr;
+            for (int64_t i = 0; i < n; ++i) {
+                a.inl[0][i] = (int32_t)src[i];
+                a.inl[1][i] = (int32_t)dst[i];
+            }
+        } else {
+            const size_t pair_bytes = pairs.size() * sizeof(int64_t);
+            if (int rc = ensure_arena(ctx, pair_bytes)) return rc;
+            Upload up = {ctx->arena, pairs.data(), pair_bytes};
+            if (int rc = stage_uploads(ctx, &up, 1)) return rc;
+            a.pairs = static_cast<const int64_t*>(ctx->arena);
+        }
         a.n = n;
         a.slab_vecs = (int64_t)(slab / 16);
         a.kc = static_cast<uint4*>(key_cache);

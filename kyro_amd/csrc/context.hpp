@@ -18,9 +18,13 @@ struct kyro_ctx_s {
     void* arena = nullptr;  // per-call scratch, stream-ordered
     size_t arena_bytes = 0;
     int* err = nullptr;     // device error word
-    void* pinned = nullptr;            // host staging for small uploads (hipHostMalloc)
-    size_t pinned_bytes = 0;
-    hipEvent_t pinned_done = nullptr;  // recorded after the last copy out of `pinned`
+    // Host staging for small uploads (hipHostMalloc): kStageSlots slots used in turn, each with
+    // an event recorded after the copies out of it.
+    void* pinned = nullptr;
+    void* pinned_dev = nullptr;  // the same memory as the device addresses it
+    size_t pinned_slot_bytes = 0;
+    int pinned_next = 0;
+    hipEvent_t pinned_done[4] = {};
 };
 
 namespace kyro {
@@ -55,9 +59,13 @@ struct Upload {
     size_t bytes;
 };
 
-// Queues the copies on the context's stream through its pinned staging buffer. The host data
-// is copied into staging before this returns, so the caller may reuse it at once; staging is
-// reused only after the previous upload's copies have executed.
+constexpr int kStageSlots = 4;  // slots of the pinned staging ring (kyro_ctx_s::pinned_done)
+static_assert(sizeof(kyro_ctx_s::pinned_done) / sizeof(hipEvent_t) == kStageSlots, "staging ring size");
+
+// Queues the copies on the context's stream through the next slot of its pinned staging ring.
+// The host data is copied into staging before this returns, so the caller may reuse it at once.
+// A slot is reused only after the copies out of it have executed, so the host waits only when
+// kStageSlots uploads are still queued ahead.
 int stage_uploads(kyro_ctx ctx, const Upload* ups, int n);
 
 template <typename F>

@@ -106,15 +106,29 @@ struct KvAppendArgs {
 hipError_t launch_kv_append(const KvAppendArgs& a, hipStream_t stream);
 
 // Whole-block copies within a cache pair (copy-on-write of a prefix block).
+constexpr int kCopyInline = 240;  // block pairs passed in the kernel arguments (2 x 240 x 4 B)
 struct CopyBlocksArgs {
-    const int64_t* pairs;  // [2, n]: sources then destinations
+    const int64_t* pairs;  // [2, n]: sources then destinations; nullptr: in `inl` (n <= kCopyInline)
     int64_t n;
     int64_t slab_vecs;     // 16-byte vectors in one block of one cache
     uint4* kc;
     uint4* vc;
+    int32_t inl[2][kCopyInline];
 };
 
 hipError_t launch_copy_blocks(const CopyBlocksArgs& a, hipStream_t stream);
+
+// Scatter of up to kMaxUploads staged uploads (8-byte words) from device-mapped host staging.
+constexpr int kMaxUploads = 4;
+struct UploadArgs {
+    const char* src;                 // the staging slot, as the device addresses it
+    int n;
+    int64_t off[kMaxUploads];        // byte offset of upload u in the slot (8-byte aligned)
+    uint64_t* dst[kMaxUploads];
+    int64_t words[kMaxUploads];
+};
+
+hipError_t launch_upload_scatter(const UploadArgs& a, hipStream_t stream);
 
 // Plain-decode sampling with logit processors.
 // One non-empty histogram bin of a vocabulary chunk: count, and for top-p the sum of

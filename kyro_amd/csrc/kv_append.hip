@@ -125,7 +125,8 @@ __global__ __launch_bounds__(kThreads) void copy_blocks_kernel(CopyBlocksArgs a)
     const int64_t pair = blockIdx.y;
     const int64_t v = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (v >= a.slab_vecs) return;
-    const int64_t src = a.pairs[pair], dst = a.pairs[a.n + pair];
+    const int64_t src = a.pairs ? a.pairs[pair] : a.inl[0][pair];
+    const int64_t dst = a.pairs ? a.pairs[a.n + pair] : a.inl[1][pair];
     a.kc[dst * a.slab_vecs + v] = a.kc[src * a.slab_vecs + v];
     a.vc[dst * a.slab_vecs + v] = a.vc[src * a.slab_vecs + v];
 }

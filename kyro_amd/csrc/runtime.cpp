@@ -60,24 +60,46 @@ int stage_uploads(kyro_ctx ctx, const Upload* ups, int n) {
     size_t total = 0;
     for (int i = 0; i < n; ++i) total += align_up(ups[i].bytes, 256);
     if (total == 0) return KYRO_OK;
-    if (!ctx->pinned_done) KYRO_HIP(hipEventCreateWithFlags(&ctx->pinned_done, hipEventDisableTiming));
-    else KYRO_HIP(hipEventSynchronize(ctx->pinned_done));  // the last upload has left staging
-    if (total > ctx->pinned_bytes) {
-        const size_t want = align_up(std::max(total, ctx->pinned_bytes * 3 / 2), size_t(1) << 16);
+    if (total > ctx->pinned_slot_bytes) {  // grow: every slot's copies must have left staging
+        for (int s = 0; s < kStageSlots; ++s)
+            if (ctx->pinned_done[s]) KYRO_HIP(hipEventSynchronize(ctx->pinned_done[s]));
+        const size_t want = align_up(std::max(total, ctx->pinned_slot_bytes * 3 / 2), size_t(1) << 16);
         if (ctx->pinned) KYRO_HIP(hipHostFree(ctx->pinned));
         ctx->pinned = nullptr;
-        ctx->pinned_bytes = 0;
-        KYRO_HIP(hipHostMalloc(&ctx->pinned, want, hipHostMallocDefault));
-        ctx->pinned_bytes = want;
+        ctx->pinned_slot_bytes = 0;
+        // Coherent and mapped: small uploads are read by a kernel straight from staging.
+        KYRO_HIP(hipHostMalloc(&ctx->pinned, want * kStageSlots, hipHostMallocMapped | hipHostMallocCoherent));
+        KYRO_HIP(hipHostGetDevicePointer(&ctx->pinned_dev, ctx->pinned, 0));
+        ctx->pinned_slot_bytes = want;
     }
-    char* p = static_cast<char*>(ctx->pinned);
+    const int slot = ctx->pinned_next;
+    ctx->pinned_next = (slot + 1) % kStageSlots;
+    if (!ctx->pinned_done[slot]) KYRO_HIP(hipEventCreateWithFlags(&ctx->pinned_done[slot], hipEventDisableTiming));
+    else KYRO_HIP(hipEventSynchronize(ctx->pinned_done[slot]));  // the slot's last upload has left it
+    char* p = static_cast<char*>(ctx->pinned) + (size_t)slot * ctx->pinned_slot_bytes;
+    // Small uploads of whole 8-byte words go out in one scatter kernel that reads staging
+    // directly; the others as one host-to-device copy each.
+    bool scatter = n <= kyro::kMaxUploads && total <= (size_t(1) << 22);
+    for (int i = 0; i < n; ++i)
+        if (ups[i].bytes % 8 != 0 || reinterpret_cast<uintptr_t>(ups[i].dst) % 8 != 0) scatter = false;
+    kyro::UploadArgs sa{};
+    sa.src = static_cast<const char*>(ctx->pinned_dev) + (size_t)slot * ctx->pinned_slot_bytes;
+    size_t off = 0;
     for (int i = 0; i < n; ++i) {
         if (ups[i].bytes == 0) continue;
-        std::memcpy(p, ups[i].src, ups[i].bytes);
-        KYRO_HIP(hipMemcpyAsync(ups[i].dst, p, ups[i].bytes, hipMemcpyHostToDevice, ctx->stream));
-        p += align_up(ups[i].bytes, 256);
+        std::memcpy(p + off, ups[i].src, ups[i].bytes);
+        if (scatter) {
+            sa.off[sa.n] = (int64_t)off;
+            sa.dst[sa.n] = static_cast<uint64_t*>(ups[i].dst);
+            sa.words[sa.n] = (int64_t)(ups[i].bytes / 8);
+            ++sa.n;
+        } else {
+            KYRO_HIP(hipMemcpyAsync(ups[i].dst, p + off, ups[i].bytes, hipMemcpyHostToDevice, ctx->stream));
+        }
+        off += align_up(ups[i].bytes, 256);
     }
-    KYRO_HIP(hipEventRecord(ctx->pinned_done, ctx->stream));
+    if (scatter) KYRO_HIP(kyro::launch_upload_scatter(sa, ctx->stream));
+    KYRO_HIP(hipEventRecord(ctx->pinned_done[slot], ctx->stream));
     return KYRO_OK;
 }
 
@@ -148,9 +170,11 @@ int kyro_ctx_destroy(kyro_ctx ctx) {
         if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
         if (ctx->arena) (void)hipFree(ctx->arena);
         if (ctx->err) (void)hipFree(ctx->err);
-        if (ctx->pinned_done) (void)hipEventSynchronize(ctx->pinned_done);
+        for (hipEvent_t& e : ctx->pinned_done)
+            if (e) (void)hipEventSynchronize(e);
         if (ctx->pinned) (void)hipHostFree(ctx->pinned);
-        if (ctx->pinned_done) (void)hipEventDestroy(ctx->pinned_done);
+        for (hipEvent_t& e : ctx->pinned_done)
+            if (e) (void)hipEventDestroy(e);
         if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
         return KYRO_OK;
