@@ -39,9 +39,16 @@ struct AttnArgs {
     int max_blocks, num_blocks, total_q, max_q_len, rows_cap;
     int causal, out_bf16, dtype_bf16;
     float scale_log2;  // softmax scale * log2(e)
-    int splits, chunk_blocks, units, units_padded;
-    int row_groups;  // workgroups per (unit, split), each covering rows_per_group rows
+    int splits, chunk_blocks, units;
+    int hpw;           // kv heads (units) per workgroup: 2 in the MFMA kernel when Hkv is even
+    int ugroups;       // units / hpw
+    int ugroups_padded;  // ugroups rounded up to a multiple of 8 (the XCD count)
+    int row_groups;  // workgroups per (unit group, split), each covering rows_per_group rows
 };
+
+// Block pairs one MFMA wave can hold the ids of (two 64-lane slots). A split has at most
+// 2 * kMfmaMaxPairsPerWave * (kernel waves per head) blocks.
+constexpr int kMfmaMaxPairsPerWave = 128;
 
 // Query rows one attention workgroup covers.
 constexpr int kVectorRowsPerGroup = 8;

@@ -41,19 +41,20 @@ struct SeqInfo {
     bool ok;
 };
 
-// Workgroup -> (unit = sequence * Hkv + kv head, split, row group). Consecutive workgroups go to
-// different XCDs; the splits and row groups of one unit share (blockIdx % 8) and therefore one
-// XCD, and a unit's row groups are dispatched back to back, so the K/V they all read is fetched
-// from HBM once and served to the others from that XCD's L2.
-__device__ __forceinline__ bool map_workgroup(const AttnArgs& a, int& unit, int& split, int& rg) {
+// Workgroup -> (unit group, split, row group). A unit is sequence * Hkv + kv head; a group is
+// a.hpw consecutive units (kv heads of one sequence). Consecutive workgroups go to different
+// XCDs; the splits and row groups of one group share (blockIdx % 8) and therefore one XCD, and a
+// group's row groups are dispatched back to back, so the K/V they all read is fetched from HBM
+// once and served to the others from that XCD's L2.
+__device__ __forceinline__ bool map_workgroup(const AttnArgs& a, int& ugroup, int& split, int& rg) {
     const int wg = blockIdx.x;
     const int xcd = wg & 7;
     const int local = wg >> 3;
     rg = local % a.row_groups;
     const int rest = local / a.row_groups;
     split = rest % a.splits;
-    unit = (rest / a.splits) * 8 + xcd;
-    return unit < a.units;
+    ugroup = (rest / a.splits) * 8 + xcd;
+    return ugroup < a.ugroups;
 }
 
 __device__ SeqInfo seq_info(const AttnArgs& a, int unit) {
@@ -261,15 +262,26 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 // A workgroup covers NTW 16-row tiles of its unit's rows (NTW 1 or 2: the accumulators of two
 // tiles plus two K/V pair buffers fill the register file without spills); units with more rows
 // (a large GQA group times many draft positions) get one workgroup per 32-row group.
-template <int NTW>
+//
+// With HP = 2 a workgroup takes two adjacent kv heads of the sequence, two waves each: the
+// workgroup then reads both heads' slabs of each block together (8 KiB contiguous of K and of
+// V), and a batch with 2 x 256 units runs as one round of workgroups on 256 CUs instead of two.
+template <int NTW, int HP>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     constexpr int D = kMfmaD;
-    constexpr int RW = NTW * 16;  // rows of one wave (one tile group)
-    __shared__ Frame<RW, D> frame;
+    constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
+    constexpr int WPH = kWaves / HP;  // waves per kv head
+    __shared__ Frame<RW, D> frame[HP];
     __shared__ int s_blk[kMaxChunkBlocks];
 
-    int unit, split, rg;
-    if (!map_workgroup(a, unit, split, rg)) return;
+    int ug, split, rg;
+    if (!map_workgroup(a, ug, split, rg)) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
+    const int hw = wave / WPH;  // this wave's kv head within the group
+    const int wp = wave % WPH;  // and its place among that head's waves
+    const int unit = ug * HP + hw;
+    // The group's units belong to one sequence, so everything but the kv head is the same for
+    // every wave, and the early returns below are taken by the whole workgroup or by none of it.
     const SeqInfo si = seq_info(a, unit);
     if (!si.ok) return;
     const int nsplit = num_splits_for(a, si.nblk);
@@ -278,7 +290,6 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     if (row0 > 0 && row0 >= si.rows) return;  // this row group is past the sequence's rows
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int r = lane & 15;  // MFMA row/column within a 16-tile
     const int g = lane >> 4;  // 16-lane group
     const int blk_begin = split * a.chunk_blocks;
@@ -415,17 +426,17 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             }
         };
 
-        // Each wave streams the pairs w, w + 4, w + 8, ... of the split. The loads of the next
-        // pair are issued before the current pair is computed (two register buffers, unrolled).
-        constexpr int step = 2 * kWaves;
+        // Each wave streams the pairs wp, wp + WPH, wp + 2 WPH, ... of the split for its kv head.
+        // The loads of the next pair are issued before the current pair is computed (two
+        // register buffers, unrolled).
+        constexpr int step = 2 * WPH;
         {
             // Pair j of this wave covers blocks pb0 + j step and pb0 + j step + 1. Lane j % 64 holds
-            // the ids of pair j in slot j / 64 (a split has at most kMaxChunkBlocks blocks, so at
-            // most kPairSlots * 64 pairs per wave); the loop reads them with readlane into scalar
+            // the ids of pair j in slot j / 64 (the host keeps a split within
+            // kMfmaMaxPairsPerWave pairs per wave); the loop reads them with readlane into scalar
             // registers and needs no vector temporaries for addressing.
-            constexpr int kPairSlots = kMaxChunkBlocks / (2 * kWaves * 64);
-            static_assert(kPairSlots * 64 * 2 * kWaves >= kMaxChunkBlocks, "pair table too small");
-            const int pb0 = blk_begin + 2 * wave;
+            constexpr int kPairSlots = kMfmaMaxPairsPerWave / 64;
+            const int pb0 = blk_begin + 2 * wp;
             int pid0[kPairSlots], pid1[kPairSlots];
 #pragma unroll
             for (int t = 0; t < kPairSlots; ++t) {
@@ -473,32 +484,33 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             lsum[nt] += shfl_xor_f(lsum[nt], 32);
         }
 
-        // Merge the four waves: common max, then the rescaled accumulators are added into LDS in
-        // a fixed order (wave 0 stores), so the result is bitwise reproducible. Lane (r, g) owns
-        // head dims 32 g + 8 e + dt of row 16 nt + r.
+        // Merge each kv head's waves in its frame: common max, then the rescaled accumulators
+        // are added into LDS in a fixed order (the head's first wave stores), so the result is
+        // bitwise reproducible. Lane (r, g) owns head dims 32 g + 8 e + dt of row 16 nt + r.
+        Frame<RW, D>& fr = frame[hw];
         if (g == 0) {
 #pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) frame.m[wave][nt * 16 + r] = m[nt];
+            for (int nt = 0; nt < NTW; ++nt) fr.m[wp][nt * 16 + r] = m[nt];
         }
         __syncthreads();
         float f[NTW];
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
             const int n = nt * 16 + r;
-            float M = frame.m[0][n];
+            float M = fr.m[0][n];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) M = fmaxf(M, frame.m[w][n]);
+            for (int w = 1; w < WPH; ++w) M = fmaxf(M, fr.m[w][n]);
             f[nt] = (m[nt] == kNegInf) ? 0.f : fast_exp2(m[nt] - M);
             if (g == 0) {
-                frame.l[wave][n] = lsum[nt] * f[nt];
-                if (wave == 0) frame.mx[n] = M;
+                fr.l[wp][n] = lsum[nt] * f[nt];
+                if (wp == 0) fr.mx[n] = M;
             }
         }
-        for (int w = 0; w < kWaves; ++w) {
-            if (wave == w) {
+        for (int w = 0; w < WPH; ++w) {  // every wave of the workgroup takes part in each barrier
+            if (wp == w) {
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
-                    float* dst = &frame.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 32 * g];
+                    float* dst = &fr.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 32 * g];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -511,7 +523,12 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             __syncthreads();
         }
         const int nrows = min(RW, si.rows - row0);
-        frame_flush<RW, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
+#pragma unroll
+        for (int h = 0; h < HP; ++h) {  // the whole workgroup stores each head's rows
+            SeqInfo sh = si;
+            sh.kvh = (ug * HP + h) % a.Hkv;
+            frame_flush<RW, D>(a, sh, ug * HP + h, split, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH);
+        }
     }
 }
 
@@ -702,11 +719,17 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 
 hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t stream) {
     const dim3 block(kThreads);
-    const dim3 grid((unsigned)(a.units_padded * a.splits * a.row_groups));
+    const dim3 grid((unsigned)(a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
-        if (mfma_rows_per_group(a.rows_cap) == 16) attn_mfma_kernel<1><<<grid, block, 0, stream>>>(a);
-        else attn_mfma_kernel<2><<<grid, block, 0, stream>>>(a);
+        const bool rows16 = mfma_rows_per_group(a.rows_cap) == 16;
+        if (a.hpw == 2) {
+            if (rows16) attn_mfma_kernel<1, 2><<<grid, block, 0, stream>>>(a);
+            else attn_mfma_kernel<2, 2><<<grid, block, 0, stream>>>(a);
+        } else {
+            if (rows16) attn_mfma_kernel<1, 1><<<grid, block, 0, stream>>>(a);
+            else attn_mfma_kernel<2, 1><<<grid, block, 0, stream>>>(a);
+        }
     } else {
         const bool bf16 = a.dtype_bf16;
         if (a.D == 128) {

@@ -353,7 +353,12 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         const double scale = p->scale > 0 ? (double)p->scale : 1.0 / std::sqrt((double)p->head_dim);
         a.scale_log2 = (float)(scale * 1.4426950408889634);
         a.units = p->batch_size * p->num_kv_heads;
-        a.units_padded = (a.units + 7) / 8 * 8;
+        // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
+        // waves per head): the workgroup then reads both heads' slabs of each block together, and
+        // the Llama-3-8B step fits the chip in one round of workgroups.
+        a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0) ? 2 : 1;
+        a.ugroups = a.units / a.hpw;
+        a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
         // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
         // (vector) or 16 / 32 (MFMA) rows that stream the same K/V.
         const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
@@ -370,20 +375,25 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             // With four or more workgroups per CU already, splitting only adds per-workgroup
             // set-up and a combine pass (one workgroup fills a CU, so nothing hides them).
             constexpr int kTargetChunk = 256, kCUs = 256, kMinChunk = 16;
-            const int per_split = a.units * a.row_groups;
+            const int per_split = a.ugroups * a.row_groups;
             splits = per_split >= 4 * kCUs ? 1 : (mb + kTargetChunk - 1) / kTargetChunk;
             if (per_split * splits < kCUs)
                 splits = std::min((kCUs + per_split - 1) / per_split, std::max(1, mb / kMinChunk));
         }
+        // Longest split: the LDS block-id staging, and for the MFMA kernel the block pairs a wave
+        // holds ids for (its waves per head x two 64-lane slots).
+        const int max_chunk = kernel == kyro::ATTN_KERNEL_MFMA
+                                  ? std::min(kyro::kMaxChunkBlocks, 2 * kyro::kMfmaMaxPairsPerWave * (4 / a.hpw))
+                                  : kyro::kMaxChunkBlocks;
         splits = std::min(splits, mb);
-        splits = std::max(splits, (mb + kyro::kMaxChunkBlocks - 1) / kyro::kMaxChunkBlocks);
+        splits = std::max(splits, (mb + max_chunk - 1) / max_chunk);
         int chunk = (mb + splits - 1) / splits;
-        chunk = std::min((chunk + 1) / 2 * 2, kyro::kMaxChunkBlocks);
+        chunk = std::min((chunk + 1) / 2 * 2, max_chunk);
         splits = (mb + chunk - 1) / chunk;
         a.splits = splits;
         a.chunk_blocks = chunk;
         // One launch carries at most 2^32 - 1 work items along x.
-        if ((uint64_t)a.units_padded * splits * a.row_groups * 256 > 0xffffffffull)
+        if ((uint64_t)a.ugroups_padded * splits * a.row_groups * 256 > 0xffffffffull)
             return fail(KYRO_EUNSUPPORTED, "paged_attention: %d units x %d splits x %d row groups is too large for one launch",
                         a.units, splits, a.row_groups);
 
