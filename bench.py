@@ -386,11 +386,15 @@ def other_workload(name, warmup, steps):
         out = torch.empty(t["q"].shape, dtype=torch.bfloat16, device=dev)
         logical = acase.kv_bytes() + acase.q_out_bytes(2)
         unique = acase.unique_kv_bytes() + acase.q_out_bytes(2)
-        res = {"logical_bytes": logical, "unique_bytes": unique, "context_tokens": int(acase.context_lens.sum())}
+        # tables that share blocks between sequences (a common prefix) keep the K/V loads cacheable
+        reuse = "shared" if acase.unique_kv_bytes() < acase.kv_bytes() else "auto"
+        res = {"logical_bytes": logical, "unique_bytes": unique, "context_tokens": int(acase.context_lens.sum()),
+               "kv_reuse": reuse}
         for path in ("auto", "vector", "mfma"):
             us = _median_us(lambda: attn.forward_async(
                 t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"],
-                max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
+                max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path, kv_reuse=reuse),
+                warmup, steps)
             res[path] = {"us": us, "GB_s_unique": unique / us / 1e3, "frac_unique": unique / us / 1e3 / PEAK_HBM_GBS,
                          "GB_s_logical": logical / us / 1e3}
         res["roofline"] = _roofline(unique, res["auto"]["us"])

@@ -101,9 +101,12 @@ int kyro_bm_match_prefix(kyro_bm bm, const uint32_t* tokens, int64_t n, int64_t*
 /* Writes, on ctx's stream, block_table[b][i] = i-th block of request_ids[b] (0 past its blocks)
  * for b < B, i < max_blocks, and context_lens[b] = its token count (context_lens may be NULL).
  * Device pointers: block_table [B, max_blocks] int64, context_lens [B] int64. A request with
- * more than max_blocks blocks, or an unknown id, is KYRO_EINVAL. */
+ * more than max_blocks blocks, or an unknown id, is KYRO_EINVAL. out_shared (host, may be NULL)
+ * receives 1 when some block appears in the tables of two of the requests, else 0: the
+ * kv_reuse hint of the attention launch over these tables (KYRO_KV_REUSE_SHARED when 1). */
 int kyro_bm_write_tables(kyro_bm bm, kyro_ctx ctx, const uint64_t* request_ids, int32_t B,
-                         int32_t max_blocks, int64_t* block_table, int64_t* context_lens);
+                         int32_t max_blocks, int64_t* block_table, int64_t* context_lens,
+                         int32_t* out_shared);
 
 /* ---------------------------------------------------------------- block copies */
 

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 6
+#define KYRO_ABI_VERSION 7
 
 typedef enum kyro_status {
     KYRO_OK = 0,
@@ -109,6 +109,23 @@ typedef enum kyro_attn_path {
     KYRO_ATTN_MFMA = 2
 } kyro_attn_path;
 
+/* How often one launch reads each cached (block, kv head) slab; a cache-policy hint for the MFMA
+ * kernel's K/V loads that never changes results. Streaming loads (the nontemporal hint) read
+ * data used once ~14% faster, but a slab read again soon after (by another row group of the
+ * same kv head, or by another sequence whose table holds the same block) then comes from HBM
+ * again instead of L2.
+ *   AUTO:   streaming when each slab is read by one workgroup, i.e. a kv head's query rows
+ *           (GQA group x max_q_len) fit one row group of 32 (16 for <= 16 rows); cached otherwise.
+ *           Right when no two sequences of the batch share a block.
+ *   SHARED: cached loads; for tables that share blocks between sequences (prefix caching;
+ *           kyro_bm_write_tables reports it).
+ *   STREAM: streaming loads regardless. */
+typedef enum kyro_kv_reuse {
+    KYRO_KV_REUSE_AUTO = 0,
+    KYRO_KV_REUSE_SHARED = 1,
+    KYRO_KV_REUSE_STREAM = 2
+} kyro_kv_reuse;
+
 /* Mirrors PagedAttention { block_size, num_heads, head_dim, num_kv_heads }
  * (src/model/attention_kernel.rs:4-9) plus the shapes the Rust side reads off its tensors. */
 typedef struct kyro_paged_attention_params {
@@ -130,6 +147,7 @@ typedef struct kyro_paged_attention_params {
     int32_t max_q_len;           /* upper bound on query rows per sequence; 0 => 1 without
                                     q_start_loc, total_q with it (sizes the split workspace;
                                     a sequence above it latches KYRO_EINVAL) */
+    int32_t kv_reuse;            /* kyro_kv_reuse (0 => AUTO) */
 } kyro_paged_attention_params;
 
 /*

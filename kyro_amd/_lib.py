@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libkyro_verify.so")
 KYRO_OK, KYRO_EINVAL, KYRO_EOOM, KYRO_EHIP, KYRO_EUNSUPPORTED, KYRO_ENOSPACE = 0, 1, 2, 3, 4, 5
 KYRO_F32, KYRO_BF16 = 0, 1
 KYRO_ATTN_AUTO, KYRO_ATTN_VECTOR, KYRO_ATTN_MFMA = 0, 1, 2
+KYRO_KV_REUSE_AUTO, KYRO_KV_REUSE_SHARED, KYRO_KV_REUSE_STREAM = 0, 1, 2
 
 _STATUS_NAMES = {0: "KYRO_OK", 1: "KYRO_EINVAL", 2: "KYRO_EOOM", 3: "KYRO_EHIP", 4: "KYRO_EUNSUPPORTED",
                  5: "KYRO_ENOSPACE"}
@@ -37,7 +38,7 @@ class PagedAttentionParams(ctypes.Structure):
         ("dtype", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
         ("causal", ctypes.c_int32), ("scale", ctypes.c_float),
         ("path", ctypes.c_int32), ("num_splits", ctypes.c_int32),
-        ("max_q_len", ctypes.c_int32),
+        ("max_q_len", ctypes.c_int32), ("kv_reuse", ctypes.c_int32),
     ]
 
 
@@ -63,7 +64,7 @@ class SampleParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("batch_size", "vocab_size", "logits_dtype", "num_masks")]
 
 
-ABI_VERSION = 6  # KYRO_ABI_VERSION of include/kyro_verify.h
+ABI_VERSION = 7  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -107,7 +108,7 @@ _SIGNATURES = {
     "kyro_bm_check": ([_P], ctypes.c_int),
     "kyro_bm_num_cached_blocks": ([_P], ctypes.c_int64),
     "kyro_bm_match_prefix": ([_P, _P, ctypes.c_int64, _P, ctypes.c_int64, _P, _P], ctypes.c_int),
-    "kyro_bm_write_tables": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P], ctypes.c_int),
+    "kyro_bm_write_tables": ([_P, _P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, _P], ctypes.c_int),
     "kyro_copy_blocks": ([_P, ctypes.POINTER(CopyBlocksParams), _P, _P, _P, _P, ctypes.c_int64], ctypes.c_int),
     # include/kyro_sample.h
     "kyro_sample_tokens": ([_P, ctypes.POINTER(SampleParams)] + [_P] * 14, ctypes.c_int),

@@ -24,6 +24,8 @@ from . import _lib
 
 _DTYPES = {torch.float32: _lib.KYRO_F32, torch.bfloat16: _lib.KYRO_BF16}
 _PATHS = {"auto": _lib.KYRO_ATTN_AUTO, "vector": _lib.KYRO_ATTN_VECTOR, "mfma": _lib.KYRO_ATTN_MFMA}
+_KV_REUSE = {"auto": _lib.KYRO_KV_REUSE_AUTO, "shared": _lib.KYRO_KV_REUSE_SHARED,
+             "stream": _lib.KYRO_KV_REUSE_STREAM}
 
 
 def _require(t: torch.Tensor, name: str, dtype=None, ndim=None, device=None):
@@ -50,11 +52,15 @@ class PagedAttention:
 
     def forward(self, query, key_cache, value_cache, block_table, context_lens, *,
                 q_start_loc=None, max_q_len=None, causal=True, out_dtype=torch.float32,
-                path="auto", num_splits=0, scale=None, out=None):
+                path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto"):
         """Attention of every query row against its sequence's paged context.
 
         ``q_start_loc`` (int32 [batch+1]) gives each sequence's rows of ``query``; ``max_q_len``
-        bounds the rows per sequence (computed from q_start_loc when omitted). The call
+        bounds the rows per sequence (computed from q_start_loc when omitted). ``kv_reuse`` is a
+        cache-policy hint for the K/V loads that never changes the result: "auto" streams them
+        when each cached slab is read once per launch, "shared" keeps them cacheable for tables
+        that share blocks between sequences (``BlockManager.write_tables`` reports that),
+        "stream" streams them regardless. The call
         synchronises, so errors the device detects (bad block ids, context lengths beyond the
         table) raise KyroError here, as the reference returns Err from ``forward``;
         :meth:`forward_async` is the non-blocking variant.
@@ -62,13 +68,13 @@ class PagedAttention:
         out = self.forward_async(query, key_cache, value_cache, block_table, context_lens,
                                  q_start_loc=q_start_loc, max_q_len=max_q_len, causal=causal,
                                  out_dtype=out_dtype, path=path, num_splits=num_splits,
-                                 scale=scale, out=out)
+                                 scale=scale, out=out, kv_reuse=kv_reuse)
         _lib.context(query.device.index or 0).sync()
         return out
 
     def forward_async(self, query, key_cache, value_cache, block_table, context_lens, *,
                       q_start_loc=None, max_q_len=None, causal=True, out_dtype=torch.float32,
-                      path="auto", num_splits=0, scale=None, out=None):
+                      path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto"):
         """Queues the kernel on torch's current stream and returns without synchronising.
         Device-detected errors surface at the next ``kyro_amd.sync(device)``."""
         dev = query.device
@@ -113,7 +119,8 @@ class PagedAttention:
         params = _lib.PagedAttentionParams(
             self.block_size, self.num_heads, self.head_dim, self.num_kv_heads, batch, total_q,
             block_table.shape[1], nb, _DTYPES[query.dtype], _DTYPES[out_dtype], 1 if causal else 0,
-            float(scale) if scale else 0.0, _PATHS[path], int(num_splits), int(max_q_len))
+            float(scale) if scale else 0.0, _PATHS[path], int(num_splits), int(max_q_len),
+            _KV_REUSE[kv_reuse])
         ctx = _lib.context(dev.index or 0)
         ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(_lib.lib().kyro_paged_attention_mq(

@@ -196,9 +196,10 @@ class BlockManager:
     def num_cached_blocks(self) -> int:
         return int(_lib.lib().kyro_bm_num_cached_blocks(self._h))
 
-    def write_tables(self, request_ids, block_table, context_lens=None) -> None:
+    def write_tables(self, request_ids, block_table, context_lens=None) -> bool:
         """Writes the device block table ([B, max_blocks] int64) and context lengths ([B] int64) of
-        the requests, on torch's current stream."""
+        the requests, on torch's current stream. Returns True when two of the requests hold a
+        common block (then attention over these tables takes ``kv_reuse="shared"``)."""
         import torch
 
         rid = np.ascontiguousarray(np.asarray(request_ids, dtype=np.uint64).reshape(-1))
@@ -211,9 +212,11 @@ class BlockManager:
         dev = block_table.device
         ctx = _lib.context(dev.index or 0)
         ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
+        shared = ctypes.c_int32(0)
         _lib.check(_lib.lib().kyro_bm_write_tables(
             self._h, ctx.handle, _ptr(rid), B, block_table.shape[1], block_table.data_ptr(),
-            context_lens.data_ptr() if context_lens is not None else None))
+            context_lens.data_ptr() if context_lens is not None else None, ctypes.byref(shared)))
+        return bool(shared.value)
 
 
 def copy_blocks(key_cache, value_cache, pairs) -> None:

@@ -13,7 +13,11 @@ using namespace kyro::rt;
 
 struct kyro_bm_s {
     kyro::bm::BlockManager m;
-    kyro_bm_s(int bs, int64_t gpu, int64_t cpu) : m(bs, gpu, cpu) {}
+    // Per block: (call number << 32) | (1 + the request that listed it last), for telling
+    // kyro_bm_write_tables' callers whether two requests share a block.
+    std::vector<uint64_t> seen;
+    uint32_t calls = 0;
+    kyro_bm_s(int bs, int64_t gpu, int64_t cpu) : m(bs, gpu, cpu), seen((size_t)gpu, 0) {}
 };
 
 struct kyro_radix_s {
@@ -205,12 +209,19 @@ int kyro_bm_match_prefix(kyro_bm bm, const uint32_t* tokens, int64_t n, int64_t*
 }
 
 int kyro_bm_write_tables(kyro_bm bm, kyro_ctx ctx, const uint64_t* request_ids, int32_t B, int32_t max_blocks,
-                         int64_t* block_table, int64_t* context_lens) {
+                         int64_t* block_table, int64_t* context_lens, int32_t* out_shared) {
     return guarded([&]() -> int {
         if (int rc = check_ctx(ctx)) return rc;
         if (!bm || B < 0 || max_blocks <= 0 || (B > 0 && (!request_ids || !block_table)))
             return fail(KYRO_EINVAL, "bm_write_tables: bad arguments");
+        if (out_shared) *out_shared = 0;
         if (B == 0) return KYRO_OK;
+        if (++bm->calls == 0) {  // the call counter wrapped: forget every older mark
+            std::fill(bm->seen.begin(), bm->seen.end(), 0);
+            bm->calls = 1;
+        }
+        const uint64_t call = (uint64_t)bm->calls << 32;
+        int32_t shared = 0;
         std::vector<int64_t> table((size_t)B * max_blocks, 0), lens((size_t)B, 0);
         for (int32_t b = 0; b < B; ++b) {
             const kyro::bm::Request* r = bm->m.find(request_ids[b]);
@@ -221,7 +232,15 @@ int kyro_bm_write_tables(kyro_bm bm, kyro_ctx ctx, const uint64_t* request_ids, 
                             (unsigned long long)request_ids[b], r->blocks.size(), max_blocks);
             std::copy(r->blocks.begin(), r->blocks.end(), table.begin() + (size_t)b * max_blocks);
             lens[(size_t)b] = r->num_tokens;
+            for (const int64_t blk : r->blocks) {
+                if (blk < 0 || (size_t)blk >= bm->seen.size()) continue;
+                uint64_t& s = bm->seen[(size_t)blk];
+                const uint64_t mine = call | (uint64_t)(b + 1);
+                if ((s & ~0xffffffffull) == call && s != mine) shared = 1;
+                s = mine;
+            }
         }
+        if (out_shared) *out_shared = shared;
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
         Upload ups[2] = {{block_table, table.data(), table.size() * sizeof(int64_t)},

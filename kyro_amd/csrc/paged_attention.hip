@@ -222,7 +222,8 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // missing block: past the split, or a bad id). Each (block, kv head) slab is read through a
 // buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
 // addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
-// a prefetched pair in flight.
+// a prefetched pair in flight. POL is the loads' cache policy (kLoadCached or kLoadStream).
+template <int POL>
 __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t block_stride, size_t kv_off, int r, int g) {
@@ -241,10 +242,10 @@ __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict_
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), (short)0, kSlabBytes, kRawBufferWord3);
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-            p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * s, 0));
+            p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * s, POL));
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 256 * e, 0));
+            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 256 * e, POL));
     }
 }
 
@@ -266,7 +267,9 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 // With HP = 2 a workgroup takes two adjacent kv heads of the sequence, two waves each: the
 // workgroup then reads both heads' slabs of each block together (8 KiB contiguous of K and of
 // V), and a batch with 2 x 256 units runs as one round of workgroups on 256 CUs instead of two.
-template <int NTW, int HP>
+// POL is the cache policy of the K/V loads: kLoadStream when no other workgroup reads the same
+// slabs (the host decides), kLoadCached otherwise.
+template <int NTW, int HP, int POL>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
@@ -456,21 +459,27 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
                 }
             };
             const int npairs = pb0 < blk_end ? (blk_end - 1 - pb0) / step + 1 : 0;
+            // The ids of the pair after j, or -1 (the zero slab, cache-hot) past the last pair.
+            auto next_ids = [&](int j, int& b0, int& b1) {
+                pair_ids(min(j + 1, kPairSlots * 64 - 1), b0, b1);
+                b0 = j + 1 < npairs ? b0 : -1;
+                b1 = j + 1 < npairs ? b1 : -1;
+            };
             KVPair bufA, bufB;
             if (npairs > 0) {
-                // The next pair's loads are issued unconditionally: past the last pair they load
-                // the current pair again (L2-hot, and dropped), so no branch separates a prefetch
-                // from the wait that precedes the computation of the pair before it.
+                // The next pair's loads are issued unconditionally: past the last pair they read
+                // the zero slab (and are dropped), so no branch separates a prefetch from the
+                // wait that precedes the computation of the pair before it.
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<POL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 while (true) {
-                    pair_ids(min(j + 1, npairs - 1), b0, b1);
-                    load_pair(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    next_ids(j, b0, b1);
+                    load_pair<POL>(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
                     compute(bufA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
-                    pair_ids(min(j + 1, npairs - 1), a0, a1);
-                    load_pair(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    next_ids(j, a0, a1);
+                    load_pair<POL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                     compute(bufB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
@@ -723,13 +732,20 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
         const bool rows16 = mfma_rows_per_group(a.rows_cap) == 16;
-        if (a.hpw == 2) {
-            if (rows16) attn_mfma_kernel<1, 2><<<grid, block, 0, stream>>>(a);
-            else attn_mfma_kernel<2, 2><<<grid, block, 0, stream>>>(a);
-        } else {
-            if (rows16) attn_mfma_kernel<1, 1><<<grid, block, 0, stream>>>(a);
-            else attn_mfma_kernel<2, 1><<<grid, block, 0, stream>>>(a);
+#define KYRO_MFMA_LAUNCH(POL)                                                           \
+        if (a.hpw == 2) {                                                               \
+            if (rows16) attn_mfma_kernel<1, 2, POL><<<grid, block, 0, stream>>>(a);     \
+            else attn_mfma_kernel<2, 2, POL><<<grid, block, 0, stream>>>(a);            \
+        } else {                                                                        \
+            if (rows16) attn_mfma_kernel<1, 1, POL><<<grid, block, 0, stream>>>(a);     \
+            else attn_mfma_kernel<2, 1, POL><<<grid, block, 0, stream>>>(a);            \
         }
+        if (a.stream_kv) {
+            KYRO_MFMA_LAUNCH(kLoadStream)
+        } else {
+            KYRO_MFMA_LAUNCH(kLoadCached)
+        }
+#undef KYRO_MFMA_LAUNCH
     } else {
         const bool bf16 = a.dtype_bf16;
         if (a.D == 128) {

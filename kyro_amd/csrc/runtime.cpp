@@ -304,6 +304,8 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: 64, 128)", p->head_dim);
         if (p->path < KYRO_ATTN_AUTO || p->path > KYRO_ATTN_MFMA)
             return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
+        if (p->kv_reuse < KYRO_KV_REUSE_AUTO || p->kv_reuse > KYRO_KV_REUSE_STREAM)
+            return fail(KYRO_EINVAL, "paged_attention: kv_reuse %d unknown", p->kv_reuse);
         if (p->batch_size == 0 || p->total_q == 0) return KYRO_OK;
         if (!query || !key_cache || !value_cache || !block_table || !context_lens || !out)
             return fail(KYRO_EINVAL, "paged_attention: null device pointer");
@@ -364,6 +366,9 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
                                                                     : kyro::kVectorRowsPerGroup;
         a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
+        // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
+        // of a kv head, or (as the caller says) other sequences holding the same blocks.
+        a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
 
         // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
         const int mb = std::max(1, p->max_blocks_per_seq);

@@ -38,7 +38,27 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().kyro_abi_version() == 6
+    text = open(os.path.join(ROOT, "include", "kyro_verify.h")).read()
+    declared = int(re.search(r"#define KYRO_ABI_VERSION (\d+)", text).group(1))
+    assert _lib.lib().kyro_abi_version() == declared == _lib.ABI_VERSION
+
+
+def struct_fields(name):
+    """Member names, in order, of `typedef struct name { ... } name;` in the headers."""
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        m = re.search(r"typedef struct " + name + r" \{(.*?)\} " + name + ";", text, flags=re.S)
+        if m:
+            return re.findall(r"([A-Za-z_][A-Za-z0-9_]*)\s*(?:\[[^]]*\])?\s*;", m.group(1))
+    raise AssertionError(f"{name} not declared")
+
+
+@pytest.mark.parametrize("cname, pyname", [
+    ("kyro_paged_attention_params", "PagedAttentionParams"), ("kyro_spec_verify_params", "SpecVerifyParams"),
+    ("kyro_kv_append_params", "KvAppendParams"), ("kyro_copy_blocks_params", "CopyBlocksParams"),
+    ("kyro_sample_params", "SampleParams")])
+def test_ctypes_structs_mirror_the_headers(cname, pyname):
+    assert [f[0] for f in getattr(_lib, pyname)._fields_] == struct_fields(cname)
 
 
 def test_null_context_is_einval():

@@ -121,6 +121,25 @@ def test_repeat_calls_are_bitwise_identical(gpu):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
+@pytest.mark.parametrize("q_len, gqa", [(8, (32, 8)), (9, (64, 8)), (3, (6, 3))])
+def test_kv_reuse_hint_never_changes_the_result(gpu, q_len, gqa):
+    """The hint only picks the K/V loads' cache policy: 32 rows per kv head (one row group,
+    streamed under "auto"), 72 rows (three row groups, cached under "auto"), and an odd kv head
+    count (one kv head per workgroup) with 6 rows; every hint gives the same bits."""
+    H, Hkv = gqa
+    case = wl.make_attention_case(context_lens=[700, 33, 2048, 16], q_lens=[q_len] * 4, num_heads=H,
+                                  num_kv_heads=Hkv, shared_prefix_blocks=2, seed=5)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, H, 128, Hkv)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    outs = {r: attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", kv_reuse=r)
+            for r in ("auto", "shared", "stream")}
+    assert torch.equal(outs["auto"], outs["shared"]) and torch.equal(outs["auto"], outs["stream"])
+    h.assert_attention_close(outs["auto"], case, h.oracle_attention(case, [0, 2]), h.ATOL_BF16)
+    with pytest.raises(KeyError):
+        attn.forward(*args, q_start_loc=t["q_start_loc"], kv_reuse="sometimes")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_cache_slots_past_the_context_are_never_used(gpu, dtype):
     """The slots after a sequence's last token in its last block, and every block no table

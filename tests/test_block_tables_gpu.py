@@ -31,8 +31,13 @@ def test_write_tables_matches_the_host_lists(gpu):
     order = list(rng.permutation(live))
     table = torch.full((len(order), 64), -7, dtype=torch.int64, device=gpu)
     lens = torch.full((len(order),), -7, dtype=torch.int64, device=gpu)
-    bm.write_tables(order, table, lens)
+    shared = bm.write_tables(order, table, lens)
     torch.cuda.synchronize()
+    blocks_of = [bm.request(rid)[0] for rid in order]
+    flat = [x for bl in blocks_of for x in bl]
+    assert shared == (len(flat) != len(set(flat)))
+    # one request alone never shares a block with another
+    assert bm.write_tables(order[:1], table[:1]) is False
     for b, rid in enumerate(order):
         blocks, n = bm.request(rid)
         row = table[b].cpu().numpy()
@@ -129,9 +134,11 @@ def test_serving_simulation_reads_back_every_requests_kv(gpu):
     B = len(rids)
     table = torch.zeros((B, 32), dtype=torch.int64, device=gpu)
     lens = torch.zeros((B,), dtype=torch.int64, device=gpu)
-    bm.write_tables(rids, table, lens)
+    shared = bm.write_tables(rids, table, lens)
     torch.cuda.synchronize()
     t_host = table.cpu().numpy()
+    flat = [x for rid in rids for x in bm.request(rid)[0]]
+    assert shared == (len(flat) != len(set(flat)))
     for b, rid in enumerate(rids):
         toks = live[rid]
         n = len(toks)
@@ -146,7 +153,7 @@ def test_serving_simulation_reads_back_every_requests_kv(gpu):
     # attention of one query per request through the device tables equals attention over the
     # request's own contiguous K/V
     q = rng.standard_normal((B, H, d), dtype=np.float32)
-    out = attn.forward(torch.from_numpy(q).to(gpu), kc, vc, table, lens)
+    out = attn.forward(torch.from_numpy(q).to(gpu), kc, vc, table, lens, kv_reuse="shared" if shared else "auto")
     for b, rid in enumerate(rids):
         toks = live[rid]
         n = len(toks)
