@@ -51,7 +51,8 @@ int main(void) {
     kyro_buf bq = upload(ctx, q, sizeof(q)), bk = upload(ctx, kc, sizeof(kc)), bv = upload(ctx, vc, sizeof(vc));
     kyro_buf bt = upload(ctx, table, sizeof(table)), bl = upload(ctx, lens, sizeof(lens)), bqs = upload(ctx, qs, sizeof(qs));
     kyro_buf bo = upload(ctx, NULL, sizeof(out));
-    kyro_paged_attention_params ap = {BS, H, D, HKV, B, TQ, MB, NB, KYRO_F32, KYRO_F32, 1, 0.f, KYRO_ATTN_AUTO, 0, 2};
+    kyro_paged_attention_params ap = {BS, H, D, HKV, B, TQ, MB, NB, KYRO_F32, KYRO_F32, 1, 0.f, KYRO_ATTN_AUTO, 0, 2,
+                                      KYRO_KV_REUSE_AUTO};
     CHECK(kyro_paged_attention_mq(ctx, &ap, kyro_buf_ptr(bq), kyro_buf_ptr(bqs), kyro_buf_ptr(bk), kyro_buf_ptr(bv),
                                   kyro_buf_ptr(bt), kyro_buf_ptr(bl), kyro_buf_ptr(bo)) == KYRO_OK, "attention");
     CHECK(kyro_buf_download(ctx, out, bo, 0, sizeof(out)) == KYRO_OK, "download");
