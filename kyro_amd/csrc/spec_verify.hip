@@ -5,19 +5,26 @@
 // first rejection, from p after full acceptance) and the greedy argmax-match rule of the reference
 // when T <= 0. Draws are sample_token's inverse-CDF walk in index order (src/worker.rs:352-360).
 //
-// Three stream-ordered kernels, sized so the dominant pass spreads over the whole chip:
-//   1. spec_stats_kernel     grid (sequence x vocab chunk, row): one streaming pass over every
-//                             needed logit row; per chunk {max, sum exp2((x - max) log2e / T)},
-//                             or {max, first argmax} for greedy rows, and the logit at the
-//                             row's draft token as it streams past. Draft rows of greedy
-//                             sequences and rows past a sequence's k are never read.
-//   2. spec_resample_kernel  grid (sequence x vocab chunk): wave 0 of every workgroup merges the
-//                             sequence's chunk statistics and runs the acceptance scan (lane i
-//                             tests u_i q_i(x_i) < p_i(x_i), a ballot finds the first rejection);
-//                             the chunk-0 workgroup stores the outputs. Then the workgroup sums the
-//                             residual (and p) mass of its chunk of the one row to resample.
-//   3. spec_pick_kernel      one workgroup per sequence: locates the chunk holding u * total with
-//                             a block scan of the chunk sums, then walks that chunk in index order.
+// Five stream-ordered kernels, sized so the streaming passes spread over the whole chip:
+//   1. spec_stats_kernel       grid (sequence x vocab chunk, window row): one streaming pass over
+//                               the rows of the first `win` draft positions; per chunk
+//                               {max, sum exp2((x - max) log2e / T)}, or {max, first argmax} for
+//                               greedy rows, and the logit at the row's draft token as it streams
+//                               past. Draft rows of greedy sequences and rows past k are never read.
+//   2. spec_decide_kernel      one wave per sequence: the acceptance scan over the window (lane i
+//                               tests u_i q_i(x_i) < p_i(x_i), a ballot finds the first rejection);
+//                               a sequence that accepted every window draft is left pending, with
+//                               the (row, chunk) items of its remaining rows.
+//   3. spec_stats_tail_kernel  the pending sequences' remaining rows, as in 1, over a fixed grid.
+//   4. spec_resample_kernel    grid (sequence x vocab chunk): a pending sequence's scan is finished
+//                               here (every workgroup; the chunk-0 one stores the outputs), then
+//                               each workgroup sums the residual (and p) mass of its chunk of the
+//                               row to resample.
+//   5. spec_pick_kernel        one workgroup per sequence: locates the chunk holding u * total with
+//                               a block scan of the chunk sums, then walks that chunk in index order.
+// The draw stays a launch of its own: handing the chunk sums to the last resample workgroup of a
+// sequence instead needs a device-scope release per workgroup, which on gfx950 writes back the
+// XCD's L2 (buffer_wbl2), and that took the sampler from 73 to 166 µs.
 // Right after the streaming pass every dependent global round trip costs microseconds (cold
 // caches and translations), so each kernel issues all loads that do not depend on another load
 // at entry, and acceptance is recomputed per workgroup rather than handed over by a launch.
