@@ -126,6 +126,23 @@ typedef enum kyro_kv_reuse {
     KYRO_KV_REUSE_STREAM = 2
 } kyro_kv_reuse;
 
+/* How the MFMA kernel spreads work over the chip. Results do not depend on it beyond float
+ * rounding of split merges.
+ *   AUTO:     BALANCED when num_splits is 0, the batch has at most 256 sequences and either
+ *             max_blocks_per_seq > 256 or GRID would split contexts; GRID otherwise.
+ *   GRID:     one workgroup per (sequence, kv head pair, context split, row group), with
+ *             num_splits splits of max_blocks_per_seq (0: chosen from the shapes alone).
+ *   BALANCED: a persistent grid of one workgroup per CU reads the context lengths on the
+ *             device, splits only sequences longer than the per-CU share of the work, and starts
+ *             the longest work items first (at most 256 sequences, num_splits must be 0; an
+ *             extra combine launch always follows). For batches whose context lengths differ
+ *             widely. */
+typedef enum kyro_attn_schedule {
+    KYRO_ATTN_SCHEDULE_AUTO = 0,
+    KYRO_ATTN_SCHEDULE_GRID = 1,
+    KYRO_ATTN_SCHEDULE_BALANCED = 2
+} kyro_attn_schedule;
+
 /* Mirrors PagedAttention { block_size, num_heads, head_dim, num_kv_heads }
  * (src/model/attention_kernel.rs:4-9) plus the shapes the Rust side reads off its tensors. */
 typedef struct kyro_paged_attention_params {
@@ -148,6 +165,7 @@ typedef struct kyro_paged_attention_params {
                                     q_start_loc, total_q with it (sizes the split workspace;
                                     a sequence above it latches KYRO_EINVAL) */
     int32_t kv_reuse;            /* kyro_kv_reuse (0 => AUTO) */
+    int32_t schedule;            /* kyro_attn_schedule (0 => AUTO); MFMA kernel only */
 } kyro_paged_attention_params;
 
 /*

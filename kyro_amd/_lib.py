@@ -16,6 +16,7 @@ KYRO_OK, KYRO_EINVAL, KYRO_EOOM, KYRO_EHIP, KYRO_EUNSUPPORTED, KYRO_ENOSPACE = 0
 KYRO_F32, KYRO_BF16 = 0, 1
 KYRO_ATTN_AUTO, KYRO_ATTN_VECTOR, KYRO_ATTN_MFMA = 0, 1, 2
 KYRO_KV_REUSE_AUTO, KYRO_KV_REUSE_SHARED, KYRO_KV_REUSE_STREAM = 0, 1, 2
+KYRO_ATTN_SCHEDULE_AUTO, KYRO_ATTN_SCHEDULE_GRID, KYRO_ATTN_SCHEDULE_BALANCED = 0, 1, 2
 
 _STATUS_NAMES = {0: "KYRO_OK", 1: "KYRO_EINVAL", 2: "KYRO_EOOM", 3: "KYRO_EHIP", 4: "KYRO_EUNSUPPORTED",
                  5: "KYRO_ENOSPACE"}
@@ -39,6 +40,7 @@ class PagedAttentionParams(ctypes.Structure):
         ("causal", ctypes.c_int32), ("scale", ctypes.c_float),
         ("path", ctypes.c_int32), ("num_splits", ctypes.c_int32),
         ("max_q_len", ctypes.c_int32), ("kv_reuse", ctypes.c_int32),
+        ("schedule", ctypes.c_int32),
     ]
 
 

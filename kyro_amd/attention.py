@@ -26,6 +26,8 @@ _DTYPES = {torch.float32: _lib.KYRO_F32, torch.bfloat16: _lib.KYRO_BF16}
 _PATHS = {"auto": _lib.KYRO_ATTN_AUTO, "vector": _lib.KYRO_ATTN_VECTOR, "mfma": _lib.KYRO_ATTN_MFMA}
 _KV_REUSE = {"auto": _lib.KYRO_KV_REUSE_AUTO, "shared": _lib.KYRO_KV_REUSE_SHARED,
              "stream": _lib.KYRO_KV_REUSE_STREAM}
+_SCHEDULES = {"auto": _lib.KYRO_ATTN_SCHEDULE_AUTO, "grid": _lib.KYRO_ATTN_SCHEDULE_GRID,
+              "balanced": _lib.KYRO_ATTN_SCHEDULE_BALANCED}
 
 
 def _require(t: torch.Tensor, name: str, dtype=None, ndim=None, device=None):
@@ -52,7 +54,7 @@ class PagedAttention:
 
     def forward(self, query, key_cache, value_cache, block_table, context_lens, *,
                 q_start_loc=None, max_q_len=None, causal=True, out_dtype=torch.float32,
-                path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto"):
+                path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto", schedule="auto"):
         """Attention of every query row against its sequence's paged context.
 
         ``q_start_loc`` (int32 [batch+1]) gives each sequence's rows of ``query``; ``max_q_len``
@@ -60,7 +62,9 @@ class PagedAttention:
         cache-policy hint for the K/V loads that never changes the result: "auto" streams them
         when each cached slab is read once per launch, "shared" keeps them cacheable for tables
         that share blocks between sequences (``BlockManager.write_tables`` reports that),
-        "stream" streams them regardless. The call
+        "stream" streams them regardless. ``schedule`` ("auto", "grid", "balanced") chooses how
+        the MFMA kernel spreads work over the chip: "balanced" reads the context lengths on the
+        device and starts the longest work first (for batches of very different lengths). The call
         synchronises, so errors the device detects (bad block ids, context lengths beyond the
         table) raise KyroError here, as the reference returns Err from ``forward``;
         :meth:`forward_async` is the non-blocking variant.
@@ -68,13 +72,13 @@ class PagedAttention:
         out = self.forward_async(query, key_cache, value_cache, block_table, context_lens,
                                  q_start_loc=q_start_loc, max_q_len=max_q_len, causal=causal,
                                  out_dtype=out_dtype, path=path, num_splits=num_splits,
-                                 scale=scale, out=out, kv_reuse=kv_reuse)
+                                 scale=scale, out=out, kv_reuse=kv_reuse, schedule=schedule)
         _lib.context(query.device.index or 0).sync()
         return out
 
     def forward_async(self, query, key_cache, value_cache, block_table, context_lens, *,
                       q_start_loc=None, max_q_len=None, causal=True, out_dtype=torch.float32,
-                      path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto"):
+                      path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto", schedule="auto"):
         """Queues the kernel on torch's current stream and returns without synchronising.
         Device-detected errors surface at the next ``kyro_amd.sync(device)``."""
         dev = query.device
@@ -120,7 +124,7 @@ class PagedAttention:
             self.block_size, self.num_heads, self.head_dim, self.num_kv_heads, batch, total_q,
             block_table.shape[1], nb, _DTYPES[query.dtype], _DTYPES[out_dtype], 1 if causal else 0,
             float(scale) if scale else 0.0, _PATHS[path], int(num_splits), int(max_q_len),
-            _KV_REUSE[kv_reuse])
+            _KV_REUSE[kv_reuse], _SCHEDULES[schedule])
         ctx = _lib.context(dev.index or 0)
         ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(_lib.lib().kyro_paged_attention_mq(

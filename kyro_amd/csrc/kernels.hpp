@@ -49,9 +49,34 @@ struct AttnArgs {
     int hpw;           // kv heads (units) per workgroup: 2 in the MFMA kernel when Hkv is even
     int ugroups;       // units / hpw
     int ugroups_padded;  // ugroups rounded up to a multiple of 8 (the XCD count)
-    int row_groups;
-    int stream_kv;     // MFMA kernel: K/V loads with kLoadStream (1) or kLoadCached (0)  // workgroups per (unit group, split), each covering rows_per_group rows
+    int row_groups;    // workgroups per (unit group, split), each covering rows_per_group rows
+    int stream_kv;     // MFMA kernel: K/V loads with kLoadStream (1) or kLoadCached (0)
+    // Balanced schedule (MFMA kernel, automatic splits): a persistent grid of plan_grid
+    // workgroups computes per-sequence splits from the context lengths and walks the work items
+    // largest first. Partial states live in per-item slots of plan_rw rows per kv head;
+    // plan_seq[b] = {splits, row groups, first slot, 0} tells the combine pass where.
+    int plan;
+    int plan_grid;
+    int plan_rw;
+    int plan_max_chunk;
+    int4* plan_seq;
 };
+
+// Sequences one balanced-schedule launch can plan (one per thread of a workgroup).
+constexpr int kPlanMaxSeqs = 256;
+// Shortest split the balanced schedule makes, in blocks.
+constexpr int kPlanMinChunk = 16;
+
+// Upper bound on the partial-state slots of a balanced-schedule launch: the per-sequence
+// chunk is at least half the per-workgroup share of the work (or the longest chunk allowed),
+// so the splits number at most 2 x grid (or work / max_chunk) plus one per (kv head group,
+// row group) of every sequence.
+inline long long plan_slot_bound(long long B, long long ugroups_per_seq, long long row_groups, long long max_blocks,
+                                 long long max_chunk, long long grid) {
+    const long long s = B * ugroups_per_seq * row_groups;
+    const long long by_chunk = (s * max_blocks + max_chunk - 1) / max_chunk;
+    return s + (by_chunk > 2 * grid ? by_chunk : 2 * grid);
+}
 
 // Block pairs one MFMA wave can hold the ids of (two 64-lane slots). A split has at most
 // 2 * kMfmaMaxPairsPerWave * (kernel waves per head) blocks.

@@ -131,10 +131,11 @@ struct Frame {
 };
 
 // After every wave has added its rescaled accumulator: either normalise and store the rows
-// (single split) or park the split's partial state in the workspace.
+// (single split) or park the split's partial state in the workspace, local row n at workspace
+// row pbase + n.
 template <int R, int D>
-__device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int split, int nsplit,
-                            int row0, int nrows, Frame<R, D>& f, int nslots = kWaves) {
+__device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int nsplit, int row0, int nrows,
+                            Frame<R, D>& f, int nslots, size_t pbase) {
     constexpr int Q = D / 4;
     if (nsplit == 1) {
         for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
@@ -148,55 +149,83 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int unit, int 
         }
         return;
     }
-    const size_t base = ((size_t)unit * a.splits + split) * a.rows_cap;
     for (int n = threadIdx.x; n < nrows; n += kThreads) {
         float L = 0.f;
         for (int w = 0; w < nslots; ++w) L += f.l[w][n];
-        a.ws_m[base + row0 + n] = f.mx[n];
-        a.ws_l[base + row0 + n] = L;
+        a.ws_m[pbase + n] = f.mx[n];
+        a.ws_l[pbase + n] = L;
     }
     for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
         const int n = idx / Q, d = (idx - n * Q) * 4;
         const float* src = &f.acc[n * Frame<R, D>::kStride + d];
-        *reinterpret_cast<float4*>(a.ws_acc + (base + row0 + n) * D + d) =
-            make_float4(src[0], src[1], src[2], src[3]);
+        *reinterpret_cast<float4*>(a.ws_acc + (pbase + n) * D + d) = make_float4(src[0], src[1], src[2], src[3]);
     }
 }
 
 // Second pass for multi-split units: merges the parked partial states of every split of one
-// (sequence, kv head) and writes the normalised rows. One workgroup per unit; units whose
-// sequence needed a single split were stored directly by the first pass and exit here.
+// (sequence, kv head) and writes the normalised rows. The grid is (unit, block of rows): a
+// workgroup takes kThreads / (D / 4) rows of one unit, a thread one 4-float column of one row;
+// units whose sequence needed a single split were stored directly by the first pass and exit
+// here. The split loops are unrolled so that their loads are issued together.
+//
+// Under the balanced schedule the split count and the slots come from plan_seq (written by the
+// first pass): split s of row n (row group n / plan_rw) of kv head h sits in slot
+// first + (s * ugroups_per_seq + h / hpw) * row_groups + n / plan_rw, head h % hpw.
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
+    constexpr int Q = D / 4;
+    constexpr int RPW = kThreads / Q;  // rows per workgroup
     const int unit = blockIdx.x;
     if (unit >= a.units) return;
     const SeqInfo si = seq_info(a, unit);
     if (!si.ok) return;
-    const int nsplit = num_splits_for(a, si.nblk);
-    if (nsplit <= 1) return;
-    constexpr int Q = D / 4;
-    const size_t base = (size_t)unit * a.splits * a.rows_cap;
-    for (int idx = threadIdx.x; idx < si.rows * Q; idx += kThreads) {
-        const int n = idx / Q, d = (idx - n * Q) * 4;
-        float M = kNegInf;
-        for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_m[base + (size_t)s * a.rows_cap + n]);
-        float L = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (M != kNegInf) {
-            for (int s = 0; s < nsplit; ++s) {
-                const size_t r = base + (size_t)s * a.rows_cap + n;
-                const float w = fast_exp2(a.ws_m[r] - M);
-                L += w * a.ws_l[r];
-                const float4 v = *reinterpret_cast<const float4*>(a.ws_acc + r * D + d);
-                acc.x += w * v.x;
-                acc.y += w * v.y;
-                acc.z += w * v.z;
-                acc.w += w * v.w;
-            }
-        }
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    const int n = blockIdx.y * RPW + (int)threadIdx.x / Q;
+    if (n >= si.rows) return;
+    int nsplit, nrg = 0, first = 0;
+    if (a.plan) {
+        const int4 ps = a.plan_seq[si.b];
+        nsplit = ps.x;
+        nrg = ps.y;
+        first = ps.z;
+        if (nrg <= 0) return;
+    } else {
+        nsplit = num_splits_for(a, si.nblk);
     }
+    if (nsplit <= 1) return;
+    const int d = ((int)threadIdx.x % Q) * 4;
+    // Workspace row of split s, local row n of this unit: consecutive splits are `stride` rows
+    // apart.
+    size_t r0, stride;
+    if (a.plan) {
+        const int upseq = a.ugroups / a.B;
+        const int rg = n / a.plan_rw;
+        const size_t slot = (size_t)first + (size_t)(si.kvh / a.hpw) * nrg + rg;
+        r0 = (slot * a.hpw + si.kvh % a.hpw) * a.plan_rw + (n - rg * a.plan_rw);
+        stride = (size_t)upseq * nrg * a.hpw * a.plan_rw;
+    } else {
+        r0 = (size_t)unit * a.splits * a.rows_cap + n;
+        stride = a.rows_cap;
+    }
+    float M = kNegInf;
+#pragma unroll 8
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_m[r0 + s * stride]);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (M != kNegInf) {
+#pragma unroll 4
+        for (int s = 0; s < nsplit; ++s) {
+            const size_t r = r0 + s * stride;
+            const float w = fast_exp2(a.ws_m[r] - M);
+            L += w * a.ws_l[r];
+            const float4 v = *reinterpret_cast<const float4*>(a.ws_acc + r * D + d);
+            acc.x += w * v.x;
+            acc.y += w * v.y;
+            acc.z += w * v.z;
+            acc.w += w * v.w;
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 // ------------------------------------------------------------------------------ MFMA kernel
@@ -260,6 +289,222 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
     __syncthreads();
 }
 
+// ------------------------------------------------------------------------ balanced schedule
+//
+// Under automatic splits every workgroup of the MFMA launch reads all context lengths and derives
+// the same plan in LDS (no extra launch and no host round trip):
+//  * work of sequence b: W_b = kv head groups x row groups x blocks; per-workgroup share
+//    L = ceil(sum W / grid);
+//  * chunk C = L when no sequence is longer than L (nothing splits, so a uniform batch keeps one
+//    item per (sequence, kv head group)), else ceil(L / 2), within [kPlanMinChunk, max chunk];
+//    a longer sequence splits into equal even chunks;
+//  * sequences are ordered by chunk length, longest first (lower index first among equals), so
+//    the longest items start first;
+//  * item groups (sequence, chunk, kv head group) are dealt round-robin to 8 lanes, one per XCD;
+//    the row groups of an item group take consecutive positions of one lane (item indices 8
+//    apart), so they run together on one XCD and share its L2;
+//  * workgroup w takes item w of every band of `grid` items, from the other end in odd bands,
+//    which evens out the workgroups' totals.
+struct PlanLds {
+    alignas(16) uint32_t key[kPlanMaxSeqs];  // by sequence: (chunk << 16) | (0xffff - b); larger first
+    int b[kPlanMaxSeqs];         // the rest by position in that order
+    int ns[kPlanMaxSeqs];        // splits
+    int ch[kPlanMaxSeqs];        // blocks per split
+    int r[kPlanMaxSeqs];         // row groups (0: no work)
+    int ctx[kPlanMaxSeqs];
+    int q0[kPlanMaxSeqs];
+    int qlen[kPlanMaxSeqs];
+    int g0[kPlanMaxSeqs];        // first item group
+    int slot0[kPlanMaxSeqs];     // first partial-state slot
+    int lane0[8][kPlanMaxSeqs];  // items of earlier sequences on each lane
+    int lane_len[8];
+    int red[kWaves][9];
+    long long red64[kWaves];
+};
+static_assert(kPlanMaxSeqs == kThreads, "plan_build reads one sequence per thread");
+
+// Exclusive prefix sums of V values per thread over the workgroup's threads; total[] gets the
+// sums. `red` is LDS scratch.
+template <int V>
+__device__ __forceinline__ void block_scan_excl(int (&v)[V], int (&total)[V], int (*red)[9]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        int x = v[j];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        incl[j] = x;
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) red[wave][j] = incl[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        int before = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            before += w < wave ? red[w][j] : 0;
+            tot += red[w][j];
+        }
+        v[j] = incl[j] - v[j] + before;
+        total[j] = tot;
+    }
+    __syncthreads();
+}
+
+// Builds the plan (every thread of the workgroup takes part; thread t reads sequence t).
+// Returns the number of item positions (8 x the longest lane). Workgroup 0 latches input
+// errors and publishes {splits, row groups, first slot} per sequence for the combine pass.
+template <int RW, int HP>
+__device__ int plan_build(const AttnArgs& a, PlanLds& P) {
+    const int t = threadIdx.x;
+    const int wave = t >> 6;
+    const int U = a.Hkv / HP;
+    int ctx = 0, q0 = 0, qlen = 0, r = 0, nb = 0;
+    if (t < a.B) {
+        const int64_t c = a.ctx_lens[t];
+        int s0 = t, s1 = t + 1;
+        if (a.q_start) {
+            s0 = a.q_start[t];
+            s1 = a.q_start[t + 1];
+        }
+        bool ok = true;
+        if (c < 0 || c > (int64_t)a.max_blocks * a.bs) {
+            ok = false;
+            if (blockIdx.x == 0) latch_error(a.err, ERR_CTX_LEN);
+        }
+        if (s0 < 0 || s1 < s0 || s1 > a.total_q || s1 - s0 > a.max_q_len) {
+            ok = false;
+            if (blockIdx.x == 0) latch_error(a.err, ERR_Q_LAYOUT);
+        }
+        if (ok) {
+            ctx = (int)c;
+            q0 = s0;
+            qlen = s1 - s0;
+            r = (qlen * a.group + RW - 1) / RW;
+            nb = (ctx + a.bs - 1) / a.bs;
+        }
+    }
+    // Total work and the longest sequence that has rows.
+    long long w = (long long)U * r * nb;
+    int mx = r > 0 ? nb : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        w += __shfl_xor(w, o, 64);
+        mx = max(mx, __shfl_xor(mx, o, 64));
+    }
+    if ((t & 63) == 0) {
+        P.red64[wave] = w;
+        P.red[wave][0] = mx;
+    }
+    __syncthreads();
+    long long T = 0;
+    int maxnb = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        T += P.red64[i];
+        maxnb = max(maxnb, P.red[i][0]);
+    }
+    const long long L = (T + a.plan_grid - 1) / a.plan_grid;
+    long long C = maxnb <= L ? L : (L + 1) / 2;
+    C = C < kPlanMinChunk ? kPlanMinChunk : C;
+    C = (C + 1) & ~1ll;
+    C = C > a.plan_max_chunk ? a.plan_max_chunk : C;
+    int ns = 1, ch = nb;
+    if (nb > C) {
+        ns = (int)((nb + C - 1) / C);
+        ch = (nb + ns - 1) / ns;
+        ch = (ch + 1) & ~1;
+        ns = (nb + ch - 1) / ch;
+    }
+    const uint32_t key = ((uint32_t)(r > 0 ? ch : 0) << 16) | (uint32_t)(0xffff - t);
+    P.key[t] = t < a.B ? key : 0u;  // padding keys rank below every sequence
+    __syncthreads();
+    if (t < a.B) {
+        // Rank = number of larger keys: four keys per LDS read, reads issued together.
+        int rank = 0;
+        const uint4* k4 = reinterpret_cast<const uint4*>(P.key);
+#pragma unroll 4
+        for (int j = 0; j < (a.B + 3) / 4; ++j) {
+            const uint4 k = k4[j];
+            rank += (k.x > key ? 1 : 0) + (k.y > key ? 1 : 0) + (k.z > key ? 1 : 0) + (k.w > key ? 1 : 0);
+        }
+        P.b[rank] = t;
+        P.ns[rank] = ns;
+        P.ch[rank] = ch;
+        P.r[rank] = r;
+        P.ctx[rank] = ctx;
+        P.q0[rank] = q0;
+        P.qlen[rank] = qlen;
+    }
+    __syncthreads();
+    // Item groups and slots in that order; each sequence's item groups dealt to the 8 lanes.
+    int rp = 0, nig = 0;
+    if (t < a.B) {
+        rp = P.r[t];
+        nig = rp > 0 ? U * P.ns[t] : 0;
+    }
+    int sa[1] = {nig}, ta[1];
+    block_scan_excl<1>(sa, ta, P.red);
+    const int g0 = sa[0];
+    int sb[9], tb[9];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) sb[x] = ((g0 + nig + 7 - x) / 8 - (g0 + 7 - x) / 8) * rp;
+    sb[8] = nig * rp;
+    block_scan_excl<9>(sb, tb, P.red);
+    if (t < a.B) {
+        P.g0[t] = g0;
+        P.slot0[t] = sb[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) P.lane0[x][t] = sb[x];
+        if (blockIdx.x == 0) a.plan_seq[P.b[t]] = make_int4(P.ns[t], rp, sb[8], 0);
+    }
+    if (t < 8) P.lane_len[t] = tb[t];
+    int longest = 0;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) longest = max(longest, tb[x]);
+    __syncthreads();
+    return 8 * longest;
+}
+
+struct PlanItem {
+    int p;      // position of the sequence in the plan order
+    int hp;     // kv head group within the sequence
+    int rg;     // row group
+    int chunk;  // split
+    int slot;   // partial-state slot
+};
+
+// Item position i of the plan, or false for an empty position of a short lane.
+template <int HP>
+__device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, int i, PlanItem& it) {
+    const int x = i & 7, k = i >> 3;
+    if (k >= P.lane_len[x]) return false;
+    int lo = 0, hi = a.B - 1;  // the last sequence whose lane-x items start at or before k
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (P.lane0[x][mid] <= k) lo = mid;
+        else hi = mid - 1;
+    }
+    const int rr = P.r[lo];
+    const int idx = k - P.lane0[x][lo];
+    const int igl = idx / rr;
+    const int q = ((x - P.g0[lo]) & 7) + 8 * igl;  // item group within the sequence
+    const int U = a.Hkv / HP;
+    it.p = lo;
+    it.rg = idx - igl * rr;
+    it.chunk = q / U;
+    it.hp = q - it.chunk * U;
+    it.slot = P.slot0[lo] + q * rr + it.rg;
+    return true;
+}
+
 // A workgroup covers NTW 16-row tiles of its unit's rows (NTW 1 or 2: the accumulators of two
 // tiles plus two K/V pair buffers fill the register file without spills); units with more rows
 // (a large GQA group times many draft positions) get one workgroup per 32-row group.
@@ -269,34 +514,25 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 // V), and a batch with 2 x 256 units runs as one round of workgroups on 256 CUs instead of two.
 // POL is the cache policy of the K/V loads: kLoadStream when no other workgroup reads the same
 // slabs (the host decides), kLoadCached otherwise.
+//
+// mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
+// head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
+// workspace rows pb0 + h * pbstep + n for head h of the group.
 template <int NTW, int HP, int POL>
-__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+__device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
+                                          const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
+                                          int nsplit, size_t pb0, size_t pbstep) {
     constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
     constexpr int WPH = kWaves / HP;  // waves per kv head
-    __shared__ Frame<RW, D> frame[HP];
-    __shared__ int s_blk[kMaxChunkBlocks];
-
-    int ug, split, rg;
-    if (!map_workgroup(a, ug, split, rg)) return;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int hw = wave / WPH;  // this wave's kv head within the group
     const int wp = wave % WPH;  // and its place among that head's waves
-    const int unit = ug * HP + hw;
-    // The group's units belong to one sequence, so everything but the kv head is the same for
-    // every wave, and the early returns below are taken by the whole workgroup or by none of it.
-    const SeqInfo si = seq_info(a, unit);
-    if (!si.ok) return;
-    const int nsplit = num_splits_for(a, si.nblk);
-    if (split >= nsplit) return;
     const int row0 = rg * RW;
-    if (row0 > 0 && row0 >= si.rows) return;  // this row group is past the sequence's rows
 
     const int lane = threadIdx.x & 63;
     const int r = lane & 15;  // MFMA row/column within a 16-tile
     const int g = lane >> 4;  // 16-lane group
-    const int blk_begin = split * a.chunk_blocks;
-    const int blk_end = min(si.nblk, blk_begin + a.chunk_blocks);
     const uint16_t* __restrict__ qp = reinterpret_cast<const uint16_t*>(a.q);
     const uint16_t* __restrict__ kp = reinterpret_cast<const uint16_t*>(a.k);
     const uint16_t* __restrict__ vp = reinterpret_cast<const uint16_t*>(a.v);
@@ -536,10 +772,71 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
         for (int h = 0; h < HP; ++h) {  // the whole workgroup stores each head's rows
             SeqInfo sh = si;
             sh.kvh = (ug * HP + h) % a.Hkv;
-            frame_flush<RW, D>(a, sh, ug * HP + h, split, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH);
+            frame_flush<RW, D>(a, sh, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH, pb0 + h * pbstep);
         }
     }
 }
+
+// PLAN: the balanced schedule (a persistent grid walking the plan's items) or one workgroup per
+// (kv head group, split, row group) of the grid schedule.
+template <int NTW, int HP, int POL, bool PLAN>
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+    constexpr int RW = NTW * 16;
+    constexpr int WPH = kWaves / HP;
+    __shared__ Frame<RW, kMfmaD> frame[HP];
+    __shared__ int s_blk[kMaxChunkBlocks];
+    const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / WPH;
+
+    if constexpr (PLAN) {
+        __shared__ PlanLds plan;
+        const int items = plan_build<RW, HP>(a, plan);
+        const int G = a.plan_grid;
+        const int U = a.Hkv / HP;
+        for (int base = 0, band = 0; base < items; base += G, ++band) {
+            const int i = base + ((band & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
+            PlanItem it;
+            const bool has = i < items && plan_item<HP>(a, plan, i, it);
+            if (!__builtin_amdgcn_readfirstlane(has ? 1 : 0)) continue;  // same for every lane
+            // Plan values come from LDS: make them scalar for the addressing that follows.
+            const int p = __builtin_amdgcn_readfirstlane(it.p);
+            const int hp = __builtin_amdgcn_readfirstlane(it.hp);
+            const int rg = __builtin_amdgcn_readfirstlane(it.rg);
+            const int chunk = __builtin_amdgcn_readfirstlane(it.chunk);
+            const int slot = __builtin_amdgcn_readfirstlane(it.slot);
+            SeqInfo si;
+            si.b = __builtin_amdgcn_readfirstlane(plan.b[p]);
+            si.kvh = hp * HP + hw;
+            si.ctx = __builtin_amdgcn_readfirstlane(plan.ctx[p]);
+            si.q0 = __builtin_amdgcn_readfirstlane(plan.q0[p]);
+            si.q_len = __builtin_amdgcn_readfirstlane(plan.qlen[p]);
+            si.rows = si.q_len * a.group;
+            si.nblk = (si.ctx + a.bs - 1) / a.bs;
+            si.ok = true;
+            const int ch = __builtin_amdgcn_readfirstlane(plan.ch[p]);
+            const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[p]);
+            const int blk_begin = chunk * ch;
+            const int blk_end = min(si.nblk, blk_begin + ch);
+            mfma_item<NTW, HP, POL>(a, frame, s_blk, si, si.b * U + hp, rg, blk_begin, blk_end, nsplit,
+                                    (size_t)slot * HP * RW, RW);
+        }
+    } else {
+    int ug, split, rg;
+    if (!map_workgroup(a, ug, split, rg)) return;
+    // The group's units belong to one sequence, so everything but the kv head is the same for
+    // every wave, and the early returns below are taken by the whole workgroup or by none of it.
+    const SeqInfo si = seq_info(a, ug * HP + hw);
+    if (!si.ok) return;
+    const int nsplit = num_splits_for(a, si.nblk);
+    if (split >= nsplit) return;
+    if (rg > 0 && rg * RW >= si.rows) return;  // this row group is past the sequence's rows
+    const int blk_begin = split * a.chunk_blocks;
+    const int blk_end = min(si.nblk, blk_begin + a.chunk_blocks);
+    mfma_item<NTW, HP, POL>(a, frame, s_blk, si, ug, rg, blk_begin, blk_end, nsplit,
+                            ((size_t)ug * HP * a.splits + split) * a.rows_cap + rg * RW,
+                            (size_t)a.splits * a.rows_cap);
+    }
+}
+
 
 // ---------------------------------------------------------------------------- vector kernel
 
@@ -718,7 +1015,8 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
             }
             __syncthreads();
         }
-        frame_flush<R, D>(a, si, unit, split, nsplit, row0, nrows > 0 ? nrows : 0, frame);
+        frame_flush<R, D>(a, si, nsplit, row0, nrows > 0 ? nrows : 0, frame, kWaves,
+                          ((size_t)unit * a.splits + split) * a.rows_cap + row0);
     }
 }
 
@@ -728,22 +1026,30 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 
 hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t stream) {
     const dim3 block(kThreads);
-    const dim3 grid((unsigned)(a.ugroups_padded * a.splits * a.row_groups));
+    const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
         const bool rows16 = mfma_rows_per_group(a.rows_cap) == 16;
-#define KYRO_MFMA_LAUNCH(POL)                                                           \
-        if (a.hpw == 2) {                                                               \
-            if (rows16) attn_mfma_kernel<1, 2, POL><<<grid, block, 0, stream>>>(a);     \
-            else attn_mfma_kernel<2, 2, POL><<<grid, block, 0, stream>>>(a);            \
-        } else {                                                                        \
-            if (rows16) attn_mfma_kernel<1, 1, POL><<<grid, block, 0, stream>>>(a);     \
-            else attn_mfma_kernel<2, 1, POL><<<grid, block, 0, stream>>>(a);            \
+#define KYRO_MFMA_LAUNCH(POL, PLAN)                                                           \
+        if (a.hpw == 2) {                                                                     \
+            if (rows16) attn_mfma_kernel<1, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);     \
+            else attn_mfma_kernel<2, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);            \
+        } else {                                                                              \
+            if (rows16) attn_mfma_kernel<1, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);     \
+            else attn_mfma_kernel<2, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);            \
         }
-        if (a.stream_kv) {
-            KYRO_MFMA_LAUNCH(kLoadStream)
+        if (a.plan) {
+            if (a.stream_kv) {
+                KYRO_MFMA_LAUNCH(kLoadStream, true)
+            } else {
+                KYRO_MFMA_LAUNCH(kLoadCached, true)
+            }
         } else {
-            KYRO_MFMA_LAUNCH(kLoadCached)
+            if (a.stream_kv) {
+                KYRO_MFMA_LAUNCH(kLoadStream, false)
+            } else {
+                KYRO_MFMA_LAUNCH(kLoadCached, false)
+            }
         }
 #undef KYRO_MFMA_LAUNCH
     } else {
@@ -756,8 +1062,9 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
             else attn_vector_kernel<float, 64><<<grid, block, 0, stream>>>(a);
         }
     }
-    if (a.splits > 1) {
-        const dim3 cgrid((unsigned)a.units);
+    if (a.plan || a.splits > 1) {
+        const int rpw = kThreads / (a.D / 4);
+        const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
         if (a.D == 128) attn_combine_kernel<128><<<cgrid, block, 0, stream>>>(a);
         else attn_combine_kernel<64><<<cgrid, block, 0, stream>>>(a);
     }

@@ -306,6 +306,13 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
         if (p->kv_reuse < KYRO_KV_REUSE_AUTO || p->kv_reuse > KYRO_KV_REUSE_STREAM)
             return fail(KYRO_EINVAL, "paged_attention: kv_reuse %d unknown", p->kv_reuse);
+        if (p->schedule < KYRO_ATTN_SCHEDULE_AUTO || p->schedule > KYRO_ATTN_SCHEDULE_BALANCED)
+            return fail(KYRO_EINVAL, "paged_attention: schedule %d unknown", p->schedule);
+        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->num_splits != 0)
+            return fail(KYRO_EINVAL, "paged_attention: the balanced schedule chooses its own splits (num_splits must be 0)");
+        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->batch_size > kyro::kPlanMaxSeqs)
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule plans at most %d sequences",
+                        kyro::kPlanMaxSeqs);
         if (p->batch_size == 0 || p->total_q == 0) return KYRO_OK;
         if (!query || !key_cache || !value_cache || !block_table || !context_lens || !out)
             return fail(KYRO_EINVAL, "paged_attention: null device pointer");
@@ -329,6 +336,9 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         } else {
             kernel = (mfma_ok && group * max_q_len >= 4) ? kyro::ATTN_KERNEL_MFMA : kyro::ATTN_KERNEL_VECTOR;
         }
+        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
+                        "(bf16, head_dim 128, block_size 16)");
 
         kyro::AttnArgs a{};
         a.q = query;
@@ -397,15 +407,43 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         splits = (mb + chunk - 1) / chunk;
         a.splits = splits;
         a.chunk_blocks = chunk;
+        // The balanced schedule: asked for, or where the grid's splits (from the table width
+        // alone) would have to guess at the context lengths: a split grid, or a table wider than
+        // 256 blocks (4096 tokens), where a few long sequences can leave one workgroup streaming
+        // long after the rest of the chip is idle.
+        a.plan = kernel == kyro::ATTN_KERNEL_MFMA && p->num_splits == 0 && p->batch_size <= kyro::kPlanMaxSeqs &&
+                 (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED ||
+                  (p->schedule == KYRO_ATTN_SCHEDULE_AUTO && (splits > 1 || mb > 256)));
+        size_t plan_slots = 0;
+        if (a.plan) {
+            constexpr int kCUs = 256;
+            a.plan_grid = kCUs;
+            a.plan_rw = rows_per_group;
+            a.plan_max_chunk = max_chunk / 2 * 2;
+            a.splits = 1;
+            plan_slots = (size_t)kyro::plan_slot_bound(a.B, a.ugroups / a.B, a.row_groups, mb, a.plan_max_chunk,
+                                                       a.plan_grid);
+        }
         // One launch carries at most 2^32 - 1 work items along x.
-        if ((uint64_t)a.ugroups_padded * splits * a.row_groups * 256 > 0xffffffffull)
+        if (!a.plan && (uint64_t)a.ugroups_padded * splits * a.row_groups * 256 > 0xffffffffull)
             return fail(KYRO_EUNSUPPORTED, "paged_attention: %d units x %d splits x %d row groups is too large for one launch",
                         a.units, splits, a.row_groups);
 
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
         size_t ws_bytes = 0;
-        if (splits > 1) {
+        if (a.plan) {
+            const size_t rows = plan_slots * a.hpw * a.plan_rw;
+            const size_t mb_bytes = align_up(rows * sizeof(float), 256);
+            ws_bytes = 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256) +
+                       align_up((size_t)a.B * sizeof(int4), 256);
+            if (int rc = ensure_arena(ctx, ws_bytes)) return rc;
+            char* base = static_cast<char*>(ctx->arena);
+            a.ws_m = reinterpret_cast<float*>(base);
+            a.ws_l = reinterpret_cast<float*>(base + mb_bytes);
+            a.ws_acc = reinterpret_cast<float*>(base + 2 * mb_bytes);
+            a.plan_seq = reinterpret_cast<int4*>(base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256));
+        } else if (splits > 1) {
             const size_t rows = (size_t)a.units * splits * a.rows_cap;
             ws_bytes = align_up(rows * sizeof(float), 256) * 2 + align_up(rows * a.D * sizeof(float), 256);
             if (int rc = ensure_arena(ctx, ws_bytes)) return rc;

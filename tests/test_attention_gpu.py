@@ -185,6 +185,80 @@ def test_long_context_in_one_split(gpu):
         h.assert_attention_close(out, case, exp, h.ATOL_BF16)
 
 
+# ------------------------------------------------------------------ balanced schedule
+
+BALANCED = [
+    # (heads, kv heads, ctx lens, q lens): skew, empty contexts, sequences without rows, odd
+    # kv head counts (one kv head per workgroup), three row groups, one split-clamped context
+    ((32, 8), [3000, 17, 0, 512, 9000, 33, 1], [8, 8, 3, 0, 5, 1, 8]),
+    ((64, 8), [260, 4100, 9, 700, 1, 2049], [9, 1, 4, 6, 9, 9]),
+    ((12, 3), [5000, 40, 16, 1500], [2, 5, 1, 3]),
+    ((8, 2), [20000, 100], [3, 1]),
+    ((32, 8), [64], [8]),
+]
+
+
+@pytest.mark.parametrize("shape", BALANCED, ids=lambda s: f"{s[0][0]}x{s[0][1]}b{len(s[1])}")
+def test_balanced_schedule_parity(gpu, shape):
+    """The persistent balanced schedule against the oracle on every sequence, and against the
+    grid schedule (same rows to bf16 rounding of split merges)."""
+    (H, Hkv), ctx, ql = shape
+    case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
+                                  dtype="bf16", seed=17)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, H, 128, Hkv)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    out = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
+    h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16)
+    grid = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="grid")
+    assert (out - grid).abs().max().item() < 1e-2
+    again = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
+    assert torch.equal(out, again)
+
+
+def test_balanced_schedule_at_most_256_sequences(gpu):
+    """256 sequences (one per thread of the plan), lengths from 1 to 600 tokens; 257 is refused
+    under "balanced" and planned on the grid under "auto"."""
+    rng = np.random.default_rng(3)
+    ctx = rng.integers(1, 600, size=256).tolist()
+    ql = rng.integers(1, 6, size=256).tolist()
+    case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=8, num_kv_heads=2,
+                                  dtype="bf16", seed=4)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 8, 128, 2)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    out = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
+    h.assert_attention_close(out, case, h.oracle_attention(case, [0, 1, 77, 128, 254, 255]), h.ATOL_BF16)
+    case2 = wl.make_attention_case(context_lens=ctx + [500], q_lens=ql + [2], num_heads=8, num_kv_heads=2,
+                                   dtype="bf16", seed=4)
+    t2 = h.attention_tensors(case2, gpu)
+    args2 = (t2["query"], t2["key_cache"], t2["value_cache"], t2["block_table"], t2["context_lens"])
+    with pytest.raises(kyro_amd.KyroError, match="at most 256"):
+        attn.forward(*args2, q_start_loc=t2["q_start_loc"], path="mfma", schedule="balanced")
+    out2 = attn.forward(*args2, q_start_loc=t2["q_start_loc"], path="mfma")
+    h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 255, 256]), h.ATOL_BF16)
+
+
+def test_balanced_schedule_errors(gpu):
+    case = wl.make_attention_case(context_lens=[300, 40], q_lens=[2, 3], num_heads=8, num_kv_heads=2,
+                                  dtype="bf16", seed=6)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 8, 128, 2)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"])
+    with pytest.raises(kyro_amd.KyroError, match="num_splits"):
+        attn.forward(*args, t["context_lens"], q_start_loc=t["q_start_loc"], schedule="balanced", num_splits=2)
+    with pytest.raises(kyro_amd.KyroError, match="MFMA"):
+        attn.forward(*args, t["context_lens"], q_start_loc=t["q_start_loc"], schedule="balanced", path="vector")
+    # a context length beyond the table latches an error; the other sequence is still computed
+    # and the context recovers on the next call
+    bad = t["context_lens"].clone()
+    bad[0] = case.block_table.shape[1] * 16 + 1
+    with pytest.raises(kyro_amd.KyroError, match="context length"):
+        attn.forward(*args, bad, q_start_loc=t["q_start_loc"], schedule="balanced")
+    out = attn.forward(*args, t["context_lens"], q_start_loc=t["q_start_loc"], schedule="balanced")
+    h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16)
+
+
 # ---------------------------------------------------------------- full-size workloads
 
 
