@@ -100,9 +100,9 @@ int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, 
 
 /* ---------------------------------------------------------------- paged attention */
 
-/* Attention-kernel choice. AUTO picks MFMA when the GQA group x queries fill >= 1 16-row tile
- * with enough rows to pay for it, the vector kernel otherwise (bf16), and always the vector
- * kernel for f32. */
+/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (bf16 query and
+ * caches, head_dim 128, block_size 16), whatever the number of query rows, and the vector kernel
+ * otherwise (f32, head_dim 64, other block sizes). */
 typedef enum kyro_attn_path {
     KYRO_ATTN_AUTO = 0,
     KYRO_ATTN_VECTOR = 1,
