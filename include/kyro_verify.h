@@ -196,8 +196,12 @@ typedef struct kyro_spec_verify_params {
     int32_t logits_dtype; /* kyro_dtype of both logits tensors (KYRO_F32) */
     int32_t window;       /* draft positions whose logit rows are read before the first
                              acceptance scan; rows after it are read only for sequences that
-                             accept all of them. 0 = default (3); >= max_draft reads every row
-                             in one pass. Outputs do not depend on it. */
+                             accept all of them. 0 = default: 3, or every row in one pass when
+                             all rows of the batch total at most 64 MB; >= max_draft + 1 reads
+                             every row in one pass. Outputs do not depend on it, only the time
+                             does: a caller that tracks its acceptance can tune it (measured best:
+                             3 for Llama-3-8B with 1.4 of 7 drafts accepted on average, 1 for a
+                             mixed batch with 0.7 of up to 8). */
 } kyro_spec_verify_params;
 
 /*

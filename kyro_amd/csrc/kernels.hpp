@@ -254,6 +254,9 @@ constexpr int kMaxDraft = 63;                // one wave holds the acceptance de
 #endif
 constexpr int kSpecWindow = KYRO_SPEC_WINDOW;
 constexpr int kMaxLazyBatch = 2048;  // larger batches read every row in the first pass
+// Default window: batches whose logit rows total at most this many bytes read them all in the
+// first pass (at ~6 TB/s, 64 MB take about as long as the tail pass's fixed cost).
+constexpr long long kSpecEagerBytes = 64ll << 20;
 #ifndef KYRO_SPEC_TAIL_WGS
 #define KYRO_SPEC_TAIL_WGS 2048
 #endif
