@@ -100,9 +100,9 @@ int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, 
 
 /* ---------------------------------------------------------------- paged attention */
 
-/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (bf16 query and
- * caches, head_dim 128, block_size 16), whatever the number of query rows, and the vector kernel
- * otherwise (f32, head_dim 64, other block sizes). */
+/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (head_dim 128,
+ * block_size 16; bf16 or f32 caches), whatever the number of query rows, and the vector kernel
+ * otherwise (head_dim 64, other block sizes). */
 typedef enum kyro_attn_path {
     KYRO_ATTN_AUTO = 0,
     KYRO_ATTN_VECTOR = 1,

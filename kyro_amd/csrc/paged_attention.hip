@@ -15,7 +15,7 @@
 // Workgroups are numbered so that all splits of one (sequence, kv head) land on one XCD (the
 // dispatcher deals workgroups round-robin over the 8 XCDs), keeping that merge in one L2.
 //
-// Two kernels share that frame:
+// Three kernels share that frame:
 //  * attn_mfma_kernel (bf16, D = 128, block_size 16): scores S^T = K Q^T and O^T = V^T P^T on
 //    v_mfma_f32_16x16x32_bf16. K and V are loaded straight from HBM into the MFMA operand
 //    layouts with 128-bit loads — K as 16 token rows x 64 contiguous bytes per instruction, V as
@@ -23,8 +23,12 @@
 //    registers with v_perm_b32. The softmax'd S^T fragment is already the P^T operand of the PV
 //    product, and the output column of O^T is the query row, so the per-row rescale stays in the
 //    lane that owns the row's softmax state.
+//  * attn_mfma_f32_kernel (f32, D = 128, block_size 16): the same products on
+//    v_mfma_f32_16x16x4_f32, one 16-token block per step;
 //  * attn_vector_kernel (f32 or bf16, D = 64 or 128, any block size): 16 lanes per token row,
 //    4 token rows per wave per step, dot products reduced with DPP inside each 16-lane row.
+// Both MFMA kernels run under either schedule: a grid of one workgroup per work item, or the
+// balanced schedule, a persistent grid that plans splits from the context lengths on the device.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -777,14 +781,288 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
     }
 }
 
-// PLAN: the balanced schedule (a persistent grid walking the plan's items) or one workgroup per
-// (kv head group, split, row group) of the grid schedule.
-template <int NTW, int HP, int POL, bool PLAN>
-__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+// ------------------------------------------------------------------ MFMA kernel, f32 caches
+//
+// The reference's own dtype. v_mfma_f32_16x16x4_f32 takes one f32 per lane for each operand:
+// A lane l = A[l % 16][l / 16], B lane l = B[l / 16][l % 16], and D lane l, element e =
+// D[4 (l / 16) + e][l % 16]. The kernel streams one 16-token block at a time (an f32 block is
+// as many registers as a bf16 pair), with the same frame, schedule and merge as the bf16 kernel.
+//  * S^T = K Q^T: lane (r, g) loads K[token r][16 s + 4 g .. + 3] (s = 0..7; 16 rows x 64
+//    contiguous bytes per instruction), and MFMA (s, e) contracts dims 16 s + 4 g + e; Q is loaded
+//    the same way for its rows.
+//  * O^T += V^T P^T over tokens 4 g + q at step q (q = 0..3): the softmax'd S^T fragment of lane
+//    (row r, g) holds tokens 4 g + e, so element q is already the B operand of step q (no
+//    shuffle). Lane (r, g) loads V[token 4 g + q][64 h + 4 r .. + 3] (h = 0, 1): component e_t
+//    is the A operand of the d-tile holding dims 64 h + 4 i + e_t, and the accumulator of that
+//    tile gives lane (r, g) dims 64 h + 16 g + 4 e' + e_t of row r.
+// 32 + 32 MFMAs per block and 16-row tile: at 32 cycles each, about 60% of a block's streaming
+// time for two tiles (GQA 32/8 with 8 draft rows), so the loads still set the pace.
+
+__device__ float kZeroSlabF32[kMfmaBS * kMfmaD];
+
+struct KVBlockF32 {
+    float4 k[8];  // [s]: token r, dims 16 s + 4 g .. + 3
+    float4 v[8];  // [2 q + h]: token 4 g + q, dims 64 h + 4 r .. + 3
+};
+
+template <int POL>
+__device__ __forceinline__ void load_block_f32(KVBlockF32& kv, const float* __restrict__ kp,
+                                               const float* __restrict__ vp, int blk, size_t block_stride,
+                                               size_t kv_off, int r, int g) {
+    constexpr int kSlabBytes = kMfmaBS * kMfmaD * 4;
+    const size_t base = (size_t)(blk >= 0 ? blk : 0) * block_stride + kv_off;
+    const float* kslab = blk >= 0 ? kp + base : kZeroSlabF32;
+    const float* vslab = blk >= 0 ? vp + base : kZeroSlabF32;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kslab), (short)0, kSlabBytes, kRawBufferWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vslab), (short)0, kSlabBytes, kRawBufferWord3);
+    const int koff = (r * kMfmaD + 4 * g) * 4;       // + 64 s
+    const int voff = (4 * g * kMfmaD + 4 * r) * 4;   // + (q * 128 + 64 h) * 4
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+        kv.k[s] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * s, POL));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            kv.v[2 * q + h] =
+                __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, (q * kMfmaD + 64 * h) * 4, POL));
+}
+
+__device__ __forceinline__ float f4_get(const float4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// One work item of the f32 kernel; the arguments are those of mfma_item.
+template <int NTW, int HP, int POL>
+__device__ __forceinline__ void mfma_item_f32(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
+                                              const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
+                                              int nsplit, size_t pb0, size_t pbstep) {
+    constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;
     constexpr int WPH = kWaves / HP;
-    __shared__ Frame<RW, kMfmaD> frame[HP];
-    __shared__ int s_blk[kMaxChunkBlocks];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hw = wave / WPH;
+    const int wp = wave % WPH;
+    const int row0 = rg * RW;
+
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const float* __restrict__ qp = reinterpret_cast<const float*>(a.q);
+    const float* __restrict__ kp = reinterpret_cast<const float*>(a.k);
+    const float* __restrict__ vp = reinterpret_cast<const float*>(a.v);
+    const size_t head_stride = (size_t)kMfmaBS * D;
+    const size_t block_stride = (size_t)a.Hkv * head_stride;
+    const size_t kv_off = (size_t)si.kvh * head_stride;
+    const float c = a.scale_log2;
+    const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
+
+    stage_block_ids(a, si, blk_begin, blk_end, s_blk);
+
+    {
+        // Q^T operands: lane (r, g) holds row row0 + 16 nt + r, dims 16 s + 4 g .. + 3.
+        float4 qB[NTW][8];
+        int vis[NTW];
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+            const int n = row0 + nt * 16 + r;
+            if (n < si.rows) {
+                const int j = n / a.group;
+                const size_t qrow = out_row(a, si, n);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) qB[nt][s] = *reinterpret_cast<const float4*>(qp + qrow * D + 16 * s + 4 * g);
+                vis[nt] = a.causal ? si.ctx - si.q_len + j + 1 : si.ctx;
+            } else {
+#pragma unroll
+                for (int s = 0; s < 8; ++s) qB[nt][s] = make_float4(0.f, 0.f, 0.f, 0.f);
+                vis[nt] = si.ctx;
+            }
+        }
+
+        float m[NTW], lsum[NTW];
+        f32x4 O[8][NTW];  // [2 h + ... ] d-tile dt = 4 h + e_t
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+            m[nt] = kNegInf;
+            lsum[nt] = 0.f;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+        auto compute = [&](KVBlockF32& kv, int pb, int blk) {
+            f32x4 S[NTW];
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(f4_get(kv.k[s], e), f4_get(qB[nt][s], e), acc, 0, 0, 0);
+                S[nt] = acc;
+            }
+            const bool full = blk >= 0 && (pb + 1) * kMfmaBS <= full_vis;
+            if (!full) {
+                // V rows of tokens past the context are zeroed, as in the bf16 kernel.
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (pb * kMfmaBS + 4 * g + q >= si.ctx) {
+                        kv.v[2 * q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                        kv.v[2 * q + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+            }
+            float pv[NTW][4];
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) {
+                float sv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sv[e] = S[nt][e];
+                if (!full) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = pb * kMfmaBS + 4 * g + e;
+                        if (!(blk >= 0 && t < vis[nt])) sv[e] = kNegInf;
+                    }
+                }
+                float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+                mx = fmaxf(mx, shfl_xor_f(mx, 16));
+                mx = fmaxf(mx, shfl_xor_f(mx, 32));
+                const float m_new = fmaxf(m[nt], mx * c);
+                const float mref = (m_new == kNegInf) ? 0.f : m_new;
+                const float alpha = fast_exp2(m[nt] - mref);
+                float ps = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    pv[nt][e] = fast_exp2(__builtin_fmaf(sv[e], c, -mref));
+                    ps += pv[nt][e];
+                }
+                lsum[nt] = lsum[nt] * alpha + ps;
+                if (__any(m_new > m[nt] && m[nt] != kNegInf)) {
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) O[dt][nt] *= alpha;
+                }
+                m[nt] = m_new;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const float av = f4_get(kv.v[2 * q + (dt >> 2)], dt & 3);
+#pragma unroll
+                    for (int nt = 0; nt < NTW; ++nt)
+                        O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, pv[nt][q], O[dt][nt], 0, 0, 0);
+                }
+        };
+
+        // Each wave streams blocks wp, wp + WPH, ... of the split; the next block's loads are issued
+        // before the current block is computed. Lane j % 64 holds the id of the wave's block j in
+        // slot j / 64.
+        {
+            constexpr int kSlots = 2 * kMfmaMaxPairsPerWave / 64;
+            const int b0 = blk_begin + wp;
+            int bid[kSlots];
+#pragma unroll
+            for (int t = 0; t < kSlots; ++t) {
+                const int bj = b0 + (t * 64 + lane) * WPH;
+                bid[t] = bj < blk_end ? s_blk[bj - blk_begin] : -1;
+            }
+            auto block_id = [&](int j) {
+                int x = __builtin_amdgcn_readlane(bid[0], j & 63);
+#pragma unroll
+                for (int t = 1; t < kSlots; ++t) {
+                    const int y = __builtin_amdgcn_readlane(bid[t], j & 63);
+                    x = (j >> 6) == t ? y : x;
+                }
+                return x;
+            };
+            const int nblk = b0 < blk_end ? (blk_end - 1 - b0) / WPH + 1 : 0;
+            auto next_id = [&](int j) {
+                const int x = block_id(min(j + 1, kSlots * 64 - 1));
+                return j + 1 < nblk ? x : -1;
+            };
+            KVBlockF32 bufA, bufB;
+            if (nblk > 0) {
+                int j = 0;
+                int ia = block_id(0), ib;
+                load_block_f32<POL>(bufA, kp, vp, ia, block_stride, kv_off, r, g);
+                while (true) {
+                    ib = next_id(j);
+                    load_block_f32<POL>(bufB, kp, vp, ib, block_stride, kv_off, r, g);
+                    compute(bufA, b0 + j * WPH, ia);
+                    if (++j >= nblk) break;
+                    ia = next_id(j);
+                    load_block_f32<POL>(bufA, kp, vp, ia, block_stride, kv_off, r, g);
+                    compute(bufB, b0 + j * WPH, ib);
+                    if (++j >= nblk) break;
+                }
+            }
+        }
+
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+            lsum[nt] += shfl_xor_f(lsum[nt], 16);
+            lsum[nt] += shfl_xor_f(lsum[nt], 32);
+        }
+
+        Frame<RW, D>& fr = frame[hw];
+        if (g == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NTW; ++nt) fr.m[wp][nt * 16 + r] = m[nt];
+        }
+        __syncthreads();
+        float f[NTW];
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+            const int n = nt * 16 + r;
+            float M = fr.m[0][n];
+#pragma unroll
+            for (int w = 1; w < WPH; ++w) M = fmaxf(M, fr.m[w][n]);
+            f[nt] = (m[nt] == kNegInf) ? 0.f : fast_exp2(m[nt] - M);
+            if (g == 0) {
+                fr.l[wp][n] = lsum[nt] * f[nt];
+                if (wp == 0) fr.mx[n] = M;
+            }
+        }
+        // Lane (r, g) holds dims 64 h + 16 g + 4 e' + e_t of row 16 nt + r in O[4 h + e_t][nt][e'].
+        for (int w = 0; w < WPH; ++w) {
+            if (wp == w) {
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) {
+                    float* dst = &fr.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 16 * g];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int e2 = 0; e2 < 4; ++e2)
+#pragma unroll
+                            for (int et = 0; et < 4; ++et) {
+                                const float v = O[4 * h + et][nt][e2] * f[nt];
+                                float* p = dst + 64 * h + 4 * e2 + et;
+                                *p = (w == 0) ? v : *p + v;
+                            }
+                }
+            }
+            __syncthreads();
+        }
+        const int nrows = min(RW, si.rows - row0);
+#pragma unroll
+        for (int h = 0; h < HP; ++h) {
+            SeqInfo sh = si;
+            sh.kvh = (ug * HP + h) % a.Hkv;
+            frame_flush<RW, D>(a, sh, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH, pb0 + h * pbstep);
+        }
+    }
+}
+
+// PLAN: the balanced schedule (a persistent grid walking the plan's items) or one workgroup per
+// (kv head group, split, row group) of the grid schedule. `item` runs one work item: (this
+// wave's SeqInfo, kv head group, row group, first block, end block, splits, workspace row of
+// head 0, workspace rows between heads).
+template <int NTW, int HP, bool PLAN, typename Item>
+__device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
+    constexpr int RW = NTW * 16;
+    constexpr int WPH = kWaves / HP;
     const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) / WPH;
 
     if constexpr (PLAN) {
@@ -816,25 +1094,45 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
             const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[p]);
             const int blk_begin = chunk * ch;
             const int blk_end = min(si.nblk, blk_begin + ch);
-            mfma_item<NTW, HP, POL>(a, frame, s_blk, si, si.b * U + hp, rg, blk_begin, blk_end, nsplit,
-                                    (size_t)slot * HP * RW, RW);
+            item(si, si.b * U + hp, rg, blk_begin, blk_end, nsplit, (size_t)slot * HP * RW, (size_t)RW);
         }
     } else {
-    int ug, split, rg;
-    if (!map_workgroup(a, ug, split, rg)) return;
-    // The group's units belong to one sequence, so everything but the kv head is the same for
-    // every wave, and the early returns below are taken by the whole workgroup or by none of it.
-    const SeqInfo si = seq_info(a, ug * HP + hw);
-    if (!si.ok) return;
-    const int nsplit = num_splits_for(a, si.nblk);
-    if (split >= nsplit) return;
-    if (rg > 0 && rg * RW >= si.rows) return;  // this row group is past the sequence's rows
-    const int blk_begin = split * a.chunk_blocks;
-    const int blk_end = min(si.nblk, blk_begin + a.chunk_blocks);
-    mfma_item<NTW, HP, POL>(a, frame, s_blk, si, ug, rg, blk_begin, blk_end, nsplit,
-                            ((size_t)ug * HP * a.splits + split) * a.rows_cap + rg * RW,
-                            (size_t)a.splits * a.rows_cap);
+        int ug, split, rg;
+        if (!map_workgroup(a, ug, split, rg)) return;
+        // The group's units belong to one sequence, so everything but the kv head is the same for
+        // every wave, and the early returns below are taken by the whole workgroup or by none of it.
+        const SeqInfo si = seq_info(a, ug * HP + hw);
+        if (!si.ok) return;
+        const int nsplit = num_splits_for(a, si.nblk);
+        if (split >= nsplit) return;
+        if (rg > 0 && rg * RW >= si.rows) return;  // this row group is past the sequence's rows
+        const int blk_begin = split * a.chunk_blocks;
+        const int blk_end = min(si.nblk, blk_begin + a.chunk_blocks);
+        item(si, ug, rg, blk_begin, blk_end, nsplit, ((size_t)ug * HP * a.splits + split) * a.rows_cap + rg * RW,
+             (size_t)a.splits * a.rows_cap);
     }
+}
+
+// bf16 caches.
+template <int NTW, int HP, int POL, bool PLAN>
+__global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
+    __shared__ Frame<NTW * 16, kMfmaD> frame[HP];
+    __shared__ int s_blk[kMaxChunkBlocks];
+    mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
+                                        size_t pbs) {
+        mfma_item<NTW, HP, POL>(a, frame, s_blk, si, ug, rg, bb, be, ns, pb0, pbs);
+    });
+}
+
+// f32 caches.
+template <int NTW, int HP, int POL, bool PLAN>
+__global__ __launch_bounds__(kThreads) void attn_mfma_f32_kernel(AttnArgs a) {
+    __shared__ Frame<NTW * 16, kMfmaD> frame[HP];
+    __shared__ int s_blk[kMaxChunkBlocks];
+    mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
+                                        size_t pbs) {
+        mfma_item_f32<NTW, HP, POL>(a, frame, s_blk, si, ug, rg, bb, be, ns, pb0, pbs);
+    });
 }
 
 
@@ -1030,13 +1328,19 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
         const bool rows16 = mfma_rows_per_group(a.rows_cap) == 16;
-#define KYRO_MFMA_LAUNCH(POL, PLAN)                                                           \
-        if (a.hpw == 2) {                                                                     \
-            if (rows16) attn_mfma_kernel<1, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);     \
-            else attn_mfma_kernel<2, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);            \
-        } else {                                                                              \
-            if (rows16) attn_mfma_kernel<1, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);     \
-            else attn_mfma_kernel<2, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);            \
+#define KYRO_MFMA_LAUNCH2(K, POL, PLAN)                                                     \
+        if (a.hpw == 2) {                                                                   \
+            if (rows16) K<1, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);                  \
+            else K<2, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);                         \
+        } else {                                                                            \
+            if (rows16) K<1, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);                  \
+            else K<2, 1, POL, PLAN><<<grid, block, 0, stream>>>(a);                         \
+        }
+#define KYRO_MFMA_LAUNCH(POL, PLAN)                                                         \
+        if (a.dtype_bf16) {                                                                 \
+            KYRO_MFMA_LAUNCH2(attn_mfma_kernel, POL, PLAN)                                  \
+        } else {                                                                            \
+            KYRO_MFMA_LAUNCH2(attn_mfma_f32_kernel, POL, PLAN)                              \
         }
         if (a.plan) {
             if (a.stream_kv) {
@@ -1052,6 +1356,7 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
             }
         }
 #undef KYRO_MFMA_LAUNCH
+#undef KYRO_MFMA_LAUNCH2
     } else {
         const bool bf16 = a.dtype_bf16;
         if (a.D == 128) {

@@ -324,12 +324,11 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         if (max_q_len <= 0) max_q_len = q_start_loc ? p->total_q : 1;
         if (!q_start_loc) max_q_len = 1;
 
-        const bool mfma_ok = p->dtype == KYRO_BF16 && p->head_dim == 128 && p->block_size == 16;
+        const bool mfma_ok = p->head_dim == 128 && p->block_size == 16;  // bf16 or f32 caches
         int kernel;
         if (p->path == KYRO_ATTN_MFMA) {
             if (!mfma_ok)
-                return fail(KYRO_EUNSUPPORTED,
-                            "paged_attention: the MFMA kernel needs bf16, head_dim 128, block_size 16");
+                return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs head_dim 128, block_size 16");
             kernel = kyro::ATTN_KERNEL_MFMA;
         } else if (p->path == KYRO_ATTN_VECTOR) {
             kernel = kyro::ATTN_KERNEL_VECTOR;
@@ -341,7 +340,7 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         }
         if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
             return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
-                        "(bf16, head_dim 128, block_size 16)");
+                        "(head_dim 128, block_size 16)");
 
         kyro::AttnArgs a{};
         a.q = query;

@@ -71,8 +71,8 @@ SMALL = [
 @pytest.mark.parametrize("splits", [1, 3])
 def test_small_parity(gpu, dtype, shape, path, splits):
     (H, Hkv), D, ctx, ql = shape
-    if path == "mfma" and (dtype != "bf16" or D != 128):
-        pytest.skip("the MFMA kernel is bf16 / head_dim 128 only")
+    if path == "mfma" and D != 128:
+        pytest.skip("the MFMA kernels take head_dim 128 only")
     case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
                                   head_dim=D, dtype=dtype, seed=21, num_blocks=200)
     t = h.attention_tensors(case, gpu)
@@ -162,7 +162,7 @@ def test_cache_slots_past_the_context_are_never_used(gpu, dtype):
     t = h.attention_tensors(case, gpu)
     exp = h.oracle_attention(case)
     attn = make_attention(16, 8, 128, 2)
-    for path in (("vector", "mfma") if dtype == "bf16" else ("vector",)):
+    for path in ("vector", "mfma"):
         for splits in (1, 2):
             out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
                                t["context_lens"], q_start_loc=t["q_start_loc"], path=path,
@@ -198,20 +198,22 @@ BALANCED = [
 ]
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("shape", BALANCED, ids=lambda s: f"{s[0][0]}x{s[0][1]}b{len(s[1])}")
-def test_balanced_schedule_parity(gpu, shape):
+def test_balanced_schedule_parity(gpu, shape, dtype):
     """The persistent balanced schedule against the oracle on every sequence, and against the
-    grid schedule (same rows to bf16 rounding of split merges)."""
+    grid schedule (same rows up to the rounding of split merges)."""
     (H, Hkv), ctx, ql = shape
     case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
-                                  dtype="bf16", seed=17)
+                                  dtype=dtype, seed=17)
     t = h.attention_tensors(case, gpu)
     attn = make_attention(16, H, 128, Hkv)
     args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
     out = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
-    h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16)
+    tol = h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32
+    h.assert_attention_close(out, case, h.oracle_attention(case), tol)
     grid = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="grid")
-    assert (out - grid).abs().max().item() < 1e-2
+    assert (out - grid).abs().max().item() < (1e-2 if dtype == "bf16" else 1e-4)
     again = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
     assert torch.equal(out, again)
 
@@ -278,6 +280,20 @@ def test_full_mha_llama2_7b(gpu):
         other = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
                              t["context_lens"], q_start_loc=t["q_start_loc"], path=path)
         assert (other - out).abs().max().item() < 1e-2
+
+
+def test_full_mha_llama2_7b_f32(gpu):
+    """The reference's dtype at the Llama-2-7B layer shape: f32 Q/K/V on the f32 MFMA kernel
+    (AUTO) and on the vector kernel, both against the oracle within the f32 tolerance."""
+    case = wl.make_attention_case(context_lens=[512, 1000, 2048, 1777], q_lens=[5] * 4, num_heads=32,
+                                  num_kv_heads=32, dtype="f32", seed=3)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 32, 128, 32)
+    exp = h.oracle_attention(case)
+    for path in ("auto", "vector"):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                           t["context_lens"], q_start_loc=t["q_start_loc"], path=path)
+        h.assert_attention_close(out, case, exp, h.ATOL_F32)
 
 
 def test_full_gqa_llama3_8b_properties(gpu):
