@@ -18,6 +18,8 @@ struct kyro_ctx_s {
     void* arena = nullptr;  // per-call scratch, stream-ordered
     size_t arena_bytes = 0;
     int* err = nullptr;     // device error word
+    int* sched = nullptr;   // kyro::kSchedWords device counters of the balanced attention schedule
+                            // (zero between launches: the last workgroup of a launch resets them)
     // Host staging for small uploads (hipHostMalloc): kStageSlots slots used in turn, each with
     // an event recorded after the copies out of it.
     void* pinned = nullptr;

@@ -60,7 +60,12 @@ struct AttnArgs {
     int plan_rw;
     int plan_max_chunk;
     int4* plan_seq;
+    // kSchedWords counters, zero at launch: the items claimed on each of the 8 XCD lanes beyond
+    // the grid's first items, then the workgroups done; the last workgroup resets them to zero.
+    int* sched;
 };
+
+constexpr int kSchedWords = 9;
 
 // Sequences one balanced-schedule launch can plan (one per thread of a workgroup).
 constexpr int kPlanMaxSeqs = 256;

@@ -304,11 +304,12 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //    a longer sequence splits into equal even chunks;
 //  * sequences are ordered by chunk length, longest first (lower index first among equals), so
 //    the longest items start first;
-//  * item groups (sequence, chunk, kv head group) are dealt round-robin to 8 lanes, one per XCD;
-//    the row groups of an item group take consecutive positions of one lane (item indices 8
-//    apart), so they run together on one XCD and share its L2;
-//  * workgroup w takes item w of every band of `grid` items, from the other end in odd bands,
-//    which evens out the workgroups' totals.
+//  * item groups (sequence, chunk, kv head group) are dealt to 8 lanes, one per XCD, in a snake
+//    (lanes 0..7, then 7..0), which keeps the lanes' totals even; the row groups of an item group
+//    take consecutive positions of one lane (item indices 8 apart), so they run together on one
+//    XCD and share its L2;
+//  * a workgroup takes one item of its XCD's lane at a time, the next unclaimed one (a counter
+//    per lane), so the workgroups of an XCD share its lane's items greedily, largest first.
 struct PlanLds {
     alignas(16) uint32_t key[kPlanMaxSeqs];  // by sequence: (chunk << 16) | (0xffff - b); larger first
     int b[kPlanMaxSeqs];         // the rest by position in that order
@@ -326,6 +327,28 @@ struct PlanLds {
     long long red64[kWaves];
 };
 static_assert(kPlanMaxSeqs == kThreads, "plan_build reads one sequence per thread");
+
+// Item group g goes to lane snake_lane(g): lanes 0..7 in even rounds of 8 groups and 7..0 in odd
+// ones, so that with groups sorted largest first no lane always gets the larger of each round.
+__device__ __forceinline__ int snake_pos(int r, int x) { return (r & 1) ? 7 - x : x; }
+
+// Number of groups g in [A, A + n) on lane x.
+__device__ __forceinline__ int snake_count(int A, int n, int x) {
+    if (n <= 0) return 0;
+    const int r0 = A >> 3, r1 = (A + n - 1) >> 3;
+    int c = max(0, r1 - r0 - 1);
+    const int first = 8 * r0 + snake_pos(r0, x);
+    c += (first >= A && first < A + n) ? 1 : 0;
+    if (r1 > r0) c += (8 * r1 + snake_pos(r1, x) < A + n) ? 1 : 0;
+    return c;
+}
+
+// The i-th group (from 0) of [A, A + n) on lane x.
+__device__ __forceinline__ int snake_nth(int A, int x, int i) {
+    const int r0 = A >> 3;
+    const int r = (8 * r0 + snake_pos(r0, x) >= A ? r0 : r0 + 1) + i;
+    return 8 * r + snake_pos(r, x);
+}
 
 // Exclusive prefix sums of V values per thread over the workgroup's threads; total[] gets the
 // sums. `red` is LDS scratch.
@@ -459,7 +482,7 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
     const int g0 = sa[0];
     int sb[9], tb[9];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) sb[x] = ((g0 + nig + 7 - x) / 8 - (g0 + 7 - x) / 8) * rp;
+    for (int x = 0; x < 8; ++x) sb[x] = snake_count(g0, nig, x) * rp;
     sb[8] = nig * rp;
     block_scan_excl<9>(sb, tb, P.red);
     if (t < a.B) {
@@ -499,7 +522,7 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
     const int rr = P.r[lo];
     const int idx = k - P.lane0[x][lo];
     const int igl = idx / rr;
-    const int q = ((x - P.g0[lo]) & 7) + 8 * igl;  // item group within the sequence
+    const int q = snake_nth(P.g0[lo], x, igl) - P.g0[lo];  // item group within the sequence
     const int U = a.Hkv / HP;
     it.p = lo;
     it.rg = idx - igl * rr;
@@ -1067,14 +1090,20 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
 
     if constexpr (PLAN) {
         __shared__ PlanLds plan;
-        const int items = plan_build<RW, HP>(a, plan);
-        const int G = a.plan_grid;
+        (void)plan_build<RW, HP>(a, plan);
+        const int G = a.plan_grid;  // a multiple of 8
         const int U = a.Hkv / HP;
-        for (int base = 0, band = 0; base < items; base += G, ++band) {
-            const int i = base + ((band & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x);
-            PlanItem it;
-            const bool has = i < items && plan_item<HP>(a, plan, i, it);
-            if (!__builtin_amdgcn_readfirstlane(has ? 1 : 0)) continue;  // same for every lane
+        // Workgroup w works on lane x = w % 8, the items dealt to its XCD: first the lane's item
+        // k = w / 8, then whichever item of the lane is next unclaimed when it becomes free. The
+        // G / 8 workgroups of an XCD thus take the lane's items largest first, greedily, and the
+        // row groups of one item group (consecutive on the lane) run together and share its L2.
+        __shared__ int s_claim;
+        const int x = (int)blockIdx.x & 7;
+        const int len = plan.lane_len[x];
+        for (int k = (int)blockIdx.x >> 3; k < len;) {
+            const int i = 8 * k + x;
+            PlanItem it = {0, 0, 0, 0, 0};
+            const bool has = plan_item<HP>(a, plan, i, it);
             // Plan values come from LDS: make them scalar for the addressing that follows.
             const int p = __builtin_amdgcn_readfirstlane(it.p);
             const int hp = __builtin_amdgcn_readfirstlane(it.hp);
@@ -1094,7 +1123,21 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
             const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[p]);
             const int blk_begin = chunk * ch;
             const int blk_end = min(si.nblk, blk_begin + ch);
-            item(si, si.b * U + hp, rg, blk_begin, blk_end, nsplit, (size_t)slot * HP * RW, (size_t)RW);
+            if (__builtin_amdgcn_readfirstlane(has ? 1 : 0))  // a full lane has no empty position
+                item(si, si.b * U + hp, rg, blk_begin, blk_end, nsplit, (size_t)slot * HP * RW, (size_t)RW);
+            // Claimed after the item: an atomic issued before it would sit at the head of the
+            // in-order load counter and hold up the item's first waits (measured: 437 -> 474 us
+            // on the mixed GQA 64/8 batch).
+            if (threadIdx.x == 0) s_claim = G / 8 + atomicAdd(&a.sched[x], 1);
+            __syncthreads();
+            k = s_claim;
+            __syncthreads();  // s_claim is written again after the next item
+        }
+        // The last workgroup out resets the counters for the next launch: every other workgroup
+        // has had its last claim answered before it counts itself done.
+        if (threadIdx.x == 0 && atomicAdd(&a.sched[8], 1) == G - 1) {
+#pragma unroll
+            for (int j = 0; j < kSchedWords; ++j) a.sched[j] = 0;
         }
     } else {
         int ug, split, rg;

@@ -150,8 +150,12 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
         if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->err), sizeof(int));
         if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->sched), kyro::kSchedWords * sizeof(int));
+        if (e == hipSuccess) e = hipMemset(ctx->sched, 0, kyro::kSchedWords * sizeof(int));
+        if (e == hipSuccess) e = hipStreamSynchronize(0);  // the memsets are done before any launch
         if (e != hipSuccess) {
             if (ctx->err) (void)hipFree(ctx->err);
+            if (ctx->sched) (void)hipFree(ctx->sched);
             if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
             delete ctx;
             return fail(KYRO_EHIP, "kyro_ctx_create: %s", hipGetErrorString(e));
@@ -170,6 +174,7 @@ int kyro_ctx_destroy(kyro_ctx ctx) {
         if (ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
         if (ctx->arena) (void)hipFree(ctx->arena);
         if (ctx->err) (void)hipFree(ctx->err);
+        if (ctx->sched) (void)hipFree(ctx->sched);
         for (hipEvent_t& e : ctx->pinned_done)
             if (e) (void)hipEventSynchronize(e);
         if (ctx->pinned) (void)hipHostFree(ctx->pinned);
@@ -445,6 +450,7 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
             a.ws_l = reinterpret_cast<float*>(base + mb_bytes);
             a.ws_acc = reinterpret_cast<float*>(base + 2 * mb_bytes);
             a.plan_seq = reinterpret_cast<int4*>(base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256));
+            a.sched = ctx->sched;
         } else if (splits > 1) {
             const size_t rows = (size_t)a.units * splits * a.rows_cap;
             ws_bytes = align_up(rows * sizeof(float), 256) * 2 + align_up(rows * a.D * sizeof(float), 256);
