@@ -1,7 +1,7 @@
 // Fused acceptance sampling for the speculative verify step on gfx950.
 //
 // Replaces SpeculativeDecoder::verify_drafts (src/speculative.rs:286-339) for a whole batch, with
-// the north-star rejection rule (accept while u < min(1, p/q); resample from max(p - q, 0) at the
+// the standard rejection rule (accept while u < min(1, p/q); resample from max(p - q, 0) at the
 // first rejection, from p after full acceptance) and the greedy argmax-match rule of the reference
 // when T <= 0. Draws are sample_token's inverse-CDF walk in index order (src/worker.rs:352-360).
 //
