@@ -218,6 +218,29 @@ def test_balanced_schedule_parity(gpu, shape, dtype):
     assert torch.equal(out, again)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_balanced_schedule_random_batches(gpu, seed):
+    """Seeded random batches under the balanced schedule against the oracle on every sequence:
+    1-40 sequences, kv head counts 1-8 (odd ones: one kv head per workgroup), GQA groups 1-8,
+    0-9 query rows, contexts from 0 to 6000 tokens with a few long ones (so the plan splits
+    some and not others), bf16 and f32."""
+    rng = np.random.default_rng(1000 + seed)
+    B = int(rng.integers(1, 41))
+    Hkv = int(rng.choice([1, 2, 3, 4, 8]))
+    H = Hkv * int(rng.choice([1, 2, 4, 8]))
+    ql = rng.integers(0, 10, size=B)
+    ctx = np.where(rng.random(B) < 0.15, rng.integers(2000, 6001, size=B), rng.integers(0, 400, size=B))
+    ctx = np.maximum(ctx, 0)
+    dtype = "bf16" if seed % 3 else "f32"
+    case = wl.make_attention_case(context_lens=ctx.tolist(), q_lens=ql.tolist(), num_heads=H, num_kv_heads=Hkv,
+                                  dtype=dtype, seed=seed)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, H, 128, Hkv)
+    out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                       q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
+    h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
+
+
 def test_balanced_schedule_at_most_256_sequences(gpu):
     """256 sequences (one per thread of the plan), lengths from 1 to 600 tokens; 257 is refused
     under "balanced" and planned on the grid under "auto"."""
