@@ -128,13 +128,13 @@ typedef enum kyro_kv_reuse {
 
 /* How the MFMA kernel spreads work over the chip. Results do not depend on it beyond float
  * rounding of split merges.
- *   AUTO:     BALANCED when num_splits is 0, the batch has at most 256 sequences and either
+ *   AUTO:     BALANCED when num_splits is 0, the batch has at most 1024 sequences and either
  *             max_blocks_per_seq > 256 or GRID would split contexts; GRID otherwise.
  *   GRID:     one workgroup per (sequence, kv head pair, context split, row group), with
  *             num_splits splits of max_blocks_per_seq (0: chosen from the shapes alone).
  *   BALANCED: a persistent grid of one workgroup per CU reads the context lengths on the
  *             device, splits only sequences longer than the per-CU share of the work, and starts
- *             the longest work items first (at most 256 sequences, num_splits must be 0; an
+ *             the longest work items first (at most 1024 sequences, num_splits must be 0; an
  *             extra combine launch always follows). For batches whose context lengths differ
  *             widely. */
 typedef enum kyro_attn_schedule {

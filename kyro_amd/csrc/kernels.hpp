@@ -67,8 +67,8 @@ struct AttnArgs {
 
 constexpr int kSchedWords = 9;
 
-// Sequences one balanced-schedule launch can plan (one per thread of a workgroup).
-constexpr int kPlanMaxSeqs = 256;
+// Sequences one balanced-schedule launch can plan (four per thread of a workgroup).
+constexpr int kPlanMaxSeqs = 1024;
 // Shortest split the balanced schedule makes, in blocks.
 constexpr int kPlanMinChunk = 16;
 

@@ -326,7 +326,7 @@ struct PlanLds {
     int red[kWaves][9];
     long long red64[kWaves];
 };
-static_assert(kPlanMaxSeqs == kThreads, "plan_build reads one sequence per thread");
+static_assert(kPlanMaxSeqs % kThreads == 0, "plan_build reads kPlanMaxSeqs / kThreads sequences per thread");
 
 // Item group g goes to lane snake_lane(g): lanes 0..7 in even rounds of 8 groups and 7..0 in odd
 // ones, so that with groups sorted largest first no lane always gets the larger of each round.
@@ -385,42 +385,56 @@ __device__ __forceinline__ void block_scan_excl(int (&v)[V], int (&total)[V], in
     __syncthreads();
 }
 
-// Builds the plan (every thread of the workgroup takes part; thread t reads sequence t).
+// Builds the plan (every thread of the workgroup takes part; thread t reads sequences
+// t + j kThreads and owns plan positions S t .. S t + S - 1, S = kPlanMaxSeqs / kThreads).
 // Returns the number of item positions (8 x the longest lane). Workgroup 0 latches input
 // errors and publishes {splits, row groups, first slot} per sequence for the combine pass.
+// Up to kThreads sequences are ordered longest chunk first; larger batches keep their order
+// (the claiming still shares the work out greedily, and the sort would cost more than it saves).
 template <int RW, int HP>
 __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
+    constexpr int S = kPlanMaxSeqs / kThreads;
     const int t = threadIdx.x;
     const int wave = t >> 6;
     const int U = a.Hkv / HP;
-    int ctx = 0, q0 = 0, qlen = 0, r = 0, nb = 0;
-    if (t < a.B) {
-        const int64_t c = a.ctx_lens[t];
-        int s0 = t, s1 = t + 1;
-        if (a.q_start) {
-            s0 = a.q_start[t];
-            s1 = a.q_start[t + 1];
-        }
-        bool ok = true;
-        if (c < 0 || c > (int64_t)a.max_blocks * a.bs) {
-            ok = false;
-            if (blockIdx.x == 0) latch_error(a.err, ERR_CTX_LEN);
-        }
-        if (s0 < 0 || s1 < s0 || s1 > a.total_q || s1 - s0 > a.max_q_len) {
-            ok = false;
-            if (blockIdx.x == 0) latch_error(a.err, ERR_Q_LAYOUT);
-        }
-        if (ok) {
-            ctx = (int)c;
-            q0 = s0;
-            qlen = s1 - s0;
-            r = (qlen * a.group + RW - 1) / RW;
-            nb = (ctx + a.bs - 1) / a.bs;
+    int ctx[S], q0[S], qlen[S], r[S], nb[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int sq = t + j * kThreads;
+        ctx[j] = q0[j] = qlen[j] = r[j] = nb[j] = 0;
+        if (sq < a.B) {
+            const int64_t c = a.ctx_lens[sq];
+            int s0 = sq, s1 = sq + 1;
+            if (a.q_start) {
+                s0 = a.q_start[sq];
+                s1 = a.q_start[sq + 1];
+            }
+            bool ok = true;
+            if (c < 0 || c > (int64_t)a.max_blocks * a.bs) {
+                ok = false;
+                if (blockIdx.x == 0) latch_error(a.err, ERR_CTX_LEN);
+            }
+            if (s0 < 0 || s1 < s0 || s1 > a.total_q || s1 - s0 > a.max_q_len) {
+                ok = false;
+                if (blockIdx.x == 0) latch_error(a.err, ERR_Q_LAYOUT);
+            }
+            if (ok) {
+                ctx[j] = (int)c;
+                q0[j] = s0;
+                qlen[j] = s1 - s0;
+                r[j] = (qlen[j] * a.group + RW - 1) / RW;
+                nb[j] = (ctx[j] + a.bs - 1) / a.bs;
+            }
         }
     }
     // Total work and the longest sequence that has rows.
-    long long w = (long long)U * r * nb;
-    int mx = r > 0 ? nb : 0;
+    long long w = 0;
+    int mx = 0;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        w += (long long)U * r[j] * nb[j];
+        mx = max(mx, r[j] > 0 ? nb[j] : 0);
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         w += __shfl_xor(w, o, 64);
@@ -439,58 +453,90 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         maxnb = max(maxnb, P.red[i][0]);
     }
     const long long L = (T + a.plan_grid - 1) / a.plan_grid;
-    long long C = maxnb <= L ? L : (L + 1) / 2;
-    C = C < kPlanMinChunk ? kPlanMinChunk : C;
-    C = (C + 1) & ~1ll;
-    C = C > a.plan_max_chunk ? a.plan_max_chunk : C;
-    int ns = 1, ch = nb;
-    if (nb > C) {
-        ns = (int)((nb + C - 1) / C);
-        ch = (nb + ns - 1) / ns;
-        ch = (ch + 1) & ~1;
-        ns = (nb + ch - 1) / ch;
-    }
-    const uint32_t key = ((uint32_t)(r > 0 ? ch : 0) << 16) | (uint32_t)(0xffff - t);
-    P.key[t] = t < a.B ? key : 0u;  // padding keys rank below every sequence
-    __syncthreads();
-    if (t < a.B) {
-        // Rank = number of larger keys: four keys per LDS read, reads issued together.
-        int rank = 0;
-        const uint4* k4 = reinterpret_cast<const uint4*>(P.key);
-#pragma unroll 4
-        for (int j = 0; j < (a.B + 3) / 4; ++j) {
-            const uint4 k = k4[j];
-            rank += (k.x > key ? 1 : 0) + (k.y > key ? 1 : 0) + (k.z > key ? 1 : 0) + (k.w > key ? 1 : 0);
+    long long CL = maxnb <= L ? L : (L + 1) / 2;
+    CL = CL < kPlanMinChunk ? kPlanMinChunk : CL;
+    CL = (CL + 1) & ~1ll;
+    const int C = (int)(CL > a.plan_max_chunk ? a.plan_max_chunk : CL);
+    int ns[S], ch[S];
+    uint32_t key[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int sq = t + j * kThreads;
+        ns[j] = 1;
+        ch[j] = nb[j];
+        if (nb[j] > C) {
+            ns[j] = (nb[j] + C - 1) / C;
+            ch[j] = (nb[j] + ns[j] - 1) / ns[j];
+            ch[j] = (ch[j] + 1) & ~1;
+            ns[j] = (nb[j] + ch[j] - 1) / ch[j];
         }
-        P.b[rank] = t;
-        P.ns[rank] = ns;
-        P.ch[rank] = ch;
-        P.r[rank] = r;
-        P.ctx[rank] = ctx;
-        P.q0[rank] = q0;
-        P.qlen[rank] = qlen;
+        key[j] = ((uint32_t)(r[j] > 0 ? ch[j] : 0) << 16) | (uint32_t)(0xffff - sq);
+        P.key[sq] = sq < a.B ? key[j] : 0u;  // padding keys rank below every sequence
     }
     __syncthreads();
-    // Item groups and slots in that order; each sequence's item groups dealt to the 8 lanes.
-    int rp = 0, nig = 0;
-    if (t < a.B) {
-        rp = P.r[t];
-        nig = rp > 0 ? U * P.ns[t] : 0;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int sq = t + j * kThreads;
+        if (sq >= a.B) continue;
+        int rank = sq;
+        if (a.B <= kThreads) {
+            // Rank = number of larger keys: four keys per LDS read, reads issued together.
+            rank = 0;
+            const uint4* k4 = reinterpret_cast<const uint4*>(P.key);
+#pragma unroll 4
+            for (int i = 0; i < (a.B + 3) / 4; ++i) {
+                const uint4 k = k4[i];
+                rank += (k.x > key[j] ? 1 : 0) + (k.y > key[j] ? 1 : 0) + (k.z > key[j] ? 1 : 0) + (k.w > key[j] ? 1 : 0);
+            }
+        }
+        P.b[rank] = sq;
+        P.ns[rank] = ns[j];
+        P.ch[rank] = ch[j];
+        P.r[rank] = r[j];
+        P.ctx[rank] = ctx[j];
+        P.q0[rank] = q0[j];
+        P.qlen[rank] = qlen[j];
     }
-    int sa[1] = {nig}, ta[1];
+    __syncthreads();
+    // Item groups and slots in plan order (thread t: positions S t ..), dealt to the 8 lanes.
+    int rp[S], nig[S], gl[S];
+    int loc = 0;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int pos = S * t + j;
+        rp[j] = pos < a.B ? P.r[pos] : 0;
+        nig[j] = rp[j] > 0 ? U * P.ns[pos] : 0;
+        gl[j] = loc;
+        loc += nig[j];
+    }
+    int sa[1] = {loc}, ta[1];
     block_scan_excl<1>(sa, ta, P.red);
-    const int g0 = sa[0];
+    int cnt[S][9];
     int sb[9], tb[9];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) sb[x] = snake_count(g0, nig, x) * rp;
-    sb[8] = nig * rp;
-    block_scan_excl<9>(sb, tb, P.red);
-    if (t < a.B) {
-        P.g0[t] = g0;
-        P.slot0[t] = sb[8];
+    for (int x = 0; x < 9; ++x) sb[x] = 0;
 #pragma unroll
-        for (int x = 0; x < 8; ++x) P.lane0[x][t] = sb[x];
-        if (blockIdx.x == 0) a.plan_seq[P.b[t]] = make_int4(P.ns[t], rp, sb[8], 0);
+    for (int j = 0; j < S; ++j) {
+        gl[j] += sa[0];  // first item group of position S t + j
+#pragma unroll
+        for (int x = 0; x < 8; ++x) cnt[j][x] = snake_count(gl[j], nig[j], x) * rp[j];
+        cnt[j][8] = nig[j] * rp[j];
+#pragma unroll
+        for (int x = 0; x < 9; ++x) sb[x] += cnt[j][x];
+    }
+    block_scan_excl<9>(sb, tb, P.red);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int pos = S * t + j;
+        if (pos < a.B) {
+            P.g0[pos] = gl[j];
+            P.slot0[pos] = sb[8];
+#pragma unroll
+            for (int x = 0; x < 8; ++x) P.lane0[x][pos] = sb[x];
+            if (blockIdx.x == 0) a.plan_seq[P.b[pos]] = make_int4(P.ns[pos], rp[j], sb[8], 0);
+        }
+#pragma unroll
+        for (int x = 0; x < 9; ++x) sb[x] += cnt[j][x];
     }
     if (t < 8) P.lane_len[t] = tb[t];
     int longest = 0;

@@ -241,27 +241,34 @@ def test_balanced_schedule_random_batches(gpu, seed):
     h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
 
 
-def test_balanced_schedule_at_most_256_sequences(gpu):
-    """256 sequences (one per thread of the plan), lengths from 1 to 600 tokens; 257 is refused
-    under "balanced" and planned on the grid under "auto"."""
+@pytest.mark.parametrize("batch", [256, 1024])
+def test_balanced_schedule_large_batches(gpu, batch):
+    """256 sequences (ordered longest first by the plan) and 1024 (four per plan thread, kept in
+    their order), lengths from 1 to 600 tokens with every 97th sequence at 3000; 1025 sequences
+    are refused under "balanced" and run on the grid under "auto"."""
     rng = np.random.default_rng(3)
-    ctx = rng.integers(1, 600, size=256).tolist()
-    ql = rng.integers(1, 6, size=256).tolist()
+    ctx = rng.integers(1, 600, size=batch)
+    ctx[::97] = 3000
+    ctx = ctx.tolist()
+    ql = rng.integers(1, 6, size=batch).tolist()
     case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=8, num_kv_heads=2,
                                   dtype="bf16", seed=4)
     t = h.attention_tensors(case, gpu)
     attn = make_attention(16, 8, 128, 2)
     args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
     out = attn.forward(*args, q_start_loc=t["q_start_loc"], path="mfma", schedule="balanced")
-    h.assert_attention_close(out, case, h.oracle_attention(case, [0, 1, 77, 128, 254, 255]), h.ATOL_BF16)
+    seqs = sorted({0, 1, 97, 128, batch // 2, batch - 2, batch - 1})
+    h.assert_attention_close(out, case, h.oracle_attention(case, seqs), h.ATOL_BF16)
+    if batch < 1024:
+        return
     case2 = wl.make_attention_case(context_lens=ctx + [500], q_lens=ql + [2], num_heads=8, num_kv_heads=2,
                                    dtype="bf16", seed=4)
     t2 = h.attention_tensors(case2, gpu)
     args2 = (t2["query"], t2["key_cache"], t2["value_cache"], t2["block_table"], t2["context_lens"])
-    with pytest.raises(kyro_amd.KyroError, match="at most 256"):
+    with pytest.raises(kyro_amd.KyroError, match="at most 1024"):
         attn.forward(*args2, q_start_loc=t2["q_start_loc"], path="mfma", schedule="balanced")
     out2 = attn.forward(*args2, q_start_loc=t2["q_start_loc"], path="mfma")
-    h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 255, 256]), h.ATOL_BF16)
+    h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 1023, 1024]), h.ATOL_BF16)
 
 
 def test_balanced_schedule_errors(gpu):
