@@ -79,7 +79,13 @@ int kyro_ctx_destroy(kyro_ctx ctx);
  * until this is called. The caller keeps ownership of the stream. */
 int kyro_ctx_set_stream(kyro_ctx ctx, void* hip_stream);
 
-/* Grows the context's scratch arena to at least `bytes` now, so later calls do not allocate. */
+/* Grows the context's scratch arena to at least `bytes` now, so later calls do not allocate.
+ * A call that needs more arena than the context holds synchronises the stream, frees the arena
+ * and allocates a larger one; kernels captured into a HIP graph before that point would then
+ * address freed memory. A caller that captures calls into a graph should reserve the largest
+ * arena those calls need first (or re-capture after a growth). The balanced attention schedule
+ * also keeps small counters in the context that every launch returns to zero, so its launches
+ * replay from a graph as they run eagerly. */
 int kyro_ctx_reserve(kyro_ctx ctx, size_t bytes);
 
 /* Waits for all work queued on the context's stream, then reports latched device errors. */
