@@ -271,6 +271,41 @@ def test_balanced_schedule_large_batches(gpu, batch):
     h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 1023, 1024]), h.ATOL_BF16)
 
 
+def test_balanced_schedule_replays_from_a_graph(gpu):
+    """A balanced launch (plan, per-lane claim counters, combine pass) captured in a HIP graph
+    after an eager call on the same stream (so the arena is already large enough): every replay,
+    with eager launches of another shape and synchronisations in between, equals the eager
+    result bit for bit."""
+    case = wl.make_attention_case(context_lens=[3000, 17, 0, 900, 5000, 33], q_lens=[8, 8, 3, 1, 5, 8],
+                                  num_heads=32, num_kv_heads=8, dtype="bf16", seed=23)
+    other = wl.make_attention_case(context_lens=[700, 2100], q_lens=[2, 3], num_heads=32, num_kv_heads=8,
+                                   dtype="bf16", seed=24)
+    t = h.attention_tensors(case, gpu)
+    t2 = h.attention_tensors(other, gpu)
+    attn = make_attention(16, 32, 128, 8)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    args2 = (t2["query"], t2["key_cache"], t2["value_cache"], t2["block_table"], t2["context_lens"])
+    s = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(s):
+        eager = attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
+        eager2 = attn.forward(*args2, q_start_loc=t2["q_start_loc"], schedule="balanced")
+        out = torch.empty_like(eager)
+    torch.cuda.synchronize()
+    h.assert_attention_close(eager, case, h.oracle_attention(case), h.ATOL_BF16)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", out=out, max_q_len=8)
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        with torch.cuda.stream(s):
+            again = attn.forward(*args2, q_start_loc=t2["q_start_loc"], schedule="balanced")
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager2)
+
+
 def test_balanced_schedule_errors(gpu):
     case = wl.make_attention_case(context_lens=[300, 40], q_lens=[2, 3], num_heads=8, num_kv_heads=2,
                                   dtype="bf16", seed=6)
