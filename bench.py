@@ -94,6 +94,20 @@ def cpu_baseline(sample: int, threads: int):
                            vcase.temperature, vcase.u_accept, vcase.u_resample, precision="f32")
     t2 = time.perf_counter()
     tokens = int(np.sum(r["accepted"] + 1))
+    # The same step on one core, over the first `sample1` sequences (the oracle's per-sequence
+    # work does not depend on the batch it sits in).
+    sample1 = max(1, min(sample, 16))
+    acase1 = wl.gqa_llama3_8b(batch=sample1, ctx=CTX)
+    vcase1 = wl.verify_llama3_8b(batch=sample1, vocab=VOCAB)
+    t3 = time.perf_counter()
+    oracle.paged_attention_mq(acase1.query, acase1.key_cache, acase1.value_cache, acase1.block_table,
+                              acase1.context_lens, num_heads=HQ, num_kv_heads=HKV, head_dim=D,
+                              block_size=BS, q_start_loc=acase1.q_start_loc, threads=1,
+                              precision="f32")
+    r1 = oracle.spec_verify(vcase1.target, vcase1.draft, vcase1.draft_tokens, vcase1.num_draft,
+                            vcase1.temperature, vcase1.u_accept, vcase1.u_resample, precision="f32")
+    t4 = time.perf_counter()
+    tokens1 = int(np.sum(r1["accepted"] + 1))
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -110,6 +124,8 @@ def cpu_baseline(sample: int, threads: int):
                    f"{threads} threads ({t1 - t0:.2f} s), acceptance on 1 thread ({t2 - t1:.2f} s)"),
         "cpu_model": model,
         "host_cpus": os.cpu_count(),
+        "one_core": {"value": tokens1 / (t4 - t3), "unit": "tok/s", "cores": 1,
+                     "sample": f"{sample1} sequences of the same step on 1 thread ({t4 - t3:.2f} s)"},
     }
 
 
