@@ -71,16 +71,20 @@ constexpr int kSchedWords = 9;
 constexpr int kPlanMaxSeqs = 1024;
 // Shortest split the balanced schedule makes, in blocks.
 constexpr int kPlanMinChunk = 16;
+// A sequence longer than the per-workgroup share L of the work splits into chunks of about
+// L / kPlanChunkDiv blocks. The slot bound below depends on it: change both together.
+constexpr int kPlanChunkDiv = 2;
 
 // Upper bound on the partial-state slots of a balanced-schedule launch: the per-sequence
-// chunk is at least half the per-workgroup share of the work (or the longest chunk allowed),
-// so the splits number at most 2 x grid (or work / max_chunk) plus one per (kv head group,
-// row group) of every sequence.
+// chunk is at least L / kPlanChunkDiv (or the longest chunk allowed), so the splits number at
+// most kPlanChunkDiv x grid (or work / max_chunk) plus one per (kv head group, row group) of
+// every sequence.
 inline long long plan_slot_bound(long long B, long long ugroups_per_seq, long long row_groups, long long max_blocks,
                                  long long max_chunk, long long grid) {
     const long long s = B * ugroups_per_seq * row_groups;
     const long long by_chunk = (s * max_blocks + max_chunk - 1) / max_chunk;
-    return s + (by_chunk > 2 * grid ? by_chunk : 2 * grid);
+    const long long by_share = (long long)kPlanChunkDiv * grid;
+    return s + (by_chunk > by_share ? by_chunk : by_share);
 }
 
 // Block pairs one MFMA wave can hold the ids of (two 64-lane slots). A split has at most

@@ -300,7 +300,8 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //  * work of sequence b: W_b = kv head groups x row groups x blocks; per-workgroup share
 //    L = ceil(sum W / grid);
 //  * chunk C = L when no sequence is longer than L (nothing splits, so a uniform batch keeps one
-//    item per (sequence, kv head group)), else ceil(L / 2), within [kPlanMinChunk, max chunk];
+//    item per (sequence, kv head group)), else ceil(L / kPlanChunkDiv) (L / 2), within
+//    [kPlanMinChunk, max chunk];
 //    a longer sequence splits into equal even chunks;
 //  * sequences are ordered by chunk length, longest first (lower index first among equals), so
 //    the longest items start first;
@@ -453,7 +454,7 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         maxnb = max(maxnb, P.red[i][0]);
     }
     const long long L = (T + a.plan_grid - 1) / a.plan_grid;
-    long long CL = maxnb <= L ? L : (L + 1) / 2;
+    long long CL = maxnb <= L ? L : (L + kPlanChunkDiv - 1) / kPlanChunkDiv;
     CL = CL < kPlanMinChunk ? kPlanMinChunk : CL;
     CL = (CL + 1) & ~1ll;
     const int C = (int)(CL > a.plan_max_chunk ? a.plan_max_chunk : CL);
