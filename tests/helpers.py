@@ -2,6 +2,8 @@
 subset of sequences, and compare verify results with the documented exemptions."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import torch
 
@@ -12,6 +14,7 @@ ATOL_BF16 = 2e-2   # attention outputs, bf16 inputs
 ATOL_F32 = 1e-3    # attention outputs, f32 inputs
 PROB_ATOL = 1e-5   # p_i(x_i), q_i(x_i)
 MARGIN = 1e-5      # decisions with |u - boundary| below this may differ under f32 rounding
+ORACLE_THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 def to_device(a: np.ndarray, device, bf16: bool = False) -> torch.Tensor:
@@ -48,7 +51,7 @@ def oracle_attention(case: wl.AttentionCase, seqs=None, causal=True) -> dict:
             np.arange(nb, dtype=np.int64)[None], np.array([ctx], np.int64),
             num_heads=case.num_heads, num_kv_heads=case.num_kv_heads, head_dim=case.head_dim,
             block_size=case.block_size, q_start_loc=np.array([0, q1 - q0], np.int32), causal=causal,
-            threads=8)
+            threads=ORACLE_THREADS)
     return res
 
 

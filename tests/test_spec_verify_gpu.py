@@ -137,6 +137,19 @@ def test_full_llama3_8b(gpu):
     assert 0 < res.accepted.float().mean().item() < 7
 
 
+def test_full_skewed(gpu):
+    """Acceptance half of the skewed long-context workload (B 32, k 4, V 128256, T 1.0): the
+    default window (lazy rows after draft 3) and every row in one pass, both against the oracle."""
+    case = wl.verify_skewed()
+    orc = h.oracle_verify(case)
+    t = h.verify_tensors(case, gpu)
+    res = kyro_amd.verify_drafts(**t, return_probs=True)
+    h.assert_verify_parity(res, case, orc, max_exempt=1)
+    eager = kyro_amd.verify_drafts(**t, return_probs=True, window=64)
+    h.assert_verify_parity(eager, case, orc, max_exempt=1)
+    assert torch.equal(res.accepted, eager.accepted) and torch.equal(res.tokens, eager.tokens)
+
+
 def test_full_mixed_llama3_70b(gpu):
     _, k = wl.mixed_llama3_70b()
     case = wl.verify_mixed(k)
