@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 7
+#define KYRO_ABI_VERSION 8
 
 typedef enum kyro_status {
     KYRO_OK = 0,
@@ -193,6 +193,35 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* par
                             const int64_t* block_table, const int64_t* context_lens,
                             void* out);
 
+/* Scratch bytes a kyro_paged_attention_mq call with these params takes from the context's arena
+ * (has_q_start_loc: whether the call passes q_start_loc). Host only, no device work; ctx may be
+ * NULL, which sizes for a 256-CU device. A caller that captures calls into a HIP graph passes the
+ * largest of these to kyro_ctx_reserve first. No counterpart in the reference (candle allocates
+ * per op). */
+int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_params* params,
+                                   int has_q_start_loc, size_t* bytes);
+
+/* The balanced schedule's plan for one batch, computed on the host with the chunk and split
+ * arithmetic the device plan runs, from host copies of the context lengths and the per-sequence
+ * query rows (q_lens NULL: one row each). For analysis and tests; no counterpart in the
+ * reference. num_cus 0 means 256; chunk_div 0 means the library's divisor (a sequence longer than
+ * the per-workgroup share L of the work splits into chunks of about L / chunk_div blocks; other
+ * values model other divisors, the slot bound included). Fails with KYRO_EINVAL when the params
+ * would run on the grid schedule. out_splits [B] (may be NULL): splits per sequence (0 for a
+ * sequence without rows). */
+typedef struct kyro_attention_plan {
+    int32_t grid;          /* persistent workgroups */
+    int32_t chunk_blocks;  /* blocks per split of a sequence that splits */
+    int64_t items;         /* work items: sequence x kv head group x split x row group, one
+                              partial-state slot each */
+    int64_t slot_bound;    /* partial-state slots a launch with these params sizes; the device
+                              latches KYRO_EINVAL instead of running a plan with more items */
+} kyro_attention_plan;
+
+int kyro_paged_attention_plan(const kyro_paged_attention_params* params, int num_cus, int chunk_div,
+                              const int64_t* context_lens, const int32_t* q_lens, int32_t* out_splits,
+                              kyro_attention_plan* out);
+
 /* ---------------------------------------------------------------- speculative verify */
 
 typedef struct kyro_spec_verify_params {
@@ -239,6 +268,10 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* params,
                      const float* temperature, const float* u_accept, const float* u_resample,
                      int32_t* out_accepted, uint32_t* out_tokens,
                      float* out_p_draft, float* out_q_draft);
+
+/* Scratch bytes a kyro_spec_verify call with these params takes from the context's arena. Host
+ * only, no device work. */
+int kyro_spec_verify_workspace(const kyro_spec_verify_params* params, size_t* bytes);
 
 /* ---------------------------------------------------------------- paged KV write */
 

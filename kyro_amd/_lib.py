@@ -52,6 +52,11 @@ class SpecVerifyParams(ctypes.Structure):
     ]
 
 
+class AttentionPlan(ctypes.Structure):
+    _fields_ = [("grid", ctypes.c_int32), ("chunk_blocks", ctypes.c_int32), ("items", ctypes.c_int64),
+                ("slot_bound", ctypes.c_int64)]
+
+
 class KvAppendParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in (
         "block_size", "num_kv_heads", "head_dim", "batch_size", "total_q", "max_blocks_per_seq",
@@ -66,7 +71,7 @@ class SampleParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("batch_size", "vocab_size", "logits_dtype", "num_masks")]
 
 
-ABI_VERSION = 7  # KYRO_ABI_VERSION of include/kyro_verify.h
+ABI_VERSION = 8  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -88,7 +93,12 @@ _SIGNATURES = {
     "kyro_buf_upload": ([_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t], ctypes.c_int),
     "kyro_buf_download": ([_P, _P, _P, ctypes.c_size_t, ctypes.c_size_t], ctypes.c_int),
     "kyro_paged_attention_mq": ([_P, ctypes.POINTER(PagedAttentionParams)] + [_P] * 7, ctypes.c_int),
+    "kyro_paged_attention_workspace": ([_P, ctypes.POINTER(PagedAttentionParams), ctypes.c_int,
+                                        ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "kyro_paged_attention_plan": ([ctypes.POINTER(PagedAttentionParams), ctypes.c_int, ctypes.c_int, _P, _P, _P,
+                                   ctypes.POINTER(AttentionPlan)], ctypes.c_int),
     "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
+    "kyro_spec_verify_workspace": ([ctypes.POINTER(SpecVerifyParams), ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "kyro_paged_kv_append": ([_P, ctypes.POINTER(KvAppendParams)] + [_P] * 7, ctypes.c_int),
     # include/kyro_blocks.h
     "kyro_radix_create": ([ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(_P)], ctypes.c_int),

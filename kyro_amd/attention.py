@@ -78,9 +78,12 @@ class PagedAttention:
 
     def forward_async(self, query, key_cache, value_cache, block_table, context_lens, *,
                       q_start_loc=None, max_q_len=None, causal=True, out_dtype=torch.float32,
-                      path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto", schedule="auto"):
+                      path="auto", num_splits=0, scale=None, out=None, kv_reuse="auto", schedule="auto",
+                      context=None):
         """Queues the kernel on torch's current stream and returns without synchronising.
-        Device-detected errors surface at the next ``kyro_amd.sync(device)``."""
+        Device-detected errors surface at the next ``kyro_amd.sync(device)``. ``context`` (a
+        ``kyro_amd._lib.Context``) runs the call on that context and its arena instead of the
+        process-wide one of the device."""
         dev = query.device
         if dev.type != "cuda":
             raise ValueError("PagedAttention.forward runs on a GPU device; got " + str(dev))
@@ -125,7 +128,7 @@ class PagedAttention:
             block_table.shape[1], nb, _DTYPES[query.dtype], _DTYPES[out_dtype], 1 if causal else 0,
             float(scale) if scale else 0.0, _PATHS[path], int(num_splits), int(max_q_len),
             _KV_REUSE[kv_reuse], _SCHEDULES[schedule])
-        ctx = _lib.context(dev.index or 0)
+        ctx = context if context is not None else _lib.context(dev.index or 0)
         ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
         _lib.check(_lib.lib().kyro_paged_attention_mq(
             ctx.handle, ctypes.byref(params), query.data_ptr(),
@@ -133,3 +136,29 @@ class PagedAttention:
             key_cache.data_ptr(), value_cache.data_ptr(), block_table.data_ptr(),
             context_lens.data_ptr(), out.data_ptr()))
         return out
+
+
+def attention_plan(attn: PagedAttention, context_lens, q_lens=None, *, max_blocks_per_seq: int,
+                   num_blocks: int = 1, dtype=torch.bfloat16, schedule: str = "balanced",
+                   num_cus: int = 0, chunk_div: int = 0):
+    """The balanced schedule's plan of a batch, computed on the host by the library
+    (``kyro_paged_attention_plan``) from host arrays of context lengths and per-sequence query
+    rows. No GPU is needed. Returns (kyro_attention_plan fields as a dict, splits per sequence)."""
+    import numpy as np
+
+    ctx = np.ascontiguousarray(context_lens, dtype=np.int64)
+    batch = int(ctx.shape[0])
+    ql = None if q_lens is None else np.ascontiguousarray(q_lens, dtype=np.int32)
+    total_q = batch if ql is None else int(ql.sum())
+    max_q_len = 1 if ql is None else max(1, int(ql.max()) if batch else 1)
+    params = _lib.PagedAttentionParams(
+        attn.block_size, attn.num_heads, attn.head_dim, attn.num_kv_heads, batch, total_q,
+        int(max_blocks_per_seq), int(num_blocks), _DTYPES[dtype], _lib.KYRO_F32, 1, 0.0, _lib.KYRO_ATTN_MFMA, 0,
+        max_q_len, _lib.KYRO_KV_REUSE_AUTO, _SCHEDULES[schedule])
+    out = _lib.AttentionPlan()
+    splits = np.zeros(batch, np.int32)
+    _lib.check(_lib.lib().kyro_paged_attention_plan(
+        ctypes.byref(params), int(num_cus), int(chunk_div), ctx.ctypes.data,
+        ql.ctypes.data if ql is not None else None, splits.ctypes.data, ctypes.byref(out)))
+    info = {f: getattr(out, f) for f, _ in _lib.AttentionPlan._fields_}
+    return info, splits

@@ -13,6 +13,7 @@
 
 struct kyro_ctx_s {
     int device = 0;
+    int num_cus = 256;      // compute units of the device (hipDeviceAttributeMultiprocessorCount)
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     void* arena = nullptr;  // per-call scratch, stream-ordered

@@ -13,7 +13,8 @@ enum ErrorBits : int {
     ERR_Q_LAYOUT = 4,   // q_start_loc not monotone, out of [0, total_q], or a q_len > max_q_len
     ERR_TOKEN = 8,      // draft token id >= vocab_size
     ERR_NUM_DRAFT = 16, // num_draft outside [0, max_draft]
-    ERR_NO_DRAFT = 32   // a sampled sequence with drafts but no draft_logits
+    ERR_NO_DRAFT = 32,  // a sampled sequence with drafts but no draft_logits
+    ERR_PLAN = 64       // balanced attention schedule: more partial-state slots than the host sized
 };
 
 
@@ -59,6 +60,7 @@ struct AttnArgs {
     int plan_grid;
     int plan_rw;
     int plan_max_chunk;
+    long long plan_slots;  // partial-state slots in the workspace (plan_slot_bound)
     int4* plan_seq;
     // kSchedWords counters, zero at launch: the items claimed on each of the 8 XCD lanes beyond
     // the grid's first items, then the workgroups done; the last workgroup resets them to zero.
@@ -72,18 +74,47 @@ constexpr int kPlanMaxSeqs = 1024;
 // Shortest split the balanced schedule makes, in blocks.
 constexpr int kPlanMinChunk = 16;
 // A sequence longer than the per-workgroup share L of the work splits into chunks of about
-// L / kPlanChunkDiv blocks. The slot bound below depends on it: change both together.
+// L / kPlanChunkDiv blocks. plan_slot_bound takes the same divisor.
 constexpr int kPlanChunkDiv = 2;
 
-// Upper bound on the partial-state slots of a balanced-schedule launch: the per-sequence
-// chunk is at least L / kPlanChunkDiv (or the longest chunk allowed), so the splits number at
-// most kPlanChunkDiv x grid (or work / max_chunk) plus one per (kv head group, row group) of
-// every sequence.
-inline long long plan_slot_bound(long long B, long long ugroups_per_seq, long long row_groups, long long max_blocks,
-                                 long long max_chunk, long long grid) {
+// Balanced-schedule chunk length in blocks, from the total work T (kv head groups x row groups x
+// blocks, summed over sequences), the longest sequence maxnb (blocks) and the persistent grid:
+// L = ceil(T / grid); C = L when no sequence is longer than L, else ceil(L / div); then at least
+// kPlanMinChunk, rounded up to even, at most max_chunk (even). The device plan and the host
+// checks share this function.
+__host__ __device__ inline int plan_chunk_blocks(long long T, int maxnb, int grid, int max_chunk,
+                                                 int div = kPlanChunkDiv) {
+    const long long L = (T + grid - 1) / grid;
+    long long CL = maxnb <= L ? L : (L + div - 1) / div;
+    CL = CL < kPlanMinChunk ? kPlanMinChunk : CL;
+    CL = (CL + 1) & ~1ll;
+    return (int)(CL > max_chunk ? max_chunk : CL);
+}
+
+// Splits of a sequence of nb blocks under chunk length C: one split when nb <= C, else
+// ns = ceil(nb / C) equal chunks of ch blocks (even), the last one shorter.
+__host__ __device__ inline void plan_split(int nb, int C, int& ns, int& ch) {
+    ns = 1;
+    ch = nb;
+    if (nb > C) {
+        ns = (nb + C - 1) / C;
+        ch = (nb + ns - 1) / ns;
+        ch = (ch + 1) & ~1;
+        ns = (nb + ch - 1) / ch;
+    }
+}
+
+// Upper bound on the partial-state slots of a balanced-schedule launch (one slot per item:
+// sequence x kv head group x split x row group). Every split but one per item group is at least
+// C >= min(L / div, max_chunk) blocks long, so the extra splits number at most div x grid (or
+// work / max_chunk), plus one per (kv head group, row group) of every sequence. The device plan
+// compares its slot total with this bound and latches ERR_PLAN instead of writing past it.
+__host__ __device__ inline long long plan_slot_bound(long long B, long long ugroups_per_seq, long long row_groups,
+                                                     long long max_blocks, long long max_chunk, long long grid,
+                                                     int div = kPlanChunkDiv) {
     const long long s = B * ugroups_per_seq * row_groups;
     const long long by_chunk = (s * max_blocks + max_chunk - 1) / max_chunk;
-    const long long by_share = (long long)kPlanChunkDiv * grid;
+    const long long by_share = (long long)div * grid;
     return s + (by_chunk > by_share ? by_chunk : by_share);
 }
 

@@ -453,24 +453,13 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         T += P.red64[i];
         maxnb = max(maxnb, P.red[i][0]);
     }
-    const long long L = (T + a.plan_grid - 1) / a.plan_grid;
-    long long CL = maxnb <= L ? L : (L + kPlanChunkDiv - 1) / kPlanChunkDiv;
-    CL = CL < kPlanMinChunk ? kPlanMinChunk : CL;
-    CL = (CL + 1) & ~1ll;
-    const int C = (int)(CL > a.plan_max_chunk ? a.plan_max_chunk : CL);
+    const int C = plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk);
     int ns[S], ch[S];
     uint32_t key[S];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int sq = t + j * kThreads;
-        ns[j] = 1;
-        ch[j] = nb[j];
-        if (nb[j] > C) {
-            ns[j] = (nb[j] + C - 1) / C;
-            ch[j] = (nb[j] + ns[j] - 1) / ns[j];
-            ch[j] = (ch[j] + 1) & ~1;
-            ns[j] = (nb[j] + ch[j] - 1) / ch[j];
-        }
+        plan_split(nb[j], C, ns[j], ch[j]);
         key[j] = ((uint32_t)(r[j] > 0 ? ch[j] : 0) << 16) | (uint32_t)(0xffff - sq);
         P.key[sq] = sq < a.B ? key[j] : 0u;  // padding keys rank below every sequence
     }
@@ -526,6 +515,17 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         for (int x = 0; x < 9; ++x) sb[x] += cnt[j][x];
     }
     block_scan_excl<9>(sb, tb, P.red);
+    if (tb[8] > a.plan_slots) {
+        // More partial-state slots than the workspace holds: a plan/bound mismatch. Latch it and
+        // run no item (every workgroup derives the same totals, so all of them skip the walk and
+        // still count themselves done); the combine pass sees no row groups anywhere.
+        if (t < 8) P.lane_len[t] = 0;
+        for (int pos = t; pos < a.B; pos += kThreads)
+            if (blockIdx.x == 0) a.plan_seq[pos] = make_int4(0, 0, 0, 0);
+        if (blockIdx.x == 0 && t == 0) latch_error(a.err, ERR_PLAN);
+        __syncthreads();
+        return 0;
+    }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int pos = S * t + j;

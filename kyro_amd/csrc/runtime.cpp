@@ -8,9 +8,11 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "context.hpp"
 #include "kernels.hpp"
@@ -46,6 +48,15 @@ int check_ctx(kyro_ctx ctx) {
 
 int ensure_arena(kyro_ctx ctx, size_t bytes) {
     if (bytes <= ctx->arena_bytes) return KYRO_OK;
+    // Growing frees the arena that kernels already captured into a graph would address, and a
+    // synchronisation inside a capture invalidates it: refuse, and name what to reserve.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    KYRO_HIP(hipStreamIsCapturing(ctx->stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(KYRO_EINVAL, "the call needs %zu bytes of scratch arena and the context holds %zu; the stream "
+                    "is capturing a graph, so the arena cannot grow now: call kyro_ctx_reserve(ctx, %zu) "
+                    "(or the size queries kyro_paged_attention_workspace / kyro_spec_verify_workspace) "
+                    "before capturing", bytes, ctx->arena_bytes, bytes);
     const size_t want = align_up(std::max(bytes, ctx->arena_bytes * 3 / 2), size_t(1) << 20);
     KYRO_HIP(hipStreamSynchronize(ctx->stream));
     if (ctx->arena) KYRO_HIP(hipFree(ctx->arena));
@@ -124,7 +135,284 @@ int sync_and_report(kyro_ctx ctx) {
     if (err & kyro::ERR_TOKEN) msg += " a draft, bias or penalty token id >= vocab_size, or a mask_row >= num_masks;";
     if (err & kyro::ERR_NUM_DRAFT) msg += " num_draft outside [0, max_draft];";
     if (err & kyro::ERR_NO_DRAFT) msg += " draft_logits is NULL but a sampled sequence has drafts;";
+    if (err & kyro::ERR_PLAN)
+        msg += " balanced attention schedule: the plan needs more partial-state slots than were sized "
+               "(internal error; no item ran);";
     return fail(KYRO_EINVAL, "%s", msg.c_str());
+}
+
+}  // namespace
+
+namespace {
+
+constexpr int kDefaultCUs = 256;  // MI355X; used when no context (device) is given
+
+// Everything a paged-attention launch decides from its params alone: validation, kernel, work
+// decomposition, schedule and workspace size. No device call.
+struct AttnSetup {
+    kyro::AttnArgs a{};
+    int kernel = 0;
+    bool empty = false;      // nothing to launch (B or total_q is 0)
+    size_t plan_slots = 0;   // balanced schedule: partial-state slots sized
+    size_t ws_bytes = 0;     // arena bytes the launch takes
+};
+
+int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int num_cus, AttnSetup& s,
+                    int chunk_div = kyro::kPlanChunkDiv) {
+    if (!p) return fail(KYRO_EINVAL, "paged_attention: params is null");
+    if (p->block_size <= 0 || p->num_heads <= 0 || p->head_dim <= 0 || p->num_kv_heads <= 0)
+        return fail(KYRO_EINVAL, "paged_attention: block_size/num_heads/head_dim/num_kv_heads must be > 0");
+    if (p->num_heads % p->num_kv_heads != 0)
+        return fail(KYRO_EINVAL, "paged_attention: num_heads %d not a multiple of num_kv_heads %d",
+                    p->num_heads, p->num_kv_heads);
+    if (p->batch_size < 0 || p->total_q < 0 || p->max_blocks_per_seq < 0 || p->num_blocks < 0)
+        return fail(KYRO_EINVAL, "paged_attention: negative shape");
+    if (p->dtype != KYRO_F32 && p->dtype != KYRO_BF16)
+        return fail(KYRO_EINVAL, "paged_attention: dtype %d unknown", p->dtype);
+    if (p->out_dtype != KYRO_F32 && p->out_dtype != KYRO_BF16)
+        return fail(KYRO_EINVAL, "paged_attention: out_dtype %d unknown", p->out_dtype);
+    if (!have_q_start && p->total_q != p->batch_size)
+        return fail(KYRO_EINVAL, "paged_attention: total_q %d != batch_size %d without q_start_loc",
+                    p->total_q, p->batch_size);
+    if (p->head_dim != 64 && p->head_dim != 128)
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: 64, 128)", p->head_dim);
+    if (p->path < KYRO_ATTN_AUTO || p->path > KYRO_ATTN_MFMA)
+        return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
+    if (p->kv_reuse < KYRO_KV_REUSE_AUTO || p->kv_reuse > KYRO_KV_REUSE_STREAM)
+        return fail(KYRO_EINVAL, "paged_attention: kv_reuse %d unknown", p->kv_reuse);
+    if (p->schedule < KYRO_ATTN_SCHEDULE_AUTO || p->schedule > KYRO_ATTN_SCHEDULE_BALANCED)
+        return fail(KYRO_EINVAL, "paged_attention: schedule %d unknown", p->schedule);
+    if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->num_splits != 0)
+        return fail(KYRO_EINVAL, "paged_attention: the balanced schedule chooses its own splits (num_splits must be 0)");
+    if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->batch_size > kyro::kPlanMaxSeqs)
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule plans at most %d sequences",
+                    kyro::kPlanMaxSeqs);
+    if (p->batch_size == 0 || p->total_q == 0) {
+        s.empty = true;
+        return KYRO_OK;
+    }
+    const int group = p->num_heads / p->num_kv_heads;
+    int max_q_len = p->max_q_len;
+    if (max_q_len <= 0) max_q_len = have_q_start ? p->total_q : 1;
+    if (!have_q_start) max_q_len = 1;
+
+    const bool mfma_ok = p->head_dim == 128 && p->block_size == 16;  // bf16 or f32 caches
+    int kernel;
+    if (p->path == KYRO_ATTN_MFMA) {
+        if (!mfma_ok)
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs head_dim 128, block_size 16");
+        kernel = kyro::ATTN_KERNEL_MFMA;
+    } else if (p->path == KYRO_ATTN_VECTOR) {
+        kernel = kyro::ATTN_KERNEL_VECTOR;
+    } else {
+        // MFMA wherever it applies, one query row per kv head included: the kernel is
+        // memory-bound, so padding rows to a 16-row tile costs nothing measurable (MHA decode,
+        // 1 row per kv head: 67 us against the vector kernel's 207 us).
+        kernel = mfma_ok ? kyro::ATTN_KERNEL_MFMA : kyro::ATTN_KERNEL_VECTOR;
+    }
+    if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
+                    "(head_dim 128, block_size 16)");
+
+    kyro::AttnArgs& a = s.a;
+    a.B = p->batch_size;
+    a.H = p->num_heads;
+    a.Hkv = p->num_kv_heads;
+    a.group = group;
+    a.D = p->head_dim;
+    a.bs = p->block_size;
+    a.max_blocks = p->max_blocks_per_seq;
+    a.num_blocks = p->num_blocks;
+    a.total_q = p->total_q;
+    a.max_q_len = max_q_len;
+    a.rows_cap = group * max_q_len;
+    a.causal = p->causal ? 1 : 0;
+    a.out_bf16 = p->out_dtype == KYRO_BF16;
+    a.dtype_bf16 = p->dtype == KYRO_BF16;
+    const double scale = p->scale > 0 ? (double)p->scale : 1.0 / std::sqrt((double)p->head_dim);
+    a.scale_log2 = (float)(scale * 1.4426950408889634);
+    a.units = p->batch_size * p->num_kv_heads;
+    // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
+    // waves per head): the workgroup then reads both heads' slabs of each block together, and
+    // the Llama-3-8B step fits the chip in one round of workgroups.
+    a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0) ? 2 : 1;
+    a.ugroups = a.units / a.hpw;
+    a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
+    // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
+    // (vector) or 16 / 32 (MFMA) rows that stream the same K/V.
+    const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
+                                                                : kyro::kVectorRowsPerGroup;
+    a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
+    // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
+    // of a kv head, or (as the caller says) other sequences holding the same blocks.
+    a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
+
+    // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
+    const int mb = std::max(1, p->max_blocks_per_seq);
+    int splits = p->num_splits;
+    if (splits <= 0) {
+        // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
+        // one CU streaming it alone; more splits only when the workgroups cannot cover the
+        // chip's CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
+        // With four or more workgroups per CU already, splitting only adds per-workgroup
+        // set-up and a combine pass (one workgroup fills a CU, so nothing hides them).
+        constexpr int kTargetChunk = 256, kMinChunk = 16;
+        const int kCUs = num_cus;
+        const int per_split = a.ugroups * a.row_groups;
+        splits = per_split >= 4 * kCUs ? 1 : (mb + kTargetChunk - 1) / kTargetChunk;
+        if (per_split * splits < kCUs)
+            splits = std::min((kCUs + per_split - 1) / per_split, std::max(1, mb / kMinChunk));
+    }
+    // Longest split: the LDS block-id staging, and for the MFMA kernel the block pairs a wave
+    // holds ids for (its waves per head x two 64-lane slots).
+    const int max_chunk = kernel == kyro::ATTN_KERNEL_MFMA
+                              ? std::min(kyro::kMaxChunkBlocks, 2 * kyro::kMfmaMaxPairsPerWave * (4 / a.hpw))
+                              : kyro::kMaxChunkBlocks;
+    splits = std::min(splits, mb);
+    splits = std::max(splits, (mb + max_chunk - 1) / max_chunk);
+    int chunk = (mb + splits - 1) / splits;
+    chunk = std::min((chunk + 1) / 2 * 2, max_chunk);
+    splits = (mb + chunk - 1) / chunk;
+    a.splits = splits;
+    a.chunk_blocks = chunk;
+    // The balanced schedule: asked for, or where the grid's splits (from the table width
+    // alone) would have to guess at the context lengths: a split grid, or a table wider than
+    // 256 blocks (4096 tokens), where a few long sequences can leave one workgroup streaming
+    // long after the rest of the chip is idle.
+    a.plan = kernel == kyro::ATTN_KERNEL_MFMA && p->num_splits == 0 && p->batch_size <= kyro::kPlanMaxSeqs &&
+             (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED ||
+              (p->schedule == KYRO_ATTN_SCHEDULE_AUTO && (splits > 1 || mb > 256)));
+    if (a.plan) {
+        // One persistent workgroup per CU, in whole rounds of the 8 XCD lanes the plan deals
+        // to (a partitioned device with fewer CUs still gets every lane covered).
+        a.plan_grid = std::max(8, num_cus / 8 * 8);
+        a.plan_rw = rows_per_group;
+        a.plan_max_chunk = max_chunk / 2 * 2;
+        a.splits = 1;
+        s.plan_slots = (size_t)kyro::plan_slot_bound(a.B, a.ugroups / a.B, a.row_groups, mb, a.plan_max_chunk,
+                                                     a.plan_grid, chunk_div);
+        // KYRO_TEST_PLAN_SLOT_CAP lowers the slots sized, so that a test can drive the device
+        // plan's overflow check (ERR_PLAN, no item runs) without a plan/bound mismatch.
+        if (const char* cap = std::getenv("KYRO_TEST_PLAN_SLOT_CAP")) {
+            const long long c = std::atoll(cap);
+            if (c > 0 && (size_t)c < s.plan_slots) s.plan_slots = (size_t)c;
+        }
+        a.plan_slots = (long long)s.plan_slots;
+    }
+    // One launch carries at most 2^32 - 1 work items along x.
+    if (!a.plan && (uint64_t)a.ugroups_padded * splits * a.row_groups * 256 > 0xffffffffull)
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: %d units x %d splits x %d row groups is too large for one launch",
+                    a.units, splits, a.row_groups);
+    s.kernel = kernel;
+    if (a.plan) {
+        const size_t rows = s.plan_slots * a.hpw * a.plan_rw;
+        s.ws_bytes = 2 * align_up(rows * sizeof(float), 256) + align_up(rows * a.D * sizeof(float), 256) +
+                     align_up((size_t)a.B * sizeof(int4), 256);
+    } else if (a.splits > 1) {
+        const size_t rows = (size_t)a.units * a.splits * a.rows_cap;
+        s.ws_bytes = 2 * align_up(rows * sizeof(float), 256) + align_up(rows * a.D * sizeof(float), 256);
+    }
+    return KYRO_OK;
+}
+
+// Points the launch's partial-state arrays (and the plan's per-sequence table) into `base`,
+// s.ws_bytes of device memory.
+void attention_workspace(AttnSetup& s, char* base) {
+    kyro::AttnArgs& a = s.a;
+    const size_t rows = a.plan ? s.plan_slots * a.hpw * a.plan_rw : (size_t)a.units * a.splits * a.rows_cap;
+    const size_t mb_bytes = align_up(rows * sizeof(float), 256);
+    a.ws_m = reinterpret_cast<float*>(base);
+    a.ws_l = reinterpret_cast<float*>(base + mb_bytes);
+    a.ws_acc = reinterpret_cast<float*>(base + 2 * mb_bytes);
+    if (a.plan) a.plan_seq = reinterpret_cast<int4*>(base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256));
+}
+
+// Everything a verify launch decides from its params alone: validation, chunking, window,
+// tail grid and workspace size. No device call.
+struct SpecSetup {
+    kyro::SpecArgs a{};
+    bool empty = false;  // batch_size 0
+    size_t stats_b = 0, plan_b = 0, csum_b = 0, gath_b = 0, tail_b = 0;
+    size_t ws_bytes = 0;
+};
+
+int spec_setup(const kyro_spec_verify_params* p, SpecSetup& s) {
+    if (!p) return fail(KYRO_EINVAL, "spec_verify: params is null");
+    if (p->batch_size < 0 || p->max_draft < 0 || p->vocab_size <= 0)
+        return fail(KYRO_EINVAL, "spec_verify: need batch_size >= 0, max_draft >= 0, vocab_size > 0");
+    if (p->max_draft > kyro::kMaxDraft)
+        return fail(KYRO_EUNSUPPORTED, "spec_verify: max_draft %d > %d", p->max_draft, kyro::kMaxDraft);
+    if (p->logits_dtype != KYRO_F32)
+        return fail(KYRO_EUNSUPPORTED, "spec_verify: logits_dtype must be KYRO_F32");
+    if (p->window < 0) return fail(KYRO_EINVAL, "spec_verify: window must be >= 0");
+    if (p->batch_size == 0) {
+        s.empty = true;
+        return KYRO_OK;
+    }
+    kyro::SpecArgs& a = s.a;
+    a.B = p->batch_size;
+    a.kmax = p->max_draft;
+    a.V = p->vocab_size;
+    a.chunk = kyro::kSpecChunk;
+    a.C = (a.V + a.chunk - 1) / a.chunk;
+    // Rows of the first win draft positions are read for every sequence; the rest only for
+    // sequences still undecided after them, spread over up to kSpecTailWgs workgroups. Batches
+    // beyond kMaxLazyBatch read every row in the first pass, and so do batches whose rows
+    // all together are few enough that reading them costs less than the tail pass's launch
+    // (rejection-only B 8, k 4, V 32000: 9.2 MB, 20.7 us instead of 27.1 us at W = 3).
+    a.win = p->window > 0 ? std::min(p->window, a.kmax + 1) : std::max(1, kyro::kSpecWindow);
+    const long long all_rows_bytes = (long long)a.B * (2 * a.kmax + 1) * a.V * (long long)sizeof(float);
+    if (p->window == 0 && all_rows_bytes <= kyro::kSpecEagerBytes) a.win = a.kmax + 1;
+    if (a.B > kyro::kMaxLazyBatch) a.win = a.kmax + 1;
+    const long long tail_items = a.kmax >= a.win ? (long long)a.B * (2 * (a.kmax - a.win) + 1) * a.C : 1;
+    // Up to kSpecTailWgs workgroups, more when that would give one workgroup more than 64
+    // items (the tail pass keeps one item's location per lane of a wave).
+    a.tail_wgs = (int)std::min<long long>(
+        INT32_MAX, std::max({1LL, std::min((long long)kyro::kSpecTailWgs, tail_items), (tail_items + 63) / 64}));
+    s.stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
+    s.plan_b = 2 * align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
+    s.csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
+    s.gath_b = align_up((size_t)a.B * (2 * a.kmax + 1) * sizeof(float), 256);
+    s.tail_b = align_up((size_t)a.B * sizeof(int2), 256);
+    s.ws_bytes = s.stats_b + s.plan_b + s.csum_b + s.gath_b + s.tail_b;
+    return KYRO_OK;
+}
+
+// Checks and binds the caller's device pointers.
+int spec_bind(SpecSetup& s, const void* target_logits, const void* draft_logits, const uint32_t* draft_tokens,
+              const int32_t* num_draft, const float* temperature, const float* u_accept, const float* u_resample,
+              int32_t* out_accepted, uint32_t* out_tokens, float* out_p_draft, float* out_q_draft) {
+    kyro::SpecArgs& a = s.a;
+    if (!target_logits || !num_draft || !temperature || !u_resample || !out_accepted || !out_tokens)
+        return fail(KYRO_EINVAL, "spec_verify: null device pointer");
+    if (a.kmax > 0 && (!draft_tokens || !u_accept))
+        return fail(KYRO_EINVAL, "spec_verify: draft_tokens and u_accept are required when max_draft > 0");
+    a.target = static_cast<const float*>(target_logits);
+    a.draft = static_cast<const float*>(draft_logits);
+    a.draft_tokens = draft_tokens;
+    a.num_draft = num_draft;
+    a.temperature = temperature;
+    a.u_accept = u_accept;
+    a.u_res = u_resample;
+    a.out_accepted = out_accepted;
+    a.out_tokens = out_tokens;
+    a.out_p = out_p_draft;
+    a.out_q = out_q_draft;
+    const bool aligned = (reinterpret_cast<uintptr_t>(target_logits) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(draft_logits) % 16 == 0);
+    a.vec4 = (a.V % 4 == 0) && aligned;
+    return KYRO_OK;
+}
+
+// Points the launch's statistics, plans and chunk sums into `base`, s.ws_bytes of device memory.
+void spec_workspace(SpecSetup& s, char* base) {
+    kyro::SpecArgs& a = s.a;
+    a.stats = reinterpret_cast<float2*>(base);
+    a.plan = reinterpret_cast<kyro::SpecPlan*>(base + s.stats_b);
+    a.plan_tail = reinterpret_cast<kyro::SpecPlan*>(base + s.stats_b + s.plan_b / 2);
+    a.csum = reinterpret_cast<float2*>(base + s.stats_b + s.plan_b);
+    a.gath = reinterpret_cast<float*>(base + s.stats_b + s.plan_b + s.csum_b);
+    a.tail = reinterpret_cast<int2*>(base + s.stats_b + s.plan_b + s.csum_b + s.gath_b);
 }
 
 }  // namespace
@@ -152,6 +440,8 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
         if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->sched), kyro::kSchedWords * sizeof(int));
         if (e == hipSuccess) e = hipMemset(ctx->sched, 0, kyro::kSchedWords * sizeof(int));
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device);
+        if (e == hipSuccess && ctx->num_cus <= 0) e = hipErrorInvalidDevice;
         if (e == hipSuccess) e = hipStreamSynchronize(0);  // the memsets are done before any launch
         if (e != hipSuccess) {
             if (ctx->err) (void)hipFree(ctx->err);
@@ -290,64 +580,12 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
                             const int64_t* context_lens, void* out) {
     return guarded([&]() -> int {
         if (int rc = check_ctx(ctx)) return rc;
-        if (!p) return fail(KYRO_EINVAL, "paged_attention: params is null");
-        if (p->block_size <= 0 || p->num_heads <= 0 || p->head_dim <= 0 || p->num_kv_heads <= 0)
-            return fail(KYRO_EINVAL, "paged_attention: block_size/num_heads/head_dim/num_kv_heads must be > 0");
-        if (p->num_heads % p->num_kv_heads != 0)
-            return fail(KYRO_EINVAL, "paged_attention: num_heads %d not a multiple of num_kv_heads %d",
-                        p->num_heads, p->num_kv_heads);
-        if (p->batch_size < 0 || p->total_q < 0 || p->max_blocks_per_seq < 0 || p->num_blocks < 0)
-            return fail(KYRO_EINVAL, "paged_attention: negative shape");
-        if (p->dtype != KYRO_F32 && p->dtype != KYRO_BF16)
-            return fail(KYRO_EINVAL, "paged_attention: dtype %d unknown", p->dtype);
-        if (p->out_dtype != KYRO_F32 && p->out_dtype != KYRO_BF16)
-            return fail(KYRO_EINVAL, "paged_attention: out_dtype %d unknown", p->out_dtype);
-        if (!q_start_loc && p->total_q != p->batch_size)
-            return fail(KYRO_EINVAL, "paged_attention: total_q %d != batch_size %d without q_start_loc",
-                        p->total_q, p->batch_size);
-        if (p->head_dim != 64 && p->head_dim != 128)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: 64, 128)", p->head_dim);
-        if (p->path < KYRO_ATTN_AUTO || p->path > KYRO_ATTN_MFMA)
-            return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
-        if (p->kv_reuse < KYRO_KV_REUSE_AUTO || p->kv_reuse > KYRO_KV_REUSE_STREAM)
-            return fail(KYRO_EINVAL, "paged_attention: kv_reuse %d unknown", p->kv_reuse);
-        if (p->schedule < KYRO_ATTN_SCHEDULE_AUTO || p->schedule > KYRO_ATTN_SCHEDULE_BALANCED)
-            return fail(KYRO_EINVAL, "paged_attention: schedule %d unknown", p->schedule);
-        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->num_splits != 0)
-            return fail(KYRO_EINVAL, "paged_attention: the balanced schedule chooses its own splits (num_splits must be 0)");
-        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && p->batch_size > kyro::kPlanMaxSeqs)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule plans at most %d sequences",
-                        kyro::kPlanMaxSeqs);
-        if (p->batch_size == 0 || p->total_q == 0) return KYRO_OK;
+        AttnSetup s;
+        if (int rc = attention_setup(p, q_start_loc != nullptr, ctx->num_cus, s)) return rc;
+        if (s.empty) return KYRO_OK;
         if (!query || !key_cache || !value_cache || !block_table || !context_lens || !out)
             return fail(KYRO_EINVAL, "paged_attention: null device pointer");
-        if (p->max_blocks_per_seq == 0 || p->num_blocks == 0) {
-            // Only context length 0 is possible; the kernels still write the zero rows.
-        }
-        const int group = p->num_heads / p->num_kv_heads;
-        int max_q_len = p->max_q_len;
-        if (max_q_len <= 0) max_q_len = q_start_loc ? p->total_q : 1;
-        if (!q_start_loc) max_q_len = 1;
-
-        const bool mfma_ok = p->head_dim == 128 && p->block_size == 16;  // bf16 or f32 caches
-        int kernel;
-        if (p->path == KYRO_ATTN_MFMA) {
-            if (!mfma_ok)
-                return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs head_dim 128, block_size 16");
-            kernel = kyro::ATTN_KERNEL_MFMA;
-        } else if (p->path == KYRO_ATTN_VECTOR) {
-            kernel = kyro::ATTN_KERNEL_VECTOR;
-        } else {
-            // MFMA wherever it applies, one query row per kv head included: the kernel is
-            // memory-bound, so padding rows to a 16-row tile costs nothing measurable (MHA decode,
-            // 1 row per kv head: 67 us against the vector kernel's 207 us).
-            kernel = mfma_ok ? kyro::ATTN_KERNEL_MFMA : kyro::ATTN_KERNEL_VECTOR;
-        }
-        if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
-                        "(head_dim 128, block_size 16)");
-
-        kyro::AttnArgs a{};
+        kyro::AttnArgs& a = s.a;
         a.q = query;
         a.q_start = q_start_loc;
         a.k = key_cache;
@@ -355,113 +593,75 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* p, 
         a.table = block_table;
         a.ctx_lens = context_lens;
         a.out = out;
-        a.B = p->batch_size;
-        a.H = p->num_heads;
-        a.Hkv = p->num_kv_heads;
-        a.group = group;
-        a.D = p->head_dim;
-        a.bs = p->block_size;
-        a.max_blocks = p->max_blocks_per_seq;
-        a.num_blocks = p->num_blocks;
-        a.total_q = p->total_q;
-        a.max_q_len = max_q_len;
-        a.rows_cap = group * max_q_len;
-        a.causal = p->causal ? 1 : 0;
-        a.out_bf16 = p->out_dtype == KYRO_BF16;
-        a.dtype_bf16 = p->dtype == KYRO_BF16;
-        const double scale = p->scale > 0 ? (double)p->scale : 1.0 / std::sqrt((double)p->head_dim);
-        a.scale_log2 = (float)(scale * 1.4426950408889634);
-        a.units = p->batch_size * p->num_kv_heads;
-        // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
-        // waves per head): the workgroup then reads both heads' slabs of each block together, and
-        // the Llama-3-8B step fits the chip in one round of workgroups.
-        a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0) ? 2 : 1;
-        a.ugroups = a.units / a.hpw;
-        a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
-        // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
-        // (vector) or 16 / 32 (MFMA) rows that stream the same K/V.
-        const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
-                                                                    : kyro::kVectorRowsPerGroup;
-        a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
-        // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
-        // of a kv head, or (as the caller says) other sequences holding the same blocks.
-        a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
-
-        // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
-        const int mb = std::max(1, p->max_blocks_per_seq);
-        int splits = p->num_splits;
-        if (splits <= 0) {
-            // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
-            // one CU streaming it alone; more splits only when the workgroups cannot cover the
-            // chip's 256 CUs (the MFMA kernel holds one workgroup per CU), down to 16-block chunks.
-            // With four or more workgroups per CU already, splitting only adds per-workgroup
-            // set-up and a combine pass (one workgroup fills a CU, so nothing hides them).
-            constexpr int kTargetChunk = 256, kCUs = 256, kMinChunk = 16;
-            const int per_split = a.ugroups * a.row_groups;
-            splits = per_split >= 4 * kCUs ? 1 : (mb + kTargetChunk - 1) / kTargetChunk;
-            if (per_split * splits < kCUs)
-                splits = std::min((kCUs + per_split - 1) / per_split, std::max(1, mb / kMinChunk));
-        }
-        // Longest split: the LDS block-id staging, and for the MFMA kernel the block pairs a wave
-        // holds ids for (its waves per head x two 64-lane slots).
-        const int max_chunk = kernel == kyro::ATTN_KERNEL_MFMA
-                                  ? std::min(kyro::kMaxChunkBlocks, 2 * kyro::kMfmaMaxPairsPerWave * (4 / a.hpw))
-                                  : kyro::kMaxChunkBlocks;
-        splits = std::min(splits, mb);
-        splits = std::max(splits, (mb + max_chunk - 1) / max_chunk);
-        int chunk = (mb + splits - 1) / splits;
-        chunk = std::min((chunk + 1) / 2 * 2, max_chunk);
-        splits = (mb + chunk - 1) / chunk;
-        a.splits = splits;
-        a.chunk_blocks = chunk;
-        // The balanced schedule: asked for, or where the grid's splits (from the table width
-        // alone) would have to guess at the context lengths: a split grid, or a table wider than
-        // 256 blocks (4096 tokens), where a few long sequences can leave one workgroup streaming
-        // long after the rest of the chip is idle.
-        a.plan = kernel == kyro::ATTN_KERNEL_MFMA && p->num_splits == 0 && p->batch_size <= kyro::kPlanMaxSeqs &&
-                 (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED ||
-                  (p->schedule == KYRO_ATTN_SCHEDULE_AUTO && (splits > 1 || mb > 256)));
-        size_t plan_slots = 0;
-        if (a.plan) {
-            constexpr int kCUs = 256;
-            a.plan_grid = kCUs;
-            a.plan_rw = rows_per_group;
-            a.plan_max_chunk = max_chunk / 2 * 2;
-            a.splits = 1;
-            plan_slots = (size_t)kyro::plan_slot_bound(a.B, a.ugroups / a.B, a.row_groups, mb, a.plan_max_chunk,
-                                                       a.plan_grid);
-        }
-        // One launch carries at most 2^32 - 1 work items along x.
-        if (!a.plan && (uint64_t)a.ugroups_padded * splits * a.row_groups * 256 > 0xffffffffull)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: %d units x %d splits x %d row groups is too large for one launch",
-                        a.units, splits, a.row_groups);
-
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        size_t ws_bytes = 0;
-        if (a.plan) {
-            const size_t rows = plan_slots * a.hpw * a.plan_rw;
-            const size_t mb_bytes = align_up(rows * sizeof(float), 256);
-            ws_bytes = 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256) +
-                       align_up((size_t)a.B * sizeof(int4), 256);
-            if (int rc = ensure_arena(ctx, ws_bytes)) return rc;
-            char* base = static_cast<char*>(ctx->arena);
-            a.ws_m = reinterpret_cast<float*>(base);
-            a.ws_l = reinterpret_cast<float*>(base + mb_bytes);
-            a.ws_acc = reinterpret_cast<float*>(base + 2 * mb_bytes);
-            a.plan_seq = reinterpret_cast<int4*>(base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256));
-            a.sched = ctx->sched;
-        } else if (splits > 1) {
-            const size_t rows = (size_t)a.units * splits * a.rows_cap;
-            ws_bytes = align_up(rows * sizeof(float), 256) * 2 + align_up(rows * a.D * sizeof(float), 256);
-            if (int rc = ensure_arena(ctx, ws_bytes)) return rc;
-            char* base = static_cast<char*>(ctx->arena);
-            a.ws_m = reinterpret_cast<float*>(base);
-            a.ws_l = reinterpret_cast<float*>(base + align_up(rows * sizeof(float), 256));
-            a.ws_acc = reinterpret_cast<float*>(base + 2 * align_up(rows * sizeof(float), 256));
+        if (s.ws_bytes) {
+            if (int rc = ensure_arena(ctx, s.ws_bytes)) return rc;
+            attention_workspace(s, static_cast<char*>(ctx->arena));
         }
+        if (a.plan) a.sched = ctx->sched;
         a.err = ctx->err;
-        KYRO_HIP(kyro::launch_paged_attention(a, kernel, ctx->stream));
+        KYRO_HIP(kyro::launch_paged_attention(a, s.kernel, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_params* p, int has_q_start_loc,
+                                   size_t* bytes) {
+    return guarded([&]() -> int {
+        if (!bytes) return fail(KYRO_EINVAL, "paged_attention_workspace: bytes is null");
+        *bytes = 0;
+        AttnSetup s;
+        if (int rc = attention_setup(p, has_q_start_loc != 0, ctx ? ctx->num_cus : kDefaultCUs, s)) return rc;
+        *bytes = s.ws_bytes;
+        return KYRO_OK;
+    });
+}
+
+int kyro_paged_attention_plan(const kyro_paged_attention_params* p, int num_cus, int chunk_div,
+                              const int64_t* context_lens, const int32_t* q_lens, int32_t* out_splits,
+                              kyro_attention_plan* out) {
+    return guarded([&]() -> int {
+        if (!out) return fail(KYRO_EINVAL, "paged_attention_plan: out is null");
+        *out = kyro_attention_plan{};
+        if (num_cus <= 0) num_cus = kDefaultCUs;
+        if (chunk_div <= 0) chunk_div = kyro::kPlanChunkDiv;
+        AttnSetup s;
+        if (int rc = attention_setup(p, q_lens != nullptr, num_cus, s, chunk_div)) return rc;
+        const kyro::AttnArgs& a = s.a;
+        if (s.empty) return KYRO_OK;
+        if (!context_lens) return fail(KYRO_EINVAL, "paged_attention_plan: context_lens is null");
+        if (!a.plan) return fail(KYRO_EINVAL, "paged_attention_plan: these params run on the grid schedule");
+        // The per-sequence quantities of the device plan (plan_build in paged_attention.hip):
+        // row groups r, blocks nb, work U r nb; the chunk and the splits come from the functions
+        // the device uses.
+        const int U = a.Hkv / a.hpw;
+        std::vector<int> r(a.B), nb(a.B);
+        long long T = 0;
+        int maxnb = 0;
+        for (int b = 0; b < a.B; ++b) {
+            const long long c = context_lens[b];
+            const int ql = q_lens ? q_lens[b] : 1;
+            if (c < 0 || c > (long long)a.max_blocks * a.bs || ql < 0 || ql > a.max_q_len)
+                return fail(KYRO_EINVAL, "paged_attention_plan: sequence %d: context length %lld or rows %d out of range",
+                            b, c, ql);
+            r[b] = (ql * a.group + a.plan_rw - 1) / a.plan_rw;
+            nb[b] = (int)((c + a.bs - 1) / a.bs);
+            T += (long long)U * r[b] * nb[b];
+            if (r[b] > 0) maxnb = std::max(maxnb, nb[b]);
+        }
+        const int C = kyro::plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk, chunk_div);
+        long long items = 0;
+        for (int b = 0; b < a.B; ++b) {
+            int ns, ch;
+            kyro::plan_split(nb[b], C, ns, ch);
+            if (out_splits) out_splits[b] = r[b] > 0 ? ns : 0;
+            if (r[b] > 0) items += (long long)U * ns * r[b];
+        }
+        out->grid = a.plan_grid;
+        out->chunk_blocks = C;
+        out->items = items;
+        out->slot_bound = s.plan_slots;
         return KYRO_OK;
     });
 }
@@ -473,70 +673,29 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
                      float* out_p_draft, float* out_q_draft) {
     return guarded([&]() -> int {
         if (int rc = check_ctx(ctx)) return rc;
-        if (!p) return fail(KYRO_EINVAL, "spec_verify: params is null");
-        if (p->batch_size < 0 || p->max_draft < 0 || p->vocab_size <= 0)
-            return fail(KYRO_EINVAL, "spec_verify: need batch_size >= 0, max_draft >= 0, vocab_size > 0");
-        if (p->max_draft > kyro::kMaxDraft)
-            return fail(KYRO_EUNSUPPORTED, "spec_verify: max_draft %d > %d", p->max_draft, kyro::kMaxDraft);
-        if (p->logits_dtype != KYRO_F32)
-            return fail(KYRO_EUNSUPPORTED, "spec_verify: logits_dtype must be KYRO_F32");
-        if (p->batch_size == 0) return KYRO_OK;
-        if (!target_logits || !num_draft || !temperature || !u_resample || !out_accepted || !out_tokens)
-            return fail(KYRO_EINVAL, "spec_verify: null device pointer");
-        if (p->max_draft > 0 && (!draft_tokens || !u_accept))
-            return fail(KYRO_EINVAL, "spec_verify: draft_tokens and u_accept are required when max_draft > 0");
-        kyro::SpecArgs a{};
-        a.target = static_cast<const float*>(target_logits);
-        a.draft = static_cast<const float*>(draft_logits);
-        a.draft_tokens = draft_tokens;
-        a.num_draft = num_draft;
-        a.temperature = temperature;
-        a.u_accept = u_accept;
-        a.u_res = u_resample;
-        a.out_accepted = out_accepted;
-        a.out_tokens = out_tokens;
-        a.out_p = out_p_draft;
-        a.out_q = out_q_draft;
-        a.B = p->batch_size;
-        a.kmax = p->max_draft;
-        a.V = p->vocab_size;
-        a.chunk = kyro::kSpecChunk;
-        a.C = (a.V + a.chunk - 1) / a.chunk;
-        const bool aligned = (reinterpret_cast<uintptr_t>(target_logits) % 16 == 0) &&
-                             (reinterpret_cast<uintptr_t>(draft_logits) % 16 == 0);
-        a.vec4 = (a.V % 4 == 0) && aligned;
-        // Rows of the first win draft positions are read for every sequence; the rest only for
-        // sequences still undecided after them, spread over up to kSpecTailWgs workgroups. Batches
-        // beyond kMaxLazyBatch read every row in the first pass, and so do batches whose rows
-        // all together are few enough that reading them costs less than the tail pass's launch
-        // (rejection-only B 8, k 4, V 32000: 9.2 MB, 20.7 us instead of 27.1 us at W = 3).
-        if (p->window < 0) return fail(KYRO_EINVAL, "spec_verify: window must be >= 0");
-        a.win = p->window > 0 ? std::min(p->window, a.kmax + 1) : std::max(1, kyro::kSpecWindow);
-        const long long all_rows_bytes = (long long)a.B * (2 * a.kmax + 1) * a.V * (long long)sizeof(float);
-        if (p->window == 0 && all_rows_bytes <= kyro::kSpecEagerBytes) a.win = a.kmax + 1;
-        if (a.B > kyro::kMaxLazyBatch) a.win = a.kmax + 1;
-        const long long tail_items = a.kmax >= a.win ? (long long)a.B * (2 * (a.kmax - a.win) + 1) * a.C : 1;
-        // Up to kSpecTailWgs workgroups, more when that would give one workgroup more than 64
-        // items (the tail pass keeps one item's location per lane of a wave).
-        a.tail_wgs = (int)std::min<long long>(
-            INT32_MAX, std::max({1LL, std::min((long long)kyro::kSpecTailWgs, tail_items), (tail_items + 63) / 64}));
-        const size_t stats_b = align_up((size_t)a.B * (2 * a.kmax + 1) * a.C * sizeof(float2), 256);
-        const size_t plan_b = 2 * align_up((size_t)a.B * sizeof(kyro::SpecPlan), 256);
-        const size_t csum_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
-        const size_t gath_b = align_up((size_t)a.B * (2 * a.kmax + 1) * sizeof(float), 256);
-        const size_t tail_b = align_up((size_t)a.B * sizeof(int2), 256);
+        SpecSetup s;
+        if (int rc = spec_setup(p, s)) return rc;
+        if (s.empty) return KYRO_OK;
+        if (int rc = spec_bind(s, target_logits, draft_logits, draft_tokens, num_draft, temperature, u_accept,
+                               u_resample, out_accepted, out_tokens, out_p_draft, out_q_draft))
+            return rc;
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        if (int rc = ensure_arena(ctx, stats_b + plan_b + csum_b + gath_b + tail_b)) return rc;
-        char* base = static_cast<char*>(ctx->arena);
-        a.stats = reinterpret_cast<float2*>(base);
-        a.plan = reinterpret_cast<kyro::SpecPlan*>(base + stats_b);
-        a.plan_tail = reinterpret_cast<kyro::SpecPlan*>(base + stats_b + plan_b / 2);
-        a.csum = reinterpret_cast<float2*>(base + stats_b + plan_b);
-        a.gath = reinterpret_cast<float*>(base + stats_b + plan_b + csum_b);
-        a.tail = reinterpret_cast<int2*>(base + stats_b + plan_b + csum_b + gath_b);
-        a.err = ctx->err;
-        KYRO_HIP(kyro::launch_spec_verify(a, ctx->stream));
+        if (int rc = ensure_arena(ctx, s.ws_bytes)) return rc;
+        spec_workspace(s, static_cast<char*>(ctx->arena));
+        s.a.err = ctx->err;
+        KYRO_HIP(kyro::launch_spec_verify(s.a, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_spec_verify_workspace(const kyro_spec_verify_params* p, size_t* bytes) {
+    return guarded([&]() -> int {
+        if (!bytes) return fail(KYRO_EINVAL, "spec_verify_workspace: bytes is null");
+        *bytes = 0;
+        SpecSetup s;
+        if (int rc = spec_setup(p, s)) return rc;
+        *bytes = s.ws_bytes;
         return KYRO_OK;
     });
 }

@@ -56,7 +56,7 @@ def struct_fields(name):
 @pytest.mark.parametrize("cname, pyname", [
     ("kyro_paged_attention_params", "PagedAttentionParams"), ("kyro_spec_verify_params", "SpecVerifyParams"),
     ("kyro_kv_append_params", "KvAppendParams"), ("kyro_copy_blocks_params", "CopyBlocksParams"),
-    ("kyro_sample_params", "SampleParams")])
+    ("kyro_sample_params", "SampleParams"), ("kyro_attention_plan", "AttentionPlan")])
 def test_ctypes_structs_mirror_the_headers(cname, pyname):
     assert [f[0] for f in getattr(_lib, pyname)._fields_] == struct_fields(cname)
 

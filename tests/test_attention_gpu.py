@@ -1,9 +1,11 @@
 """Paged attention on the GPU against the oracle, through the C ABI (kyro_paged_attention_mq).
 
 Mirrors the reference's own tests (src/model/attention_kernel.rs:154-227) and then checks values:
-small cases against the oracle on every sequence, full-size workloads on a subset of sequences,
-and size-independent properties (split count, kernel choice, block permutation) at full size.
+small cases and full-size workloads against the oracle on every sequence, and size-independent
+properties (block permutation) at full size.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -303,6 +305,72 @@ def test_balanced_schedule_replays_from_a_graph(gpu):
             again = attn.forward(*args2, q_start_loc=t2["q_start_loc"], schedule="balanced")
         torch.cuda.synchronize()
         assert torch.equal(again, eager2)
+
+
+def test_balanced_schedule_slot_overflow_latches_an_error(gpu, monkeypatch):
+    """With fewer partial-state slots sized than the plan needs (forced from the host through
+    KYRO_TEST_PLAN_SLOT_CAP), the device plan latches an error and runs no item instead of
+    writing past the workspace; the next call, sized normally, gives the oracle's result."""
+    case = wl.make_attention_case(context_lens=[5000, 40, 3000, 700], q_lens=[8, 3, 5, 1], num_heads=32,
+                                  num_kv_heads=8, dtype="bf16", seed=31)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 32, 128, 8)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    monkeypatch.setenv("KYRO_TEST_PLAN_SLOT_CAP", "3")
+    with pytest.raises(kyro_amd.KyroError, match="partial-state slots"):
+        attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
+    monkeypatch.delenv("KYRO_TEST_PLAN_SLOT_CAP")
+    out = attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
+    h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16)
+
+
+def test_arena_growth_is_refused_during_graph_capture(gpu):
+    """A call whose scratch exceeds the context's arena while the stream captures a graph fails
+    with a message naming the bytes to reserve (growing would free memory that captured kernels
+    address); after kyro_ctx_reserve with the size query's answer the same capture succeeds and
+    replays to the eager result."""
+    from kyro_amd import _lib
+
+    case = wl.make_attention_case(context_lens=[3000, 17, 900, 5000], q_lens=[8, 8, 1, 5], num_heads=32,
+                                  num_kv_heads=8, dtype="bf16", seed=25)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, 32, 128, 8)
+    args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
+    ctx = _lib.Context(gpu.index or 0)
+    s = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(s):
+        # binds the fresh context to s; a one-split call uses no arena
+        tiny = attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="grid", num_splits=1, context=ctx)
+        out = torch.zeros_like(tiny)
+    ctx.sync()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(kyro_amd.KyroError, match="kyro_ctx_reserve"):
+        with torch.cuda.graph(g, stream=s):
+            attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", out=out, max_q_len=8,
+                               context=ctx)
+    params = _lib.PagedAttentionParams(16, 32, 128, 8, 4, int(case.q_start_loc[-1]), case.block_table.shape[1],
+                                       case.key_cache.shape[0], _lib.KYRO_BF16, _lib.KYRO_F32, 1, 0.0, 0, 0, 8, 0,
+                                       _lib.KYRO_ATTN_SCHEDULE_BALANCED)
+    need = ctypes.c_size_t()
+    _lib.check(_lib.lib().kyro_paged_attention_workspace(ctx.handle, ctypes.byref(params), 1, ctypes.byref(need)))
+    assert need.value > 0
+    ctx.reserve(need.value)
+    with torch.cuda.stream(s):
+        eager = attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", max_q_len=8,
+                                   context=ctx)
+    ctx.sync()
+    h.assert_attention_close(eager, case, h.oracle_attention(case), h.ATOL_BF16)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", out=out, max_q_len=8,
+                           context=ctx)
+    for _ in range(2):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    del g
+    ctx.close()
 
 
 def test_balanced_schedule_errors(gpu):

@@ -1,0 +1,106 @@
+"""The balanced attention schedule's plan on the host (no GPU): the library's own chunk and split
+arithmetic (kyro_paged_attention_plan runs the functions the device plan runs) never needs more
+partial-state slots than a launch sizes, over seeded random batches.
+
+A launch sizes its workspace from the params alone (plan_slot_bound), before the context lengths
+are known; the device plan then latches KYRO_EINVAL instead of running a plan with more items.
+An experimental chunk divisor of 3 once ran against a bound derived for 2 and wrote past the
+workspace: test_a_bound_for_another_divisor_is_exceeded shows this check catches that mismatch.
+"""
+import numpy as np
+import pytest
+
+from kyro_amd import workloads as wl
+from kyro_amd.attention import PagedAttention, attention_plan
+
+
+def _ceil(a, b):
+    return -(-a // b)
+
+
+def _rows_per_group(rows_cap):
+    return 16 if rows_cap <= 16 else 32
+
+
+def _random_batch(g):
+    """Context lengths from one of four shapes (uniform short, uniform long, log-uniform over
+    128..32768, mostly short with a few very long), ragged row counts 0..9, and a head shape."""
+    B = int(g.choice([1, 2, 7, 31, 64, 128, 256, 300, 1024]))
+    kind = int(g.integers(0, 4))
+    if kind == 0:
+        ctx = g.integers(0, 600, size=B)
+    elif kind == 1:
+        ctx = g.integers(256, 8193, size=B)
+    elif kind == 2:
+        ctx = np.round(np.exp(np.log(128) + g.random(B) * (np.log(32768) - np.log(128)))).astype(np.int64)
+    else:
+        ctx = g.integers(1, 400, size=B)
+        ctx[g.random(B) < 0.05] = int(g.integers(8000, 32769))
+    ql = g.integers(0, 10, size=B) if g.random() < 0.7 else np.full(B, int(g.integers(1, 10)))
+    hkv = int(g.choice([1, 2, 4, 8, 16]))
+    group = int(g.choice([1, 2, 4, 8]))
+    return ctx.astype(np.int64), ql.astype(np.int32), hkv, group
+
+
+@pytest.mark.parametrize("chunk_div", [2, 3, 4])
+@pytest.mark.parametrize("num_cus", [256, 80, 32])
+def test_slot_bound_holds_over_random_batches(chunk_div, num_cus):
+    g = np.random.default_rng(1000 * chunk_div + num_cus)
+    worst = 0.0
+    for _ in range(400):
+        ctx, ql, hkv, group = _random_batch(g)
+        attn = PagedAttention(16, hkv * group, 128, hkv)
+        mb = max(1, int(_ceil(ctx.max(), 16)) + int(g.integers(0, 3)))
+        info, splits = attention_plan(attn, ctx, ql, max_blocks_per_seq=mb, num_cus=num_cus, chunk_div=chunk_div)
+        if ql.sum() == 0:  # no query rows: nothing is launched
+            assert info["items"] == 0 and info["grid"] == 0
+            continue
+        assert info["grid"] == max(8, num_cus // 8 * 8)
+        assert info["items"] <= info["slot_bound"], (info, ctx.tolist(), ql.tolist(), hkv, group)
+        worst = max(worst, info["items"] / info["slot_bound"])
+        # Items are sequence x kv head group x split x row group, with the row groups of the
+        # launch's row-group size (16 or 32 rows per group for the MFMA kernel).
+        hp = 2 if hkv % 2 == 0 else 1
+        rw = _rows_per_group(group * max(1, int(ql.max())))
+        r = _ceil(ql.astype(np.int64) * group, rw)
+        assert info["items"] == int(np.sum((hkv // hp) * splits.astype(np.int64) * r))
+        # Splits: one for a sequence within the chunk; otherwise even chunks that cover the
+        # sequence with no empty split; none for a sequence without rows.
+        nb = _ceil(ctx, 16)
+        C = info["chunk_blocks"]
+        assert C % 2 == 0 and C >= 16
+        for b in range(len(ctx)):
+            if r[b] == 0:
+                assert splits[b] == 0
+            elif nb[b] <= C:
+                assert splits[b] == 1
+            else:
+                ch = _ceil(nb[b], splits[b])
+                assert splits[b] >= _ceil(nb[b], C) and (splits[b] - 1) * ch < nb[b] <= splits[b] * (ch + 1)
+    assert worst > 0.0
+
+
+def test_a_uniform_batch_keeps_one_item_per_kv_head_group():
+    """Llama-3-8B verify shape (64 x 4096 tokens, GQA 32/8, 8 rows): nothing splits."""
+    info, splits = attention_plan(PagedAttention(16, 32, 128, 8), [4096] * 64, [8] * 64, max_blocks_per_seq=256)
+    assert (splits == 1).all() and info["items"] == 64 * 4
+
+
+def test_a_bound_for_another_divisor_is_exceeded():
+    """The Llama-2-7B batch (MHA 32/32, B 16, ctx 512-2048, 5 rows) planned with chunks of L/3
+    needs more slots than a bound derived for L/2 allows: the check above has the power to catch
+    the mismatch that once wrote past the workspace, and the shared divisor keeps them consistent."""
+    ctx = wl.rng(0, wl.S_CTX).integers(512, 2049, size=16)
+    attn = PagedAttention(16, 32, 128, 32)
+    three, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_div=3)
+    two, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_div=2)
+    assert two["items"] <= two["slot_bound"]
+    assert three["items"] <= three["slot_bound"]
+    assert three["items"] > two["slot_bound"]
+
+
+def test_grid_schedule_params_are_refused():
+    from kyro_amd._lib import KyroError
+
+    with pytest.raises(KyroError, match="grid schedule"):
+        attention_plan(PagedAttention(16, 8, 128, 2), [100, 200], None, max_blocks_per_seq=16, schedule="grid")
