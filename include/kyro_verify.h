@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define KYRO_ABI_VERSION 8
+#define KYRO_ABI_VERSION 9
 
 typedef enum kyro_status {
     KYRO_OK = 0,
@@ -272,6 +272,31 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* params,
 /* Scratch bytes a kyro_spec_verify call with these params takes from the context's arena. Host
  * only, no device work. */
 int kyro_spec_verify_workspace(const kyro_spec_verify_params* params, size_t* bytes);
+
+/* Maximum scratch of kyro_spec_verify_noalloc, in bytes (16 MiB). */
+#define KYRO_SPEC_VERIFY_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/*
+ * kyro_spec_verify with no allocation: the same kernels, arguments and results, with the scratch
+ * (chunk statistics, per-sequence plans, chunk sums) in a fixed array of this library on each
+ * device instead of the context's arena. It calls no hipMalloc / hipFree and no allocating
+ * routine, so it can run where allocation is not allowed: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid it. No counterpart in the reference; this is for callers
+ * that cannot allocate.
+ * Limit: a call whose scratch (kyro_spec_verify_workspace) exceeds
+ * KYRO_SPEC_VERIFY_NOALLOC_SCRATCH_BYTES fails with KYRO_EINVAL (about B x (2 kmax + 1) x
+ * ceil(V / 4096) x 8 bytes: B 64, kmax 7, V 128256 needs 270 KB; B 1024, kmax 8, V 256000 needs
+ * 9 MB). The array is set up at kyro_ctx_create and held until the process ends. Every call on a
+ * device shares that device's array: calls that overlap on one device (two contexts, or two
+ * streams) race and must be ordered by the caller. The kernels write every scratch entry they
+ * read within a call, so the last call's contents never reach the next one.
+ */
+int kyro_spec_verify_noalloc(kyro_ctx ctx, const kyro_spec_verify_params* params,
+                             const void* target_logits, const void* draft_logits,
+                             const uint32_t* draft_tokens, const int32_t* num_draft,
+                             const float* temperature, const float* u_accept, const float* u_resample,
+                             int32_t* out_accepted, uint32_t* out_tokens,
+                             float* out_p_draft, float* out_q_draft);
 
 /* ---------------------------------------------------------------- paged KV write */
 

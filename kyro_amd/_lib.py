@@ -18,6 +18,8 @@ KYRO_ATTN_AUTO, KYRO_ATTN_VECTOR, KYRO_ATTN_MFMA = 0, 1, 2
 KYRO_KV_REUSE_AUTO, KYRO_KV_REUSE_SHARED, KYRO_KV_REUSE_STREAM = 0, 1, 2
 KYRO_ATTN_SCHEDULE_AUTO, KYRO_ATTN_SCHEDULE_GRID, KYRO_ATTN_SCHEDULE_BALANCED = 0, 1, 2
 
+SPEC_VERIFY_NOALLOC_SCRATCH_BYTES = 16 << 20  # KYRO_SPEC_VERIFY_NOALLOC_SCRATCH_BYTES
+
 _STATUS_NAMES = {0: "KYRO_OK", 1: "KYRO_EINVAL", 2: "KYRO_EOOM", 3: "KYRO_EHIP", 4: "KYRO_EUNSUPPORTED",
                  5: "KYRO_ENOSPACE"}
 
@@ -71,7 +73,7 @@ class SampleParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("batch_size", "vocab_size", "logits_dtype", "num_masks")]
 
 
-ABI_VERSION = 8  # KYRO_ABI_VERSION of include/kyro_verify.h
+ABI_VERSION = 9  # KYRO_ABI_VERSION of include/kyro_verify.h
 
 _lib = None
 _lib_lock = threading.Lock()
@@ -98,6 +100,7 @@ _SIGNATURES = {
     "kyro_paged_attention_plan": ([ctypes.POINTER(PagedAttentionParams), ctypes.c_int, ctypes.c_int, _P, _P, _P,
                                    ctypes.POINTER(AttentionPlan)], ctypes.c_int),
     "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
+    "kyro_spec_verify_noalloc": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
     "kyro_spec_verify_workspace": ([ctypes.POINTER(SpecVerifyParams), ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "kyro_paged_kv_append": ([_P, ctypes.POINTER(KvAppendParams)] + [_P] * 7, ctypes.c_int),
     # include/kyro_blocks.h

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkyro_verify.so")
 SOURCES = ["runtime.cpp", "upload.hip", "blocks_abi.cpp", "block_manager.cpp", "sample_abi.cpp", "ngram_abi.cpp",
-           "paged_attention.hip", "spec_verify.hip", "kv_append.hip", "sample.hip", "ngram.hip"]
+           "paged_attention.hip", "spec_verify.hip", "kv_append.hip", "sample.hip", "ngram.hip", "noalloc.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

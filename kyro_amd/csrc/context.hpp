@@ -18,6 +18,8 @@ struct kyro_ctx_s {
     hipStream_t stream = nullptr;
     void* arena = nullptr;  // per-call scratch, stream-ordered
     size_t arena_bytes = 0;
+    void* noalloc_scratch = nullptr;  // device address of the allocation-free entry point's
+                                      // static scratch array on this device
     int* err = nullptr;     // device error word
     int* sched = nullptr;   // kyro::kSchedWords device counters of the balanced attention schedule
                             // (zero between launches: the last workgroup of a launch resets them)

@@ -168,6 +168,11 @@ struct SpecArgs {
 
 hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream);
 
+// Scratch of the allocation-free verify entry point: a static device array per device.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+// The array's device address on `device`, which must be current; resolved once per device.
+hipError_t noalloc_scratch(int device, void** out);
+
 struct KvAppendArgs {
     const void* key;         // [total_q, Hkv, D] src dtype
     const void* value;

@@ -442,6 +442,8 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         if (e == hipSuccess) e = hipMemset(ctx->sched, 0, kyro::kSchedWords * sizeof(int));
         if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device);
         if (e == hipSuccess && ctx->num_cus <= 0) e = hipErrorInvalidDevice;
+        // Set-up of kyro_spec_verify_noalloc: the static scratch array's address on this device.
+        if (e == hipSuccess) e = kyro::noalloc_scratch(device, &ctx->noalloc_scratch);
         if (e == hipSuccess) e = hipStreamSynchronize(0);  // the memsets are done before any launch
         if (e != hipSuccess) {
             if (ctx->err) (void)hipFree(ctx->err);
@@ -683,6 +685,34 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* p, const void*
         KYRO_HIP(dg.status);
         if (int rc = ensure_arena(ctx, s.ws_bytes)) return rc;
         spec_workspace(s, static_cast<char*>(ctx->arena));
+        s.a.err = ctx->err;
+        KYRO_HIP(kyro::launch_spec_verify(s.a, ctx->stream));
+        return KYRO_OK;
+    });
+}
+
+int kyro_spec_verify_noalloc(kyro_ctx ctx, const kyro_spec_verify_params* p, const void* target_logits,
+                             const void* draft_logits, const uint32_t* draft_tokens,
+                             const int32_t* num_draft, const float* temperature, const float* u_accept,
+                             const float* u_resample, int32_t* out_accepted, uint32_t* out_tokens,
+                             float* out_p_draft, float* out_q_draft) {
+    return guarded([&]() -> int {
+        if (int rc = check_ctx(ctx)) return rc;
+        SpecSetup s;
+        if (int rc = spec_setup(p, s)) return rc;
+        if (s.empty) return KYRO_OK;
+        if (s.ws_bytes > kyro::kNoAllocScratchBytes)
+            return fail(KYRO_EINVAL, "spec_verify_noalloc: the call needs %zu bytes of scratch; the allocation-free "
+                        "variant holds %zu (use kyro_spec_verify)", s.ws_bytes, kyro::kNoAllocScratchBytes);
+        if (!ctx->noalloc_scratch) return fail(KYRO_EHIP, "spec_verify_noalloc: scratch array not set up");
+        if (int rc = spec_bind(s, target_logits, draft_logits, draft_tokens, num_draft, temperature, u_accept,
+                               u_resample, out_accepted, out_tokens, out_p_draft, out_q_draft))
+            return rc;
+        DeviceGuard dg(ctx->device);
+        KYRO_HIP(dg.status);
+        // The same kernels as kyro_spec_verify, with the scratch in the static array: they write
+        // every scratch entry they read within the call, so nothing needs clearing.
+        spec_workspace(s, static_cast<char*>(ctx->noalloc_scratch));
         s.a.err = ctx->err;
         KYRO_HIP(kyro::launch_spec_verify(s.a, ctx->stream));
         return KYRO_OK;

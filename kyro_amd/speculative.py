@@ -44,10 +44,14 @@ def _dev_tensor(t, name, dtype, shape, device):
 
 
 def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, temperature,
-                        u_accept, u_resample, *, return_probs=False, out=None, window=0):
+                        u_accept, u_resample, *, return_probs=False, out=None, window=0,
+                        allocation_free=False):
     """Queues the verify kernels on torch's current stream; see :func:`verify_drafts`.
     ``window``: draft positions whose logit rows are read before the first acceptance scan
-    (0 = the library default); a tuning knob only, outputs do not depend on it."""
+    (0 = the library default); a tuning knob only, outputs do not depend on it.
+    ``allocation_free``: call kyro_spec_verify_noalloc (scratch in the library's fixed per-device
+    array, no allocation in the call; pass ``out`` and ``return_probs=False`` for a call that
+    allocates nothing on the Python side either)."""
     dev = target_logits.device
     if dev.type != "cuda":
         raise ValueError("verify_drafts runs on a GPU device; got " + str(dev))
@@ -76,7 +80,8 @@ def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, te
     ctx = _lib.context(dev.index or 0)
     ctx.set_stream(torch.cuda.current_stream(dev).cuda_stream)
     ptr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
-    _lib.check(_lib.lib().kyro_spec_verify(
+    entry = _lib.lib().kyro_spec_verify_noalloc if allocation_free else _lib.lib().kyro_spec_verify
+    _lib.check(entry(
         ctx.handle, ctypes.byref(params), ptr(target_logits), ptr(draft_logits), ptr(draft_tokens),
         ptr(num_draft), ptr(temperature), ptr(u_accept), ptr(u_resample), ptr(accepted),
         ptr(tokens), ptr(p), ptr(q)))
@@ -84,7 +89,7 @@ def verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, te
 
 
 def verify_drafts(target_logits, draft_logits, draft_tokens, num_draft, temperature, u_accept,
-                  u_resample, *, return_probs=False, window=0):
+                  u_resample, *, return_probs=False, window=0, allocation_free=False):
     """Verifies a batch of drafts (src/speculative.rs:286-339, rejection rule per Leviathan et
     al. 2023) and synchronises.
 
@@ -94,6 +99,7 @@ def verify_drafts(target_logits, draft_logits, draft_tokens, num_draft, temperat
     Returns VerifyResult; ``emitted()`` gives verify_drafts' token lists.
     """
     res = verify_drafts_async(target_logits, draft_logits, draft_tokens, num_draft, temperature,
-                              u_accept, u_resample, return_probs=return_probs, window=window)
+                              u_accept, u_resample, return_probs=return_probs, window=window,
+                              allocation_free=allocation_free)
     _lib.context(target_logits.device.index or 0).sync()
     return res
