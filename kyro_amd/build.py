@@ -1,8 +1,10 @@
-"""Builds libkyro_verify.so in-tree with hipcc for gfx950.
+"""Builds libkyro_verify.so and libkyro_verify.a in-tree with hipcc for gfx950.
 
 Run as ``python -m kyro_amd.build``. Objects go to ``kyro_amd/_build`` and compile in parallel;
-the shared library lands next to this file so the Python binding (and a GPU box that receives
-this tree) finds it without installation.
+both libraries land next to this file so the Python binding (and a GPU box that receives this
+tree) finds them without installation. The static archive is what a Rust ``build.rs`` links
+(``rustc-link-lib=static=kyro_verify``): each object carries its gfx950 code object and registers
+it at program start, so a consumer links it with its own toolchain plus ``-lamdhip64 -lstdc++``.
 """
 from __future__ import annotations
 
@@ -16,6 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkyro_verify.so")
+STATIC_LIB = os.path.join(HERE, "libkyro_verify.a")
 SOURCES = ["runtime.cpp", "upload.hip", "blocks_abi.cpp", "block_manager.cpp", "sample_abi.cpp", "ngram_abi.cpp",
            "paged_attention.hip", "spec_verify.hip", "kv_append.hip", "sample.hip", "ngram.hip", "noalloc.hip"]
 ARCH = "gfx950"
@@ -55,8 +58,16 @@ def build(verbose: bool = False, defines=(), out: str = LIB) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, out)
+    archive = os.path.splitext(out)[0] + ".a"
+    tmp_a = archive + ".tmp"
+    if os.path.exists(tmp_a):
+        os.remove(tmp_a)
+    res = subprocess.run(["ar", "rcs", tmp_a, *objs], capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"ar failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp_a, archive)
     if verbose:
-        print(f"built {out}")
+        print(f"built {out} and {archive}")
     return out
 
 
