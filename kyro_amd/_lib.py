@@ -10,7 +10,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkyro_verify.so")
+# KYRO_VERIFY_LIB names another build of the same library (the tests' host sanitizer run).
+LIB_PATH = os.environ.get("KYRO_VERIFY_LIB") or os.path.join(_HERE, "libkyro_verify.so")
 
 KYRO_OK, KYRO_EINVAL, KYRO_EOOM, KYRO_EHIP, KYRO_EUNSUPPORTED, KYRO_ENOSPACE = 0, 1, 2, 3, 4, 5
 KYRO_F32, KYRO_BF16 = 0, 1

@@ -17,8 +17,10 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SRC = os.path.join(_HERE, "kyro_oracle.c")
-LIB_F64 = os.path.join(_HERE, "libkyro_oracle.so")
-LIB_F32 = os.path.join(_HERE, "libkyro_oracle_f32.so")
+# KYRO_ORACLE_LIB / KYRO_ORACLE_F32_LIB name other builds of the same source (the tests' sanitizer
+# run loads an AddressSanitizer/UBSan build this way).
+LIB_F64 = os.environ.get("KYRO_ORACLE_LIB") or os.path.join(_HERE, "libkyro_oracle.so")
+LIB_F32 = os.environ.get("KYRO_ORACLE_F32_LIB") or os.path.join(_HERE, "libkyro_oracle_f32.so")
 
 
 def build(force: bool = True) -> None:
