@@ -4,16 +4,18 @@
 Workload: the Llama-3-8B verify step — batch 64, k = 7 drafts (8 query rows per sequence), every
 context 4096 tokens, GQA 32 query / 8 kv heads, head_dim 128, bf16 KV in 16-token blocks through
 a shuffled block table, then acceptance over a 128256-entry vocabulary at temperature 0.8 with
-target logits ~ N(0, 3) and draft logits = target + N(0, 1). Synthetic data from the
-Philox-4x32-10 streams of seed 0 (kyro_amd.workloads), resident in HBM before timing starts.
+target logits ~ N(0, 3) and draft logits = target + N(0, 1). Synthetic data of seed 0
+(kyro_amd.workloads: numpy Philox4x64-10 bit generators keyed (seed, stream), numpy's ziggurat
+normals), resident in HBM before timing starts.
 
 One step = kyro_paged_attention_mq + kyro_spec_verify on the same stream. W warm-up steps, then
-K timed steps between two synchronisations. ``value`` is verified tokens per second,
-sum_b (accepted_b + 1) / seconds per step. The same K steps are then run again with HIP events
-on the launch stream around each part; those time the attention kernel for the roofline entry
-and the per-part figures (event records cost the stream time of their own, so they stay out of
-the steps ``value`` is computed from). The CPU oracle (f32 build) is timed on a bounded sample of
-the same workload for the cpu_baseline entry.
+K timed steps. ``value`` is verified tokens per second, sum_b (accepted_b + 1) / seconds per step,
+where a step's time is the mean over K steps each timed by HIP events on the launch stream after a
+512 MiB read that evicts the L2s and the MALL (cold caches, as between two layers' worth of other
+work). ``value_warm`` times K steps back to back between two synchronisations. A third pass of K
+warm steps records HIP events around each part; those time the attention kernel for the roofline
+entry and the per-part figures. The CPU oracle (f32 build) is timed on a bounded sample of the
+same workload for the cpu_baseline entry.
 """
 from __future__ import annotations
 
@@ -35,8 +37,8 @@ B, HQ, HKV, D, BS, CTX, K_DRAFT, VOCAB, TEMP = 64, 32, 8, 128, 16, 4096, 7, 1282
 
 
 def make_inputs(dev, seed=0):
-    """The Llama-3-8B verify-step inputs of kyro_amd.workloads: counter-based Philox-4x32-10
-    streams of `seed` (one stream per tensor), normals by Box-Muller, bf16 by round-to-nearest-
+    """The Llama-3-8B verify-step inputs of kyro_amd.workloads: a numpy Philox4x64-10 generator
+    per (seed, stream) (one stream per tensor), numpy's ziggurat normals, bf16 by round-to-nearest-
     even, draft tokens drawn from softmax(draft / T) by inverse CDF. Built on the host (a few
     seconds) and uploaded before any timing."""
     import numpy as np
@@ -471,8 +473,6 @@ def main():
     ap.add_argument("--window", type=int, default=0,
                     help="draft positions read before the first acceptance scan (0 = library default)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU-baseline sample")
-    ap.add_argument("--cold-steps", type=int, default=20,
-                    help="extra steps timed one by one after a 512 MiB cache-flushing write (0 = skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
@@ -548,34 +548,6 @@ def main():
     kyro_amd.sync(0)
     torch.cuda.synchronize()
 
-    # `value`: K steps back to back, nothing else on the stream.
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    kyro_amd.sync(0)
-    sec_per_step = (t1 - t0) / args.steps
-
-    # Per-part times and the attention launch duration behind `roofline`: the same K steps again,
-    # with HIP events recorded on the launch stream before the attention kernel, between it and the
-    # sampler, and after the sampler. Each record costs the stream a few microseconds (about 10 us
-    # per step for the three), so these steps are timed apart from the ones `value` comes from.
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t2 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
-    torch.cuda.synchronize()
-    t3 = time.perf_counter()
-    kyro_amd.sync(0)
-    instrumented_sec_per_step = (t3 - t2) / args.steps
-
-    # Cold-cache timing: a 512 MiB read between steps evicts the L2s and the 256 MiB MALL; the
-    # events bracket the step only (the back-to-back loop above is what `value` reports). A
-    # flushing write would leave the caches full of dirty lines whose write-back then lands
-    # inside the next step's first kernel.
     def spread(vals):
         return {"median": float(np.median(vals)), "p10": float(np.percentile(vals, 10)),
                 "p90": float(np.percentile(vals, 90))}
@@ -585,19 +557,47 @@ def main():
                 "attention_us": spread([e[0].elapsed_time(e[1]) * 1e3 for e in evs]),
                 "sampler_us": spread([e[1].elapsed_time(e[2]) * 1e3 for e in evs])}
 
-    cold = None
-    if args.cold_steps > 0:
-        scratch = torch.ones(128 << 20, dtype=torch.float32, device=dev)
-        for _ in range(2):
-            scratch.sum()
-        cold_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.cold_steps)]
-        for ev in cold_events:
-            scratch.sum()
-            step(ev)
-        torch.cuda.synchronize()
-        kyro_amd.sync(0)
-        del scratch
-        cold = dict(steps=args.cold_steps, **summary(cold_events))
+    # `value`: K cold steps. Before each, a 512 MiB read evicts the L2s and the 256 MiB MALL, as a
+    # model's other layers would between two verify steps; HIP events on the launch stream bracket
+    # the step alone. (A flushing write would leave dirty lines whose write-back lands in the step.)
+    scratch = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+    for _ in range(2):
+        scratch.sum()
+    cold_events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for ev in cold_events:
+        scratch.sum()
+        step(ev)
+    torch.cuda.synchronize()
+    kyro_amd.sync(0)
+    del scratch
+    cold_steps_ms = [e[0].elapsed_time(e[2]) for e in cold_events]
+    sec_per_step = float(np.mean(cold_steps_ms)) * 1e-3
+
+    # Warm rate: the same K steps back to back with nothing else on the stream (logit rows partly
+    # served from the MALL, which the benchmark loop re-reads every step).
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kyro_amd.sync(0)
+    warm_sec_per_step = (t1 - t0) / args.steps
+
+    # Per-part times and the attention launch duration behind `roofline`: K more warm steps with
+    # HIP events on the launch stream before the attention kernel, between it and the sampler, and
+    # after the sampler (each record costs the stream a few microseconds).
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    kyro_amd.sync(0)
+    instrumented_sec_per_step = (t3 - t2) / args.steps
+    cold = dict(steps=args.steps, **summary(cold_events))
     attn_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     samp_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
     emitted = int((acc.cpu() + 1).sum().item())
@@ -605,7 +605,8 @@ def main():
     achieved = a_bytes / (attn_ms * 1e-3) / 1e9
     step_gbs = (a_bytes + s_bytes) / sec_per_step / 1e9
     # The step's bytes as a sampler that reads every logit row would move them (KV, Q, out, all
-    # target and draft rows): 1,574,633,472 B on this workload.
+    # target and draft rows): 1,574,633,472 B on this workload. The step never reads the rows
+    # after a sequence's first rejected draft, so this over-counts what it needs.
     all_rows_gbs = (a_bytes + sampler_bytes()) / sec_per_step / 1e9
 
     traffic = None
@@ -625,18 +626,23 @@ def main():
     line = {
         "metric": METRIC,
         "value": emitted / sec_per_step,
+        "value_warm": emitted / warm_sec_per_step,
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": sec_per_step * 1e3,
+        "ms_per_step_warm": warm_sec_per_step * 1e3,
+        "timing": "value and ms_per_step: mean of K steps each timed by HIP events after a 512 MiB "
+                  "cache-evicting read; value_warm: K steps back to back between two synchronisations",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic, Philox-4x32-10 streams of seed 0 (kyro_amd.workloads): KV, Q ~ N(0,1) bf16; "
-                "target logits ~ N(0,3); draft = target + N(0,1); draft tokens ~ softmax(draft/T) by inverse "
-                "CDF; tables: one shuffled pool of 16384 blocks",
+        "data": "synthetic, seed 0 (kyro_amd.workloads): numpy Philox4x64-10 bit generators keyed "
+                "(seed, stream), numpy ziggurat normals; KV, Q ~ N(0,1) bf16; target logits ~ N(0,3); "
+                "draft = target + N(0,1); draft tokens ~ softmax(draft/T) by inverse CDF; tables: one "
+                "shuffled pool of 16384 blocks",
         "config": {
             "workload": "Llama-3-8B verify step: paged attention (1 layer) + acceptance sampling",
             "batch": B, "draft_k": K_DRAFT, "context": CTX, "q_heads": HQ, "kv_heads": HKV,
@@ -660,6 +666,9 @@ def main():
             "algorithmic_bytes": a_bytes + s_bytes,
             "GB_s": step_gbs,
             "frac_of_peak": step_gbs / PEAK_HBM_GBS,
+            "bytes_note": "algorithmic_bytes / GB_s / frac_of_peak count the logit rows the acceptance scan "
+                          "evaluates (each once); all_rows_* count every logit row, including the rows after "
+                          "each sequence's first rejection that the step never reads",
             "all_rows_bytes": a_bytes + sampler_bytes(),
             "all_rows_GB_s": all_rows_gbs,
             "all_rows_frac_of_peak": all_rows_gbs / PEAK_HBM_GBS,
@@ -672,7 +681,7 @@ def main():
             "tokens_per_step": emitted,
             "mean_accepted": emitted / B - 1,
             "accepted_histogram": torch.bincount(acc.cpu().long(), minlength=K_DRAFT + 1).tolist(),
-            "back_to_back": summary(events),
+            "warm_instrumented": summary(events),
             "cold_cache": cold,
         },
     }
