@@ -36,6 +36,17 @@ namespace {
 
 constexpr int kT = 256;
 constexpr int kPer = kSpecChunk / kT;  // logits per thread in a chunk
+// Cache policy of the window and tail passes' logit loads (kLoadCached or kLoadStream). The
+// window pass streams (bench step with caches evicted before it: 249.0 -> 246.1 us, back to back
+// 233.4 -> 232.6 us); the tail pass keeps the default (streaming it too: 247.6 / 234.8 us).
+#ifndef KYRO_SPEC_WINDOW_POLICY
+#define KYRO_SPEC_WINDOW_POLICY 2
+#endif
+#ifndef KYRO_SPEC_TAIL_POLICY
+#define KYRO_SPEC_TAIL_POLICY 0
+#endif
+constexpr int kSpecWindowPolicy = KYRO_SPEC_WINDOW_POLICY;
+constexpr int kSpecTailPolicy = KYRO_SPEC_TAIL_POLICY;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float block_max(float v, float* sh) {
@@ -138,14 +149,14 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // `chunk`: the per-thread offsets do not depend on the chunk, so a loop can issue one chunk
 // after another without vector address arithmetic, and positions past the chunk's end read as
 // zeros (the consumer masks them, strided_index >= v1).
-template <bool VEC>
+template <bool VEC, int POL = kLoadCached>
 __device__ __forceinline__ void load_buffer(const float* chunk, int bytes, float (&x)[kPer]) {
     const __amdgpu_buffer_rsrc_t r =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(chunk), (short)0, bytes, kRawBufferWord3);
     if constexpr (VEC) {
 #pragma unroll
         for (int it = 0; it < kPer / 4; ++it) {
-            const auto f = __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16, it * kT * 16, 0);
+            const auto f = __builtin_amdgcn_raw_buffer_load_b128(r, (int)threadIdx.x * 16, it * kT * 16, POL);
             x[it * 4 + 0] = __uint_as_float(f[0]);
             x[it * 4 + 1] = __uint_as_float(f[1]);
             x[it * 4 + 2] = __uint_as_float(f[2]);
@@ -154,7 +165,7 @@ __device__ __forceinline__ void load_buffer(const float* chunk, int bytes, float
     } else {
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
-            x[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, i * kT * 4, 0));
+            x[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, i * kT * 4, POL));
     }
 }
 
@@ -281,7 +292,7 @@ __global__ __launch_bounds__(kT) void spec_stats_kernel(SpecArgs a) {
     const int v0 = c * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
     float x[kPer];
-    load_buffer<VEC>(stats_row_base(a, b, row) + v0, (v1 - v0) * 4, x);
+    load_buffer<VEC, kSpecWindowPolicy>(stats_row_base(a, b, row) + v0, (v1 - v0) * 4, x);
     const int k = a.num_draft[b];
     const float T = a.temperature[b];
     const uint32_t tk = a.kmax > 0 ? a.draft_tokens[(size_t)b * a.kmax + min(pos, a.kmax - 1)] : 0u;
@@ -717,7 +728,7 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
         m.r = __builtin_amdgcn_readlane(lrow, j);
         m.c = __builtin_amdgcn_readlane(lc, j);
         const int v0 = m.c * a.chunk;
-        load_buffer<VEC>(reinterpret_cast<const float*>(ptr), (min(a.V, v0 + a.chunk) - v0) * 4, x);
+        load_buffer<VEC, kSpecTailPolicy>(reinterpret_cast<const float*>(ptr), (min(a.V, v0 + a.chunk) - v0) * 4, x);
     };
     // Results are not stored inside the loop: a store there is counted with the loads, and a wait
     // for it (before its data registers are reused) would also wait for the prefetch issued
