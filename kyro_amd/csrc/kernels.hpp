@@ -62,6 +62,9 @@ struct AttnArgs {
     int plan_max_chunk;
     long long plan_slots;  // partial-state slots in the workspace (plan_slot_bound)
     int4* plan_seq;
+    // [B + 1]: the combine pass's work units ((kv head, 8-row chunk) of a split sequence) before
+    // sequence b; [B] is their total.
+    int* plan_cw;
     // kSchedWords counters, zero at launch: the items claimed on each of the 8 XCD lanes beyond
     // the grid's first items, then the workgroups done; the last workgroup resets them to zero.
     int* sched;

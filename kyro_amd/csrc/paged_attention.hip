@@ -175,6 +175,55 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int nsplit, in
 // Under the balanced schedule the split count and the slots come from plan_seq (written by the
 // first pass): split s of row n (row group n / plan_rw) of kv head h sits in slot
 // first + (s * ugroups_per_seq + h / hpw) * row_groups + n / plan_rw, head h % hpw.
+// Merges the nsplit partial states of one output row (workspace rows r0 + s * stride) into this
+// thread's four columns d .. d + 3 and stores them. The loads of kMergeBatch splits are issued
+// together (a split index past the last reads the last split again and is dropped), so a row with
+// up to kMergeBatch splits costs one memory round trip; longer rows merge batch after batch with
+// the usual running-max rescale (for one batch this is the plain two-pass formula).
+constexpr int kMergeBatch = 16;
+template <int D>
+__device__ __forceinline__ void merge_row(const AttnArgs& a, const SeqInfo& si, int n, int d, size_t r0,
+                                          size_t stride, int nsplit) {
+    float M = kNegInf, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < nsplit; s0 += kMergeBatch) {
+        float m[kMergeBatch], l[kMergeBatch];
+        float4 v[kMergeBatch];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const size_t r = r0 + (size_t)min(s0 + i, nsplit - 1) * stride;
+            m[i] = a.ws_m[r];
+            l[i] = a.ws_l[r];
+            v[i] = *reinterpret_cast<const float4*>(a.ws_acc + r * D + d);
+        }
+        float mb = M;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) mb = s0 + i < nsplit ? fmaxf(mb, m[i]) : mb;
+        if (mb == kNegInf) continue;  // nothing visible so far
+        if (M != kNegInf) {
+            const float f = fast_exp2(M - mb);
+            L *= f;
+            acc.x *= f;
+            acc.y *= f;
+            acc.z *= f;
+            acc.w *= f;
+        }
+        M = mb;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const float w = s0 + i < nsplit ? fast_exp2(m[i] - M) : 0.f;
+            L += w * l[i];
+            acc.x += w * v[i].x;
+            acc.y += w * v[i].y;
+            acc.z += w * v[i].z;
+            acc.w += w * v[i].w;
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+}
+
+// Grid schedule: one workgroup per (unit, RPW rows); every unit has the same split count rule.
 template <int D>
 __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
     constexpr int Q = D / 4;
@@ -185,51 +234,50 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
     if (!si.ok) return;
     const int n = blockIdx.y * RPW + (int)threadIdx.x / Q;
     if (n >= si.rows) return;
-    int nsplit, nrg = 0, first = 0;
-    if (a.plan) {
-        const int4 ps = a.plan_seq[si.b];
-        nsplit = ps.x;
-        nrg = ps.y;
-        first = ps.z;
-        if (nrg <= 0) return;
-    } else {
-        nsplit = num_splits_for(a, si.nblk);
-    }
+    const int nsplit = num_splits_for(a, si.nblk);
     if (nsplit <= 1) return;
+    merge_row<D>(a, si, n, ((int)threadIdx.x % Q) * 4, (size_t)unit * a.splits * a.rows_cap + n, a.rows_cap,
+                 nsplit);
+}
+
+// Balanced schedule (head_dim 128): the plan lists the combine work, one unit per (kv head,
+// kCombineRows rows) of each split sequence, with per-sequence prefix counts in plan_cw. A grid
+// of any size walks the list; with nothing split every workgroup reads one word and returns.
+constexpr int kCombineRows = kThreads / (128 / 4);
+__global__ __launch_bounds__(kThreads) void attn_combine_plan_kernel(AttnArgs a) {
+    constexpr int D = 128, Q = D / 4;
+    __shared__ int cw[kPlanMaxSeqs + 1];
+    const int total = a.plan_cw[a.B];
+    if ((int)blockIdx.x >= total) return;
+    for (int i = threadIdx.x; i <= a.B; i += kThreads) cw[i] = a.plan_cw[i];
+    __syncthreads();
     const int d = ((int)threadIdx.x % Q) * 4;
-    // Workspace row of split s, local row n of this unit: consecutive splits are `stride` rows
-    // apart.
-    size_t r0, stride;
-    if (a.plan) {
-        const int upseq = a.ugroups / a.B;
+    const int upseq = a.ugroups / a.B;
+    for (int w = blockIdx.x; w < total; w += gridDim.x) {
+        // The last sequence whose work starts at or before w (it has work: see plan_build).
+        int lo = 0, hi = a.B - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (cw[mid] <= w) lo = mid;
+            else hi = mid - 1;
+        }
+        SeqInfo si;
+        si.b = lo;
+        si.q0 = a.q_start ? a.q_start[lo] : lo;
+        const int q1 = a.q_start ? a.q_start[lo + 1] : lo + 1;
+        const int4 ps = a.plan_seq[lo];
+        si.rows = (q1 - si.q0) * a.group;
+        const int chunks = (si.rows + kCombineRows - 1) / kCombineRows;
+        const int local = w - cw[lo];
+        si.kvh = local / chunks;
+        const int n = (local - si.kvh * chunks) * kCombineRows + (int)threadIdx.x / Q;
+        if (n >= si.rows) continue;
+        const int nrg = ps.y, first = ps.z;
         const int rg = n / a.plan_rw;
         const size_t slot = (size_t)first + (size_t)(si.kvh / a.hpw) * nrg + rg;
-        r0 = (slot * a.hpw + si.kvh % a.hpw) * a.plan_rw + (n - rg * a.plan_rw);
-        stride = (size_t)upseq * nrg * a.hpw * a.plan_rw;
-    } else {
-        r0 = (size_t)unit * a.splits * a.rows_cap + n;
-        stride = a.rows_cap;
+        merge_row<D>(a, si, n, d, (slot * a.hpw + si.kvh % a.hpw) * a.plan_rw + (n - rg * a.plan_rw),
+                     (size_t)upseq * nrg * a.hpw * a.plan_rw, ps.x);
     }
-    float M = kNegInf;
-#pragma unroll 8
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_m[r0 + s * stride]);
-    float L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (M != kNegInf) {
-#pragma unroll 4
-        for (int s = 0; s < nsplit; ++s) {
-            const size_t r = r0 + s * stride;
-            const float w = fast_exp2(a.ws_m[r] - M);
-            L += w * a.ws_l[r];
-            const float4 v = *reinterpret_cast<const float4*>(a.ws_acc + r * D + d);
-            acc.x += w * v.x;
-            acc.y += w * v.y;
-            acc.z += w * v.z;
-            acc.w += w * v.w;
-        }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    store_row4<D>(a, out_row(a, si, n), d, acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 // ------------------------------------------------------------------------------ MFMA kernel
@@ -247,6 +295,20 @@ struct KVPair {
     uint4 v[2][4];   // [block][e]: token 4 g + e, head dims 8 r .. 8 r + 7
 };
 
+#ifndef KYRO_ATTN_K_LINES
+#define KYRO_ATTN_K_LINES 1
+#endif
+// K loaded by whole token rows (as V is), then staged through LDS into MFMA layout, or loaded
+// directly in MFMA layout. The direct form reads 16 rows x 64 bytes per instruction (half lines),
+// which holds one workgroup to ~28 GB/s against ~66 GB/s for whole lines. Row loads pay where a
+// workgroup's own rate sets the pace: one 16-row tile (MHA and decode shapes: 68.3 -> 62.9 us on
+// the MHA Llama-2-7B batch) and the balanced schedule's uneven batches (skewed prefix 187 -> 177
+// us). On a uniform batch with two tiles (the Llama-3-8B step on the grid) every CU streams at
+// its share of HBM anyway, and the staging cost 168 -> 170.6 us, so that kernel loads K directly.
+// KYRO_ATTN_K_LINES: 0 never, 1 as above, 2 always.
+template <int NTW, bool PLAN>
+constexpr bool kKLinesFor = KYRO_ATTN_K_LINES == 2 || (KYRO_ATTN_K_LINES == 1 && (NTW == 1 || PLAN));
+
 // Issues the 16 loads of one block pair. A negative block id reads as zeros (never dereferenced).
 // Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
 constexpr int kRawBufferWord3 = 0x00020000;
@@ -256,30 +318,66 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
 // addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
 // a prefetched pair in flight. POL is the loads' cache policy (kLoadCached or kLoadStream).
-template <int POL>
+template <int POL, bool KL>
 __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t block_stride, size_t kv_off, int r, int g) {
     constexpr int kSlabBytes = kMfmaBS * kMfmaD * 2;
     const int koff = (r * kMfmaD + 8 * g) * 2;        // bytes; + 64 s for head-dim slot s
     const int voff = (4 * g * kMfmaD + 8 * r) * 2;    // bytes; + 256 e for token 4 g + e
+    __amdgpu_buffer_rsrc_t kr[2], vr[2];
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
         const int blk = bi ? blk1 : blk0;
         const size_t base = (size_t)(blk >= 0 ? blk : 0) * block_stride + kv_off;
         const uint16_t* kslab = blk >= 0 ? kp + base : kZeroSlab;
         const uint16_t* vslab = blk >= 0 ? vp + base : kZeroSlab;
-        const __amdgpu_buffer_rsrc_t kr =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), (short)0, kSlabBytes, kRawBufferWord3);
-        const __amdgpu_buffer_rsrc_t vr =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), (short)0, kSlabBytes, kRawBufferWord3);
+        kr[bi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), (short)0, kSlabBytes, kRawBufferWord3);
+        vr[bi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vslab), (short)0, kSlabBytes, kRawBufferWord3);
+    }
+    // K of both blocks first: the computation of this pair starts with K (S = K Q^T) while the
+    // V loads may still be in flight.
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr, koff, 64 * s, POL));
+    for (int bi = 0; bi < 2; ++bi) {
+        if constexpr (KL) {
+            // K in V's layout (whole 256-byte token rows per 16 lanes); stage_k puts it in MFMA
+            // layout through LDS.
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                p.k[bi][e] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], voff, 256 * e, POL));
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], koff, 64 * s, POL));
+        }
+    }
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff, 256 * e, POL));
-    }
+            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 256 * e, POL));
+}
+
+// One wave's LDS tile for staging the K of one block pair: [block][token][16-byte chunk], the
+// chunk index XOR-ed with the token so that both the row-wise writes and the MFMA-layout reads
+// (16 tokens, one chunk each) fall in distinct banks.
+constexpr int kKStageChunks = 2 * kMfmaBS * (kMfmaD / 8);  // uint4 per wave (8 KiB)
+
+// K of a pair from the load layout (lane (r, g), register e: token 4 g + e, chunk r) to the MFMA
+// A-operand layout (register s: token r, chunk 4 s + g). The tile belongs to the calling wave
+// alone, and a wave's LDS operations complete in order, so no barrier is needed.
+__device__ __forceinline__ void stage_k(KVPair& p, uint4* __restrict__ tile, int r, int g) {
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 4 * g + e;
+            tile[bi * 256 + t * 16 + (r ^ t)] = __builtin_bit_cast(uint4, p.k[bi][e]);
+        }
+#pragma unroll
+    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, tile[bi * 256 + r * 16 + ((4 * s + g) ^ r)]);
 }
 
 // Stages the block ids of the workgroup's split in LDS (validated once, -1 for a bad id), so the
@@ -464,6 +562,13 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         P.key[sq] = sq < a.B ? key[j] : 0u;  // padding keys rank below every sequence
     }
     __syncthreads();
+    // The combine pass's work: kCombineRows-row chunks of every kv head of a split sequence, in
+    // sequence order (column j of the scan holds sequences j kThreads ..).
+    int cw[S], cwt[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+        cw[j] = (ns[j] > 1 && r[j] > 0) ? a.Hkv * ((qlen[j] * a.group + kCombineRows - 1) / kCombineRows) : 0;
+    block_scan_excl<S>(cw, cwt, P.red);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int sq = t + j * kThreads;
@@ -522,9 +627,22 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         if (t < 8) P.lane_len[t] = 0;
         for (int pos = t; pos < a.B; pos += kThreads)
             if (blockIdx.x == 0) a.plan_seq[pos] = make_int4(0, 0, 0, 0);
-        if (blockIdx.x == 0 && t == 0) latch_error(a.err, ERR_PLAN);
+        if (blockIdx.x == 0 && t == 0) {
+            a.plan_cw[a.B] = 0;
+            latch_error(a.err, ERR_PLAN);
+        }
         __syncthreads();
         return 0;
+    }
+    if (blockIdx.x == 0) {
+        int before = 0;
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const int sq = t + j * kThreads;
+            if (sq < a.B) a.plan_cw[sq] = before + cw[j];
+            before += cwt[j];
+        }
+        if (t == 0) a.plan_cw[a.B] = before;
     }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
@@ -592,9 +710,9 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 // mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
 // head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
 // workspace rows pb0 + h * pbstep + n for head h of the group.
-template <int NTW, int HP, int POL>
+template <int NTW, int HP, int POL, bool KL>
 __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
-                                          const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
+                                          uint4* kst, const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
                                           int nsplit, size_t pb0, size_t pbstep) {
     constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
@@ -652,7 +770,14 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
         }
 
         // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
+        uint4* const ktile = KL ? kst + wave * kKStageChunks : kst;
         auto compute = [&](KVPair& kv, int pb, int blk0, int blk1) {
+            if constexpr (KL) {
+                // Keep the next pair's loads (issued just before) ahead of the staging, so that
+                // they are in flight while this pair's K waits.
+                __builtin_amdgcn_sched_barrier(0);
+                stage_k(kv, ktile, r, g);
+            }
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
             f32x4 S[2][NTW];
 #pragma unroll
@@ -782,14 +907,14 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 // wait that precedes the computation of the pair before it.
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<POL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<POL, KL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<POL>(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    load_pair<POL, KL>(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
                     compute(bufA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<POL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    load_pair<POL, KL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                     compute(bufB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
@@ -1208,9 +1333,11 @@ template <int NTW, int HP, int POL, bool PLAN>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     __shared__ Frame<NTW * 16, kMfmaD> frame[HP];
     __shared__ int s_blk[kMaxChunkBlocks];
+    constexpr bool KL = kKLinesFor<NTW, PLAN>;
+    __shared__ uint4 s_kst[KL ? kWaves * kKStageChunks : 1];
     mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
                                         size_t pbs) {
-        mfma_item<NTW, HP, POL>(a, frame, s_blk, si, ug, rg, bb, be, ns, pb0, pbs);
+        mfma_item<NTW, HP, POL, KL>(a, frame, s_blk, s_kst, si, ug, rg, bb, be, ns, pb0, pbs);
     });
 }
 
@@ -1457,7 +1584,13 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
             else attn_vector_kernel<float, 64><<<grid, block, 0, stream>>>(a);
         }
     }
-    if (a.plan || a.splits > 1) {
+    if (a.plan) {
+        // At most one workgroup per possible work unit, and at most kCombineMaxGrid of them
+        // (each then walks several units).
+        constexpr long long kCombineMaxGrid = 2048;
+        const long long units = (long long)a.units * ((a.rows_cap + kCombineRows - 1) / kCombineRows);
+        attn_combine_plan_kernel<<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0, stream>>>(a);
+    } else if (a.splits > 1) {
         const int rpw = kThreads / (a.D / 4);
         const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
         if (a.D == 128) attn_combine_kernel<128><<<cgrid, block, 0, stream>>>(a);

@@ -307,7 +307,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (a.plan) {
         const size_t rows = s.plan_slots * a.hpw * a.plan_rw;
         s.ws_bytes = 2 * align_up(rows * sizeof(float), 256) + align_up(rows * a.D * sizeof(float), 256) +
-                     align_up((size_t)a.B * sizeof(int4), 256);
+                     align_up((size_t)a.B * sizeof(int4), 256) + align_up((size_t)(a.B + 1) * sizeof(int), 256);
     } else if (a.splits > 1) {
         const size_t rows = (size_t)a.units * a.splits * a.rows_cap;
         s.ws_bytes = 2 * align_up(rows * sizeof(float), 256) + align_up(rows * a.D * sizeof(float), 256);
@@ -315,7 +315,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     return KYRO_OK;
 }
 
-// Points the launch's partial-state arrays (and the plan's per-sequence table) into `base`,
+// Points the launch's partial-state arrays (and the plan's per-sequence tables) into `base`,
 // s.ws_bytes of device memory.
 void attention_workspace(AttnSetup& s, char* base) {
     kyro::AttnArgs& a = s.a;
@@ -324,7 +324,11 @@ void attention_workspace(AttnSetup& s, char* base) {
     a.ws_m = reinterpret_cast<float*>(base);
     a.ws_l = reinterpret_cast<float*>(base + mb_bytes);
     a.ws_acc = reinterpret_cast<float*>(base + 2 * mb_bytes);
-    if (a.plan) a.plan_seq = reinterpret_cast<int4*>(base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256));
+    if (a.plan) {
+        char* p = base + 2 * mb_bytes + align_up(rows * a.D * sizeof(float), 256);
+        a.plan_seq = reinterpret_cast<int4*>(p);
+        a.plan_cw = reinterpret_cast<int*>(p + align_up((size_t)a.B * sizeof(int4), 256));
+    }
 }
 
 // Everything a verify launch decides from its params alone: validation, chunking, window,
