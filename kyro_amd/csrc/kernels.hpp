@@ -94,16 +94,14 @@ __host__ __device__ inline int plan_chunk_blocks(long long T, int maxnb, int gri
     return (int)(CL > max_chunk ? max_chunk : CL);
 }
 
-// Splits of a sequence of nb blocks under chunk length C: one split when nb <= C, else
-// ns = ceil(nb / C) equal chunks of ch blocks (even), the last one shorter.
+// Splits of a sequence of nb blocks under chunk length C: one split when nb <= C (ch = nb), else
+// ns = ceil(nb / C) chunks of ch = C blocks from the start, the last one shorter.
 __host__ __device__ inline void plan_split(int nb, int C, int& ns, int& ch) {
     ns = 1;
     ch = nb;
     if (nb > C) {
         ns = (nb + C - 1) / C;
-        ch = (nb + ns - 1) / ns;
-        ch = (ch + 1) & ~1;
-        ns = (nb + ch - 1) / ch;
+        ch = C;
     }
 }
 

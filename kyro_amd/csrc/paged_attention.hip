@@ -400,28 +400,36 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //  * chunk C = L when no sequence is longer than L (nothing splits, so a uniform batch keeps one
 //    item per (sequence, kv head group)), else ceil(L / kPlanChunkDiv) (L / 2), within
 //    [kPlanMinChunk, max chunk];
-//    a longer sequence splits into equal even chunks;
-//  * sequences are ordered by chunk length, longest first (lower index first among equals), so
-//    the longest items start first;
-//  * item groups (sequence, chunk, kv head group) are dealt to 8 lanes, one per XCD, in a snake
-//    (lanes 0..7, then 7..0), which keeps the lanes' totals even; the row groups of an item group
-//    take consecutive positions of one lane (item indices 8 apart), so they run together on one
-//    XCD and share its L2;
+//  * a longer sequence splits into chunks of C blocks from its start, the last one shorter;
+//  * item groups (sequence, chunk, kv head group) come in two phases: first every chunk but the
+//    last of each split sequence (all C blocks long), then the last chunk of every sequence (for
+//    an unsplit sequence its only chunk), ordered by length, longest first. Greedy claiming then
+//    runs largest-first over single items rather than whole sequences: the short last chunks and
+//    short sequences fill in at the end, which measured shorter tails than splitting each
+//    sequence into equal chunks ordered by sequence;
+//  * item groups are dealt to 8 lanes, one per XCD, in a snake (lanes 0..7, then 7..0), which
+//    keeps the lanes' totals even; the row groups of an item group take consecutive positions of
+//    one lane, so they run together on one XCD and share its L2;
 //  * a workgroup takes one item of its XCD's lane at a time, the next unclaimed one (a counter
-//    per lane), so the workgroups of an XCD share its lane's items greedily, largest first.
+//    per lane), so the workgroups of an XCD share its lane's items greedily, largest first. Each
+//    workgroup keeps only its own lane's item counts.
 struct PlanLds {
-    alignas(16) uint32_t key[kPlanMaxSeqs];  // by sequence: (chunk << 16) | (0xffff - b); larger first
-    int b[kPlanMaxSeqs];         // the rest by position in that order
-    int ns[kPlanMaxSeqs];        // splits
-    int ch[kPlanMaxSeqs];        // blocks per split
-    int r[kPlanMaxSeqs];         // row groups (0: no work)
+    alignas(16) uint32_t key[kPlanMaxSeqs];  // by sequence: (last chunk << 16) | (0xffff - b); larger first
+    // By sequence:
+    int ns[kPlanMaxSeqs];      // splits (0: no rows)
+    int r[kPlanMaxSeqs];       // row groups
     int ctx[kPlanMaxSeqs];
     int q0[kPlanMaxSeqs];
     int qlen[kPlanMaxSeqs];
-    int g0[kPlanMaxSeqs];        // first item group
-    int slot0[kPlanMaxSeqs];     // first partial-state slot
-    int lane0[8][kPlanMaxSeqs];  // items of earlier sequences on each lane
-    int lane_len[8];
+    int gA[kPlanMaxSeqs];      // first phase-A item group
+    int slot0[kPlanMaxSeqs];   // first partial-state slot
+    int lane0A[kPlanMaxSeqs];  // this lane's phase-A items of earlier sequences
+    // By phase-B position (last chunks, longest first):
+    int bB[kPlanMaxSeqs];      // sequence
+    int lane0B[kPlanMaxSeqs];  // this lane's items before the position (phase A included)
+    int lenA, len;             // this lane's phase-A items, all its items
+    int GA;                    // phase-A item groups (all lanes)
+    int C;                     // chunk length, blocks
     int red[kWaves][9];
     long long red64[kWaves];
 };
@@ -484,22 +492,44 @@ __device__ __forceinline__ void block_scan_excl(int (&v)[V], int (&total)[V], in
     __syncthreads();
 }
 
-// Builds the plan (every thread of the workgroup takes part; thread t reads sequences
-// t + j kThreads and owns plan positions S t .. S t + S - 1, S = kPlanMaxSeqs / kThreads).
-// Returns the number of item positions (8 x the longest lane). Workgroup 0 latches input
-// errors and publishes {splits, row groups, first slot} per sequence for the combine pass.
-// Up to kThreads sequences are ordered longest chunk first; larger batches keep their order
-// (the claiming still shares the work out greedily, and the sort would cost more than it saves).
+// Local exclusive prefix of V values over a thread's S consecutive entries, then the block scan
+// of the thread totals: v[j][k] becomes the exclusive prefix of entry j in the workgroup's order,
+// total[k] the sum of all.
+template <int S, int V>
+__device__ __forceinline__ void scan_owned(int (&v)[S][V], int (&total)[V], int (*red)[9]) {
+    int run[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) run[k] = 0;
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const int x = v[j][k];
+            v[j][k] = run[k];
+            run[k] += x;
+        }
+    block_scan_excl<V>(run, total, red);
+#pragma unroll
+    for (int j = 0; j < S; ++j)
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[j][k] += run[k];
+}
+
+// Builds the plan (every thread of the workgroup takes part; thread t owns sequences and
+// phase-B positions S t .. S t + S - 1, S = kPlanMaxSeqs / kThreads). Workgroup 0 latches input
+// errors and publishes {splits, row groups, first slot} per sequence and the combine pass's work
+// list.
 template <int RW, int HP>
-__device__ int plan_build(const AttnArgs& a, PlanLds& P) {
+__device__ void plan_build(const AttnArgs& a, PlanLds& P) {
     constexpr int S = kPlanMaxSeqs / kThreads;
     const int t = threadIdx.x;
     const int wave = t >> 6;
+    const int x = (int)blockIdx.x & 7;  // this workgroup's lane
     const int U = a.Hkv / HP;
     int ctx[S], q0[S], qlen[S], r[S], nb[S];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-        const int sq = t + j * kThreads;
+        const int sq = S * t + j;
         ctx[j] = q0[j] = qlen[j] = r[j] = nb[j] = 0;
         if (sq < a.B) {
             const int64_t c = a.ctx_lens[sq];
@@ -552,148 +582,148 @@ __device__ int plan_build(const AttnArgs& a, PlanLds& P) {
         maxnb = max(maxnb, P.red[i][0]);
     }
     const int C = plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk);
-    int ns[S], ch[S];
-    uint32_t key[S];
+    // Per sequence: splits, phase-A item groups, partial-state slots and the combine pass's work
+    // units (kCombineRows-row chunks of every kv head of a split sequence), in sequence order.
+    int ns[S], v3[S][3], t3[3];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-        const int sq = t + j * kThreads;
-        plan_split(nb[j], C, ns[j], ch[j]);
-        key[j] = ((uint32_t)(r[j] > 0 ? ch[j] : 0) << 16) | (uint32_t)(0xffff - sq);
-        P.key[sq] = sq < a.B ? key[j] : 0u;  // padding keys rank below every sequence
+        const int sq = S * t + j;
+        int n, ch;
+        plan_split(nb[j], C, n, ch);
+        ns[j] = r[j] > 0 ? n : 0;
+        const int last = nb[j] - (n - 1) * C;  // blocks of the last chunk
+        // Unique per sequence (a sequence without rows sorts last); padding ranks below all.
+        P.key[sq] = sq < a.B ? ((uint32_t)(r[j] > 0 ? last : 0) << 16) | (uint32_t)(0xffff - sq) : 0u;
+        v3[j][0] = r[j] > 0 ? (n - 1) * U : 0;
+        v3[j][1] = ns[j] * U * r[j];
+        v3[j][2] = (ns[j] > 1) ? a.Hkv * ((qlen[j] * a.group + kCombineRows - 1) / kCombineRows) : 0;
     }
-    __syncthreads();
-    // The combine pass's work: kCombineRows-row chunks of every kv head of a split sequence, in
-    // sequence order (column j of the scan holds sequences j kThreads ..).
-    int cw[S], cwt[S];
-#pragma unroll
-    for (int j = 0; j < S; ++j)
-        cw[j] = (ns[j] > 1 && r[j] > 0) ? a.Hkv * ((qlen[j] * a.group + kCombineRows - 1) / kCombineRows) : 0;
-    block_scan_excl<S>(cw, cwt, P.red);
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-        const int sq = t + j * kThreads;
-        if (sq >= a.B) continue;
-        int rank = sq;
-        if (a.B <= kThreads) {
-            // Rank = number of larger keys: four keys per LDS read, reads issued together.
-            rank = 0;
-            const uint4* k4 = reinterpret_cast<const uint4*>(P.key);
-#pragma unroll 4
-            for (int i = 0; i < (a.B + 3) / 4; ++i) {
-                const uint4 k = k4[i];
-                rank += (k.x > key[j] ? 1 : 0) + (k.y > key[j] ? 1 : 0) + (k.z > key[j] ? 1 : 0) + (k.w > key[j] ? 1 : 0);
-            }
-        }
-        P.b[rank] = sq;
-        P.ns[rank] = ns[j];
-        P.ch[rank] = ch[j];
-        P.r[rank] = r[j];
-        P.ctx[rank] = ctx[j];
-        P.q0[rank] = q0[j];
-        P.qlen[rank] = qlen[j];
-    }
-    __syncthreads();
-    // Item groups and slots in plan order (thread t: positions S t ..), dealt to the 8 lanes.
-    int rp[S], nig[S], gl[S];
-    int loc = 0;
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-        const int pos = S * t + j;
-        rp[j] = pos < a.B ? P.r[pos] : 0;
-        nig[j] = rp[j] > 0 ? U * P.ns[pos] : 0;
-        gl[j] = loc;
-        loc += nig[j];
-    }
-    int sa[1] = {loc}, ta[1];
-    block_scan_excl<1>(sa, ta, P.red);
-    int cnt[S][9];
-    int sb[9], tb[9];
-#pragma unroll
-    for (int x = 0; x < 9; ++x) sb[x] = 0;
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-        gl[j] += sa[0];  // first item group of position S t + j
-#pragma unroll
-        for (int x = 0; x < 8; ++x) cnt[j][x] = snake_count(gl[j], nig[j], x) * rp[j];
-        cnt[j][8] = nig[j] * rp[j];
-#pragma unroll
-        for (int x = 0; x < 9; ++x) sb[x] += cnt[j][x];
-    }
-    block_scan_excl<9>(sb, tb, P.red);
-    if (tb[8] > a.plan_slots) {
+    scan_owned<S, 3>(v3, t3, P.red);  // its barriers also publish P.key
+    if (t3[1] > a.plan_slots) {
         // More partial-state slots than the workspace holds: a plan/bound mismatch. Latch it and
         // run no item (every workgroup derives the same totals, so all of them skip the walk and
-        // still count themselves done); the combine pass sees no row groups anywhere.
-        if (t < 8) P.lane_len[t] = 0;
-        for (int pos = t; pos < a.B; pos += kThreads)
-            if (blockIdx.x == 0) a.plan_seq[pos] = make_int4(0, 0, 0, 0);
+        // still count themselves done); the combine pass sees no work.
+        if (t == 0) P.len = P.lenA = 0;
+        for (int sq = t; sq < a.B; sq += kThreads)
+            if (blockIdx.x == 0) a.plan_seq[sq] = make_int4(0, 0, 0, 0);
         if (blockIdx.x == 0 && t == 0) {
             a.plan_cw[a.B] = 0;
             latch_error(a.err, ERR_PLAN);
         }
         __syncthreads();
-        return 0;
+        return;
     }
-    if (blockIdx.x == 0) {
-        int before = 0;
+    const int GA = t3[0];
+    // This lane's phase-A items per sequence (row groups consecutive).
+    int cA[S][1], tA[1];
 #pragma unroll
-        for (int j = 0; j < S; ++j) {
-            const int sq = t + j * kThreads;
-            if (sq < a.B) a.plan_cw[sq] = before + cw[j];
-            before += cwt[j];
+    for (int j = 0; j < S; ++j) cA[j][0] = snake_count(v3[j][0], r[j] > 0 ? (ns[j] - 1) * U : 0, x) * r[j];
+    scan_owned<S, 1>(cA, tA, P.red);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        const int sq = S * t + j;
+        if (sq < a.B) {
+            P.ns[sq] = ns[j];
+            P.r[sq] = r[j];
+            P.ctx[sq] = ctx[j];
+            P.q0[sq] = q0[j];
+            P.qlen[sq] = qlen[j];
+            P.gA[sq] = v3[j][0];
+            P.slot0[sq] = v3[j][1];
+            P.lane0A[sq] = cA[j][0];
+            if (blockIdx.x == 0) {
+                a.plan_seq[sq] = make_int4(ns[j], r[j], v3[j][1], 0);
+                a.plan_cw[sq] = v3[j][2];
+            }
         }
-        if (t == 0) a.plan_cw[a.B] = before;
     }
+    if (blockIdx.x == 0 && t == 0) a.plan_cw[a.B] = t3[2];
+    // Phase-B order: up to kThreads sequences by last chunk, longest first (rank = count of
+    // larger keys, four keys per LDS read); larger batches keep their order.
+    for (int sq = t; sq < a.B; sq += kThreads) {
+        int rank = sq;
+        if (a.B <= kThreads) {
+            const uint32_t key = P.key[sq];
+            rank = 0;
+            const uint4* k4 = reinterpret_cast<const uint4*>(P.key);
+#pragma unroll 4
+            for (int i = 0; i < (a.B + 3) / 4; ++i) {
+                const uint4 k = k4[i];
+                rank += (k.x > key ? 1 : 0) + (k.y > key ? 1 : 0) + (k.z > key ? 1 : 0) + (k.w > key ? 1 : 0);
+            }
+        }
+        P.bB[rank] = sq;
+    }
+    __syncthreads();
+    // This lane's phase-B items per position: U item groups each, groups GA + U p ...
+    int cB[S][1], tB[1];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int pos = S * t + j;
-        if (pos < a.B) {
-            P.g0[pos] = gl[j];
-            P.slot0[pos] = sb[8];
-#pragma unroll
-            for (int x = 0; x < 8; ++x) P.lane0[x][pos] = sb[x];
-            if (blockIdx.x == 0) a.plan_seq[P.b[pos]] = make_int4(P.ns[pos], rp[j], sb[8], 0);
-        }
-#pragma unroll
-        for (int x = 0; x < 9; ++x) sb[x] += cnt[j][x];
+        cB[j][0] = pos < a.B ? snake_count(GA + U * pos, U, x) * P.r[P.bB[pos]] : 0;
     }
-    if (t < 8) P.lane_len[t] = tb[t];
-    int longest = 0;
+    scan_owned<S, 1>(cB, tB, P.red);
 #pragma unroll
-    for (int x = 0; x < 8; ++x) longest = max(longest, tb[x]);
+    for (int j = 0; j < S; ++j) {
+        const int pos = S * t + j;
+        if (pos < a.B) P.lane0B[pos] = tA[0] + cB[j][0];
+    }
+    if (t == 0) {
+        P.lenA = tA[0];
+        P.len = tA[0] + tB[0];
+        P.GA = GA;
+        P.C = C;
+    }
     __syncthreads();
-    return 8 * longest;
 }
 
 struct PlanItem {
-    int p;      // position of the sequence in the plan order
+    int b;      // sequence
     int hp;     // kv head group within the sequence
     int rg;     // row group
     int chunk;  // split
     int slot;   // partial-state slot
 };
 
-// Item position i of the plan, or false for an empty position of a short lane.
+// The k-th item of this workgroup's lane, or false past the lane's last item.
 template <int HP>
-__device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, int i, PlanItem& it) {
-    const int x = i & 7, k = i >> 3;
-    if (k >= P.lane_len[x]) return false;
-    int lo = 0, hi = a.B - 1;  // the last sequence whose lane-x items start at or before k
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (P.lane0[x][mid] <= k) lo = mid;
-        else hi = mid - 1;
-    }
-    const int rr = P.r[lo];
-    const int idx = k - P.lane0[x][lo];
-    const int igl = idx / rr;
-    const int q = snake_nth(P.g0[lo], x, igl) - P.g0[lo];  // item group within the sequence
+__device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, int k, PlanItem& it) {
+    if (k >= P.len) return false;
+    const int x = (int)blockIdx.x & 7;
     const int U = a.Hkv / HP;
-    it.p = lo;
+    int b, g0, idx, c0;
+    // The last entry whose items start at or before k (it has items: an entry without any shares
+    // its start with the next one).
+    int lo = 0, hi = a.B - 1;
+    if (k < P.lenA) {
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (P.lane0A[mid] <= k) lo = mid;
+            else hi = mid - 1;
+        }
+        b = lo;
+        g0 = P.gA[b];
+        idx = k - P.lane0A[b];
+        c0 = 0;
+    } else {
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (P.lane0B[mid] <= k) lo = mid;
+            else hi = mid - 1;
+        }
+        b = P.bB[lo];
+        g0 = P.GA + U * lo;
+        idx = k - P.lane0B[lo];
+        c0 = P.ns[b] - 1;
+    }
+    const int rr = P.r[b];
+    const int igl = idx / rr;
+    const int q = snake_nth(g0, x, igl) - g0;  // item group within the entry
+    it.b = b;
     it.rg = idx - igl * rr;
-    it.chunk = q / U;
-    it.hp = q - it.chunk * U;
-    it.slot = P.slot0[lo] + q * rr + it.rg;
+    it.chunk = c0 + q / U;
+    it.hp = q - (q / U) * U;
+    it.slot = P.slot0[b] + (it.chunk * U + it.hp) * rr + it.rg;
     return true;
 }
 
@@ -1262,7 +1292,7 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
 
     if constexpr (PLAN) {
         __shared__ PlanLds plan;
-        (void)plan_build<RW, HP>(a, plan);
+        plan_build<RW, HP>(a, plan);
         const int G = a.plan_grid;  // a multiple of 8
         const int U = a.Hkv / HP;
         // Workgroup w works on lane x = w % 8, the items dealt to its XCD: first the lane's item
@@ -1271,31 +1301,30 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
         // row groups of one item group (consecutive on the lane) run together and share its L2.
         __shared__ int s_claim;
         const int x = (int)blockIdx.x & 7;
-        const int len = plan.lane_len[x];
+        const int len = plan.len;
+        const int C = plan.C;
         for (int k = (int)blockIdx.x >> 3; k < len;) {
-            const int i = 8 * k + x;
             PlanItem it = {0, 0, 0, 0, 0};
-            const bool has = plan_item<HP>(a, plan, i, it);
+            const bool has = plan_item<HP>(a, plan, k, it);
             // Plan values come from LDS: make them scalar for the addressing that follows.
-            const int p = __builtin_amdgcn_readfirstlane(it.p);
+            const int b = __builtin_amdgcn_readfirstlane(it.b);
             const int hp = __builtin_amdgcn_readfirstlane(it.hp);
             const int rg = __builtin_amdgcn_readfirstlane(it.rg);
             const int chunk = __builtin_amdgcn_readfirstlane(it.chunk);
             const int slot = __builtin_amdgcn_readfirstlane(it.slot);
             SeqInfo si;
-            si.b = __builtin_amdgcn_readfirstlane(plan.b[p]);
+            si.b = b;
             si.kvh = hp * HP + hw;
-            si.ctx = __builtin_amdgcn_readfirstlane(plan.ctx[p]);
-            si.q0 = __builtin_amdgcn_readfirstlane(plan.q0[p]);
-            si.q_len = __builtin_amdgcn_readfirstlane(plan.qlen[p]);
+            si.ctx = __builtin_amdgcn_readfirstlane(plan.ctx[b]);
+            si.q0 = __builtin_amdgcn_readfirstlane(plan.q0[b]);
+            si.q_len = __builtin_amdgcn_readfirstlane(plan.qlen[b]);
             si.rows = si.q_len * a.group;
             si.nblk = (si.ctx + a.bs - 1) / a.bs;
             si.ok = true;
-            const int ch = __builtin_amdgcn_readfirstlane(plan.ch[p]);
-            const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[p]);
-            const int blk_begin = chunk * ch;
-            const int blk_end = min(si.nblk, blk_begin + ch);
-            if (__builtin_amdgcn_readfirstlane(has ? 1 : 0))  // a full lane has no empty position
+            const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[b]);
+            const int blk_begin = chunk * C;
+            const int blk_end = min(si.nblk, blk_begin + C);
+            if (__builtin_amdgcn_readfirstlane(has ? 1 : 0))
                 item(si, si.b * U + hp, rg, blk_begin, blk_end, nsplit, (size_t)slot * HP * RW, (size_t)RW);
             // Claimed after the item: an atomic issued before it would sit at the head of the
             // in-order load counter and hold up the item's first waits (measured: 437 -> 474 us

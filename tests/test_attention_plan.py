@@ -64,8 +64,8 @@ def test_slot_bound_holds_over_random_batches(chunk_div, num_cus):
         rw = _rows_per_group(group * max(1, int(ql.max())))
         r = _ceil(ql.astype(np.int64) * group, rw)
         assert info["items"] == int(np.sum((hkv // hp) * splits.astype(np.int64) * r))
-        # Splits: one for a sequence within the chunk; otherwise even chunks that cover the
-        # sequence with no empty split; none for a sequence without rows.
+        # Splits: one for a sequence within the chunk; otherwise chunks of C blocks from the start,
+        # the last one shorter and not empty; none for a sequence without rows.
         nb = _ceil(ctx, 16)
         C = info["chunk_blocks"]
         assert C % 2 == 0 and C >= 16
@@ -75,8 +75,7 @@ def test_slot_bound_holds_over_random_batches(chunk_div, num_cus):
             elif nb[b] <= C:
                 assert splits[b] == 1
             else:
-                ch = _ceil(nb[b], splits[b])
-                assert splits[b] >= _ceil(nb[b], C) and (splits[b] - 1) * ch < nb[b] <= splits[b] * (ch + 1)
+                assert splits[b] == _ceil(nb[b], C) and (splits[b] - 1) * C < nb[b] <= splits[b] * C
     assert worst > 0.0
 
 
