@@ -457,6 +457,19 @@ __device__ __forceinline__ int snake_nth(int A, int x, int i) {
     return 8 * r + snake_pos(r, x);
 }
 
+// Inclusive prefix sum over a wave's 64 lanes: row_shr 1, 2, 4, 8 within each row of 16 lanes,
+// then row_bcast 15 (row 0's total into row 1, row 2's into row 3) and row_bcast 31 (the first
+// two rows' total into rows 2 and 3). Lanes a DPP source does not reach add 0.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+    return x;
+}
+
 // Exclusive prefix sums of V values per thread over the workgroup's threads; total[] gets the
 // sums. `red` is LDS scratch.
 template <int V>
@@ -464,15 +477,7 @@ __device__ __forceinline__ void block_scan_excl(int (&v)[V], int (&total)[V], in
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int incl[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-        int x = v[j];
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(x, o, 64);
-            if (lane >= o) x += y;
-        }
-        incl[j] = x;
-    }
+    for (int j = 0; j < V; ++j) incl[j] = wave_incl_sum(v[j]);
     if (lane == 63) {
 #pragma unroll
         for (int j = 0; j < V; ++j) red[wave][j] = incl[j];
@@ -526,11 +531,12 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
     const int wave = t >> 6;
     const int x = (int)blockIdx.x & 7;  // this workgroup's lane
     const int U = a.Hkv / HP;
-    int ctx[S], q0[S], qlen[S], r[S], nb[S];
+    // Context lengths and rows, read coalesced (thread t: sequences t, t + kThreads, ..) into LDS.
+    long long w = 0;
+    int mx = 0;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-        const int sq = S * t + j;
-        ctx[j] = q0[j] = qlen[j] = r[j] = nb[j] = 0;
+        const int sq = t + j * kThreads;
         if (sq < a.B) {
             const int64_t c = a.ctx_lens[sq];
             int s0 = sq, s1 = sq + 1;
@@ -547,22 +553,17 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
                 ok = false;
                 if (blockIdx.x == 0) latch_error(a.err, ERR_Q_LAYOUT);
             }
-            if (ok) {
-                ctx[j] = (int)c;
-                q0[j] = s0;
-                qlen[j] = s1 - s0;
-                r[j] = (qlen[j] * a.group + RW - 1) / RW;
-                nb[j] = (ctx[j] + a.bs - 1) / a.bs;
-            }
+            const int ctx = ok ? (int)c : 0;
+            const int ql = ok ? s1 - s0 : 0;
+            const int r = (ql * a.group + RW - 1) / RW;
+            const int nb = (ctx + a.bs - 1) / a.bs;
+            P.ctx[sq] = ctx;
+            P.q0[sq] = ok ? s0 : 0;
+            P.qlen[sq] = ql;
+            P.r[sq] = r;
+            w += (long long)U * r * nb;  // total work and the longest sequence that has rows
+            mx = max(mx, r > 0 ? nb : 0);
         }
-    }
-    // Total work and the longest sequence that has rows.
-    long long w = 0;
-    int mx = 0;
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-        w += (long long)U * r[j] * nb[j];
-        mx = max(mx, r[j] > 0 ? nb[j] : 0);
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -582,21 +583,25 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
         maxnb = max(maxnb, P.red[i][0]);
     }
     const int C = plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk);
-    // Per sequence: splits, phase-A item groups, partial-state slots and the combine pass's work
-    // units (kCombineRows-row chunks of every kv head of a split sequence), in sequence order.
-    int ns[S], v3[S][3], t3[3];
+    // Thread t owns sequences S t .. S t + S - 1 from here on. Per sequence: splits, phase-A item
+    // groups, partial-state slots and the combine pass's work units (kCombineRows-row chunks of
+    // every kv head of a split sequence), prefix-summed in sequence order.
+    int r[S], ns[S], v3[S][3], t3[3];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int sq = S * t + j;
+        r[j] = sq < a.B ? P.r[sq] : 0;
+        const int nb = sq < a.B ? (P.ctx[sq] + a.bs - 1) / a.bs : 0;
+        const int ql = sq < a.B ? P.qlen[sq] : 0;
         int n, ch;
-        plan_split(nb[j], C, n, ch);
+        plan_split(nb, C, n, ch);
         ns[j] = r[j] > 0 ? n : 0;
-        const int last = nb[j] - (n - 1) * C;  // blocks of the last chunk
+        const int last = nb - (n - 1) * C;  // blocks of the last chunk
         // Unique per sequence (a sequence without rows sorts last); padding ranks below all.
         P.key[sq] = sq < a.B ? ((uint32_t)(r[j] > 0 ? last : 0) << 16) | (uint32_t)(0xffff - sq) : 0u;
         v3[j][0] = r[j] > 0 ? (n - 1) * U : 0;
         v3[j][1] = ns[j] * U * r[j];
-        v3[j][2] = (ns[j] > 1) ? a.Hkv * ((qlen[j] * a.group + kCombineRows - 1) / kCombineRows) : 0;
+        v3[j][2] = ns[j] > 1 ? a.Hkv * ((ql * a.group + kCombineRows - 1) / kCombineRows) : 0;
     }
     scan_owned<S, 3>(v3, t3, P.red);  // its barriers also publish P.key
     if (t3[1] > a.plan_slots) {
@@ -614,23 +619,13 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
         return;
     }
     const int GA = t3[0];
-    // This lane's phase-A items per sequence (row groups consecutive).
-    int cA[S][1], tA[1];
-#pragma unroll
-    for (int j = 0; j < S; ++j) cA[j][0] = snake_count(v3[j][0], r[j] > 0 ? (ns[j] - 1) * U : 0, x) * r[j];
-    scan_owned<S, 1>(cA, tA, P.red);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         const int sq = S * t + j;
         if (sq < a.B) {
             P.ns[sq] = ns[j];
-            P.r[sq] = r[j];
-            P.ctx[sq] = ctx[j];
-            P.q0[sq] = q0[j];
-            P.qlen[sq] = qlen[j];
             P.gA[sq] = v3[j][0];
             P.slot0[sq] = v3[j][1];
-            P.lane0A[sq] = cA[j][0];
             if (blockIdx.x == 0) {
                 a.plan_seq[sq] = make_int4(ns[j], r[j], v3[j][1], 0);
                 a.plan_cw[sq] = v3[j][2];
@@ -655,22 +650,27 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
         P.bB[rank] = sq;
     }
     __syncthreads();
-    // This lane's phase-B items per position: U item groups each, groups GA + U p ...
-    int cB[S][1], tB[1];
+    // This lane's items: phase A per sequence (its groups from gA on), phase B per position (U
+    // groups each, from GA + U p on); the row groups of a group are consecutive.
+    int c2[S][2], t2[2];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-        const int pos = S * t + j;
-        cB[j][0] = pos < a.B ? snake_count(GA + U * pos, U, x) * P.r[P.bB[pos]] : 0;
+        const int i = S * t + j;
+        c2[j][0] = snake_count(v3[j][0], r[j] > 0 ? (ns[j] - 1) * U : 0, x) * r[j];
+        c2[j][1] = i < a.B ? snake_count(GA + U * i, U, x) * P.r[P.bB[i]] : 0;
     }
-    scan_owned<S, 1>(cB, tB, P.red);
+    scan_owned<S, 2>(c2, t2, P.red);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-        const int pos = S * t + j;
-        if (pos < a.B) P.lane0B[pos] = tA[0] + cB[j][0];
+        const int i = S * t + j;
+        if (i < a.B) {
+            P.lane0A[i] = c2[j][0];
+            P.lane0B[i] = t2[0] + c2[j][1];
+        }
     }
     if (t == 0) {
-        P.lenA = tA[0];
-        P.len = tA[0] + tB[0];
+        P.lenA = t2[0];
+        P.len = t2[0] + t2[1];
         P.GA = GA;
         P.C = C;
     }
