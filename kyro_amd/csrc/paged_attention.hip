@@ -17,10 +17,11 @@
 //
 // Three kernels share that frame:
 //  * attn_mfma_kernel (bf16, D = 128, block_size 16): scores S^T = K Q^T and O^T = V^T P^T on
-//    v_mfma_f32_16x16x32_bf16. K and V are loaded straight from HBM into the MFMA operand
-//    layouts with 128-bit loads — K as 16 token rows x 64 contiguous bytes per instruction, V as
-//    4 full 256-byte token rows per instruction — so no LDS staging is needed; V is transposed in
-//    registers with v_perm_b32. The softmax'd S^T fragment is already the P^T operand of the PV
+//    v_mfma_f32_16x16x32_bf16. V is loaded with 128-bit loads of 4 full 256-byte token rows per
+//    instruction and transposed in registers with v_perm_b32. K is loaded either straight into
+//    the MFMA operand layout (16 token rows x 64 contiguous bytes per instruction: the two-tile
+//    grid kernel of uniform batches) or by whole token rows straight into a per-wave LDS tile
+//    (buffer_load ... lds) and read from there in operand layout (the other instances). The softmax'd S^T fragment is already the P^T operand of the PV
 //    product, and the output column of O^T is the query row, so the per-row rescale stays in the
 //    lane that owns the row's softmax state.
 //  * attn_mfma_f32_kernel (f32, D = 128, block_size 16): the same products on
@@ -288,26 +289,35 @@ constexpr int kMfmaBS = 16;
 // zero-initialised when the code object loads, and nothing writes it).
 __device__ uint16_t kZeroSlab[kMfmaBS * kMfmaD];
 
-// K and V of one pair of 16-token blocks, already in MFMA operand layout (K) or ready for the
-// in-register transpose (V). 64 VGPRs.
+// K and V of one pair of 16-token blocks, in MFMA operand layout (K: loaded so under kKDirect,
+// read from the wave's LDS tile just before the products under kKDma) or ready for the
+// in-register transpose (V). 64 VGPRs (32 live across a prefetch under kKDma).
 struct KVPair {
     bf16x8 k[2][4];  // [block][head-dim step]: token r, head dims 32 s + 8 g .. + 7
     uint4 v[2][4];   // [block][e]: token 4 g + e, head dims 8 r .. 8 r + 7
 };
 
-#ifndef KYRO_ATTN_K_LINES
-#define KYRO_ATTN_K_LINES 1
+// How K reaches the MFMA A-operand layout:
+//  * kKDirect: loaded straight into that layout, 16 token rows x 64 bytes per instruction (half
+//    lines), which holds one workgroup to ~28 GB/s against ~66 GB/s for whole lines;
+//  * kKDma: whole 256-byte token rows per 16 lanes, loaded straight into a per-wave LDS tile
+//    (buffer_load ... lds: lane l's 16 bytes land at tile + 16 l) with the source chunk of each
+//    lane XOR-swizzled so that the MFMA-layout reads hit distinct banks; one tile per register
+//    buffer, so the next pair's K lands while this pair's is read.
+// Row loads pay where a workgroup's own rate sets the pace: one 16-row tile (MHA and decode
+// shapes) and the balanced schedule's uneven batches. On a uniform batch with two tiles (the
+// Llama-3-8B step on the grid) every CU streams at its share of HBM anyway, and the LDS pass
+// cost 167.0 -> 169.8 us there, so that kernel loads K directly. KYRO_ATTN_K_GRID2 is the mode
+// of the two-tile grid kernel, KYRO_ATTN_K_OTHER that of the others.
+enum { kKDirect = 0, kKDma = 1 };
+#ifndef KYRO_ATTN_K_GRID2
+#define KYRO_ATTN_K_GRID2 0
 #endif
-// K loaded by whole token rows (as V is), then staged through LDS into MFMA layout, or loaded
-// directly in MFMA layout. The direct form reads 16 rows x 64 bytes per instruction (half lines),
-// which holds one workgroup to ~28 GB/s against ~66 GB/s for whole lines. Row loads pay where a
-// workgroup's own rate sets the pace: one 16-row tile (MHA and decode shapes: 68.3 -> 62.9 us on
-// the MHA Llama-2-7B batch) and the balanced schedule's uneven batches (skewed prefix 187 -> 177
-// us). On a uniform batch with two tiles (the Llama-3-8B step on the grid) every CU streams at
-// its share of HBM anyway, and the staging cost 168 -> 170.6 us, so that kernel loads K directly.
-// KYRO_ATTN_K_LINES: 0 never, 1 as above, 2 always.
+#ifndef KYRO_ATTN_K_OTHER
+#define KYRO_ATTN_K_OTHER 1
+#endif
 template <int NTW, bool PLAN>
-constexpr bool kKLinesFor = KYRO_ATTN_K_LINES == 2 || (KYRO_ATTN_K_LINES == 1 && (NTW == 1 || PLAN));
+constexpr int kKModeFor = (NTW == 1 || PLAN) ? KYRO_ATTN_K_OTHER : KYRO_ATTN_K_GRID2;
 
 // Issues the 16 loads of one block pair. A negative block id reads as zeros (never dereferenced).
 // Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
@@ -318,8 +328,8 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
 // addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
 // a prefetched pair in flight. POL is the loads' cache policy (kLoadCached or kLoadStream).
-template <int POL, bool KL>
-__device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict__ kp,
+template <int POL, int KM>
+__device__ __forceinline__ void load_pair(KVPair& p, uint4* __restrict__ kt, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t block_stride, size_t kv_off, int r, int g) {
     constexpr int kSlabBytes = kMfmaBS * kMfmaD * 2;
@@ -339,12 +349,16 @@ __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict_
     // V loads may still be in flight.
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
-        if constexpr (KL) {
-            // K in V's layout (whole 256-byte token rows per 16 lanes); stage_k puts it in MFMA
-            // layout through LDS.
+        if constexpr (KM == kKDma) {
+            // Instruction e: tokens 4 e .. 4 e + 3, lane (r, g) -> LDS slot r of token t = 4 e + g,
+            // which holds the token's 16-byte chunk r ^ t.
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                p.k[bi][e] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], voff, 256 * e, POL));
+            for (int e = 0; e < 4; ++e) {
+                const int t = 4 * e + g;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    kr[bi], (__attribute__((address_space(3))) void*)(kt + bi * 256 + e * 64), 16,
+                    t * 256 + 16 * (r ^ t), 0, 0, POL);
+            }
         } else {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
@@ -358,22 +372,14 @@ __device__ __forceinline__ void load_pair(KVPair& p, const uint16_t* __restrict_
             p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 256 * e, POL));
 }
 
-// One wave's LDS tile for staging the K of one block pair: [block][token][16-byte chunk], the
-// chunk index XOR-ed with the token so that both the row-wise writes and the MFMA-layout reads
-// (16 tokens, one chunk each) fall in distinct banks.
+// One wave's LDS tile for the K of one block pair: [block][token][16-byte chunk], the chunk
+// index XOR-ed with the token so that the MFMA-layout reads (16 tokens, one chunk each) fall in
+// distinct banks.
 constexpr int kKStageChunks = 2 * kMfmaBS * (kMfmaD / 8);  // uint4 per wave (8 KiB)
 
-// K of a pair from the load layout (lane (r, g), register e: token 4 g + e, chunk r) to the MFMA
-// A-operand layout (register s: token r, chunk 4 s + g). The tile belongs to the calling wave
-// alone, and a wave's LDS operations complete in order, so no barrier is needed.
-__device__ __forceinline__ void stage_k(KVPair& p, uint4* __restrict__ tile, int r, int g) {
-#pragma unroll
-    for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 4 * g + e;
-            tile[bi * 256 + t * 16 + (r ^ t)] = __builtin_bit_cast(uint4, p.k[bi][e]);
-        }
+// K of a pair in MFMA A-operand layout (register s: token r, chunk 4 s + g) from a swizzled tile
+// (token t's chunk c at slot c ^ t). The tile belongs to the calling wave alone.
+__device__ __forceinline__ void read_k_tile(KVPair& p, const uint4* __restrict__ tile, int r, int g) {
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
@@ -740,9 +746,9 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 // mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
 // head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
 // workspace rows pb0 + h * pbstep + n for head h of the group.
-template <int NTW, int HP, int POL, bool KL>
+template <int NTW, int HP, int POL, int KM>
 __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
-                                          uint4* kst, const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
+                                          uint4* kstA, uint4* kstB, const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
                                           int nsplit, size_t pb0, size_t pbstep) {
     constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
@@ -800,13 +806,16 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
         }
 
         // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
-        uint4* const ktile = KL ? kst + wave * kKStageChunks : kst;
-        auto compute = [&](KVPair& kv, int pb, int blk0, int blk1) {
-            if constexpr (KL) {
-                // Keep the next pair's loads (issued just before) ahead of the staging, so that
-                // they are in flight while this pair's K waits.
+        // The wave's K tiles under kKDma, one per register buffer.
+        uint4* const ktA = KM == kKDma ? kstA + wave * kKStageChunks : kstA;
+        uint4* const ktB = KM == kKDma ? kstB + wave * kKStageChunks : kstB;
+        auto compute = [&](KVPair& kv, const uint4* kt, int pb, int blk0, int blk1) {
+            if constexpr (KM == kKDma) {
+                // Keep the next pair's loads (issued just before) ahead of this pair's tile
+                // reads, which then wait for this pair's K only; without the barrier the
+                // compiler hoists the reads above the loads and the prefetch is lost.
                 __builtin_amdgcn_sched_barrier(0);
-                stage_k(kv, ktile, r, g);
+                read_k_tile(kv, kt, r, g);
             }
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
             f32x4 S[2][NTW];
@@ -937,15 +946,15 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 // wait that precedes the computation of the pair before it.
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<POL, KL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<POL, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<POL, KL>(bufB, kp, vp, b0, b1, block_stride, kv_off, r, g);
-                    compute(bufA, pb0 + j * step, a0, a1);
+                    load_pair<POL, KM>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    compute(bufA, ktA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<POL, KL>(bufA, kp, vp, a0, a1, block_stride, kv_off, r, g);
-                    compute(bufB, pb0 + j * step, b0, b1);
+                    load_pair<POL, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    compute(bufB, ktB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
             }
@@ -1362,11 +1371,14 @@ template <int NTW, int HP, int POL, bool PLAN>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     __shared__ Frame<NTW * 16, kMfmaD> frame[HP];
     __shared__ int s_blk[kMaxChunkBlocks];
-    constexpr bool KL = kKLinesFor<NTW, PLAN>;
-    __shared__ uint4 s_kst[KL ? kWaves * kKStageChunks : 1];
+    constexpr int KM = kKModeFor<NTW, PLAN>;
+    // Two separate arrays, so that the compiler's wait for one tile's loads does not also wait
+    // for the other's (it tells LDS DMA destinations apart by the object written).
+    __shared__ uint4 s_kstA[KM == kKDma ? kWaves * kKStageChunks : 1];
+    __shared__ uint4 s_kstB[KM == kKDma ? kWaves * kKStageChunks : 1];
     mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
                                         size_t pbs) {
-        mfma_item<NTW, HP, POL, KL>(a, frame, s_blk, s_kst, si, ug, rg, bb, be, ns, pb0, pbs);
+        mfma_item<NTW, HP, POL, KM>(a, frame, s_blk, s_kstA, s_kstB, si, ug, rg, bb, be, ns, pb0, pbs);
     });
 }
 
