@@ -125,7 +125,14 @@ constexpr int kMfmaMaxPairsPerWave = 128;
 
 // Query rows one attention workgroup covers.
 constexpr int kVectorRowsPerGroup = 8;
-inline int mfma_rows_per_group(int rows) { return rows <= 16 ? 16 : 32; }
+// MFMA kernels: one 16-row tile, two (32 rows), or for bf16 units of more than 32 rows four
+// (kMfmaManyRows: one kv head per workgroup, Q read from LDS, only the unit's tiles computed),
+// so that a unit of up to 64 rows streams its K/V once instead of once per 32-row group. (Five
+// tiles need more than the 512 registers a wave can hold.)
+constexpr int kMfmaManyRows = 64;
+__host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16) {
+    return rows <= 16 ? 16 : (rows <= 32 || !bf16) ? 32 : kMfmaManyRows;
+}
 
 hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
 

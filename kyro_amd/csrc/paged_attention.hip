@@ -21,7 +21,10 @@
 //    instruction and transposed in registers with v_perm_b32. K is loaded either straight into
 //    the MFMA operand layout (16 token rows x 64 contiguous bytes per instruction: the two-tile
 //    grid kernel of uniform batches) or by whole token rows straight into a per-wave LDS tile
-//    (buffer_load ... lds) and read from there in operand layout (the other instances). The softmax'd S^T fragment is already the P^T operand of the PV
+//    (buffer_load ... lds) and read from there in operand layout (the other instances). A wave
+//    holds one or two 16-row tiles with Q in registers; bf16 units of 33 to 64 rows take a
+//    four-tile instance instead (one kv head per workgroup, Q staged in LDS, only the tiles
+//    that hold the unit's rows computed), so that such a unit streams its K/V once. The softmax'd S^T fragment is already the P^T operand of the PV
 //    product, and the output column of O^T is the query row, so the per-row rescale stays in the
 //    lane that owns the row's softmax state.
 //  * attn_mfma_f32_kernel (f32, D = 128, block_size 16): the same products on
@@ -317,7 +320,7 @@ enum { kKDirect = 0, kKDma = 1 };
 #define KYRO_ATTN_K_OTHER 1
 #endif
 template <int NTW, bool PLAN>
-constexpr int kKModeFor = (NTW == 1 || PLAN) ? KYRO_ATTN_K_OTHER : KYRO_ATTN_K_GRID2;
+constexpr int kKModeFor = NTW > 2 ? kKDma : (NTW == 1 || PLAN) ? KYRO_ATTN_K_OTHER : KYRO_ATTN_K_GRID2;
 
 // Issues the 16 loads of one block pair. A negative block id reads as zeros (never dereferenced).
 // Word 3 of a raw buffer resource on gfx9-family parts (32-bit data format, no swizzle).
@@ -376,6 +379,9 @@ __device__ __forceinline__ void load_pair(KVPair& p, uint4* __restrict__ kt, con
 // index XOR-ed with the token so that the MFMA-layout reads (16 tokens, one chunk each) fall in
 // distinct banks.
 constexpr int kKStageChunks = 2 * kMfmaBS * (kMfmaD / 8);  // uint4 per wave (8 KiB)
+// Staged Q rows of the many-tile kernels: 16 uint4 per row plus one of padding, so that the 16
+// rows one MFMA operand read touches start 4 banks apart.
+constexpr int kQStride = kMfmaD / 8 + 1;
 
 // K of a pair in MFMA A-operand layout (register s: token r, chunk 4 s + g) from a swizzled tile
 // (token t's chunk c at slot c ^ t). The tile belongs to the calling wave alone.
@@ -748,11 +754,15 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 // workspace rows pb0 + h * pbstep + n for head h of the group.
 template <int NTW, int HP, int POL, int KM>
 __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
-                                          uint4* kstA, uint4* kstB, const SeqInfo& si, int ug, int rg, int blk_begin, int blk_end,
-                                          int nsplit, size_t pb0, size_t pbstep) {
+                                          uint4* kstA, uint4* kstB, uint4* sq, const SeqInfo& si, int ug, int rg,
+                                          int blk_begin, int blk_end, int nsplit, size_t pb0, size_t pbstep) {
     constexpr int D = kMfmaD;
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
     constexpr int WPH = kWaves / HP;  // waves per kv head
+    // More than two tiles: Q is read from LDS per tile (sq, staged once per item) and only the
+    // tiles that hold rows of this unit are computed.
+    constexpr bool QL = NTW > 2;
+    static_assert(!QL || (HP == 1 && KM == kKDma), "the many-tile form needs one kv head and K in LDS");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int hw = wave / WPH;  // this wave's kv head within the group
     const int wp = wave % WPH;  // and its place among that head's waves
@@ -770,27 +780,43 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
     const float c = a.scale_log2;
     // Tokens below full_vis are visible to every query row of the sequence.
     const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
+    // Row tiles of this row group that hold rows of the unit (uniform).
+    const int ntile = QL ? min(NTW, (min(RW, si.rows - row0) + 15) / 16) : NTW;
 
-    stage_block_ids(a, si, blk_begin, blk_end, s_blk);
+    if constexpr (QL) {
+        // The row group's Q rows, one padded 272-byte row each (rows past the unit are zero).
+        // The previous item's readers are past the frame merge's barriers.
+        for (int idx = threadIdx.x; idx < RW * 16; idx += kThreads) {
+            const int n = idx >> 4, ch = idx & 15;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (row0 + n < si.rows) v = load16(qp + out_row(a, si, row0 + n) * D + 8 * ch);
+            sq[n * kQStride + ch] = v;
+        }
+    }
+    stage_block_ids(a, si, blk_begin, blk_end, s_blk);  // its barrier also publishes sq
 
     {
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
         // Padding rows (n >= rows) get Q = 0 and full visibility; they are never stored.
-        bf16x8 qB[NTW][4];
+        bf16x8 qB[QL ? 1 : NTW][4];
         int vis[NTW];
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
             const int n = row0 + nt * 16 + r;
             if (n < si.rows) {
                 const int j = n / a.group;
-                const size_t qrow = out_row(a, si, n);
+                if constexpr (!QL) {
+                    const size_t qrow = out_row(a, si, n);
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    qB[nt][s] = __builtin_bit_cast(bf16x8, load16(qp + qrow * D + 32 * s + 8 * g));
+                    for (int s = 0; s < 4; ++s)
+                        qB[nt][s] = __builtin_bit_cast(bf16x8, load16(qp + qrow * D + 32 * s + 8 * g));
+                }
                 vis[nt] = a.causal ? si.ctx - si.q_len + j + 1 : si.ctx;
             } else {
+                if constexpr (!QL) {
 #pragma unroll
-                for (int s = 0; s < 4; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+                    for (int s = 0; s < 4; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+                }
                 vis[nt] = si.ctx;
             }
         }
@@ -805,6 +831,67 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             for (int dt = 0; dt < 8; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
+        // Online softmax of row tile nt over one pair (S^T fragments s0, s1 of its two blocks):
+        // updates the tile's running max and sum, rescales its accumulator when the max rose, and
+        // returns P^T as the B operand of the PV product.
+        auto softmax_tile = [&](int nt, const f32x4& s0, const f32x4& s1, bool full, int pb, int blk0,
+                                int blk1) -> bf16x8 {
+            float sv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sv[e] = s0[e];
+                sv[4 + e] = s1[e];
+            }
+            if (!full) {
+#pragma unroll
+                for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = (pb + bi) * kMfmaBS + 4 * g + e;
+                        const bool ok = (bi ? blk1 : blk0) >= 0 && t < vis[nt];
+                        if (!ok) sv[bi * 4 + e] = kNegInf;
+                    }
+            }
+            float mx = sv[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+            mx = fmaxf(mx, shfl_xor_f(mx, 16));
+            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            const float m_new = fmaxf(m[nt], mx * c);
+            const float mref = (m_new == kNegInf) ? 0.f : m_new;
+            const float alpha = fast_exp2(m[nt] - mref);
+            float ps = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sv[i] = fast_exp2(__builtin_fmaf(sv[i], c, -mref));
+                ps += sv[i];
+            }
+            lsum[nt] = lsum[nt] * alpha + ps;
+            if (__any(m_new > m[nt] && m[nt] != kNegInf)) {
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) O[dt][nt] *= alpha;
+            }
+            m[nt] = m_new;
+            uint4 pw;
+            pw.x = pack_bf16x2(sv[0], sv[1]);
+            pw.y = pack_bf16x2(sv[2], sv[3]);
+            pw.z = pack_bf16x2(sv[4], sv[5]);
+            pw.w = pack_bf16x2(sv[6], sv[7]);
+            return __builtin_bit_cast(bf16x8, pw);
+        };
+        // V^T operand of d-tile dt: lane row r <-> head dim 8 r + dt, k-slots 8 g .. 8 g + 7 <->
+        // tokens 4 g .. 4 g + 3 of block 0 then of block 1.
+        auto v_operand = [&](const KVPair& kv, int dt) -> bf16x8 {
+            const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+            const int w = dt >> 1;
+            uint4 av;
+            av.x = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][1])[w], ((const uint32_t*)&kv.v[0][0])[w], sel);
+            av.y = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][3])[w], ((const uint32_t*)&kv.v[0][2])[w], sel);
+            av.z = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][1])[w], ((const uint32_t*)&kv.v[1][0])[w], sel);
+            av.w = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][3])[w], ((const uint32_t*)&kv.v[1][2])[w], sel);
+            return __builtin_bit_cast(bf16x8, av);
+        };
+
         // One pair of blocks = 32 tokens = one K-step of the PV MFMA.
         // The wave's K tiles under kKDma, one per register buffer.
         uint4* const ktA = KM == kKDma ? kstA + wave * kKStageChunks : kstA;
@@ -816,6 +903,41 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 // compiler hoists the reads above the loads and the prefetch is lost.
                 __builtin_amdgcn_sched_barrier(0);
                 read_k_tile(kv, kt, r, g);
+            }
+            const bool full = blk0 >= 0 && blk1 >= 0 && (pb + 2) * kMfmaBS <= full_vis;
+            if constexpr (QL) {
+                if (!full) {  // as below: V of tokens past the context is zeroed
+#pragma unroll
+                    for (int bi = 0; bi < 2; ++bi)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx) kv.v[bi][e] = make_uint4(0, 0, 0, 0);
+                }
+#pragma unroll
+                for (int nt = 0; nt < NTW; ++nt) {
+                    if (nt < ntile) {  // uniform: tiles past the unit's rows are skipped
+                        bf16x8 q[4];
+#pragma unroll
+                        for (int s = 0; s < 4; ++s)
+                            q[s] = __builtin_bit_cast(bf16x8, sq[(nt * 16 + r) * kQStride + 4 * s + g]);
+                        f32x4 S2[2];
+#pragma unroll
+                        for (int bi = 0; bi < 2; ++bi) {
+                            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int s = 0; s < 4; ++s)
+                                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv.k[bi][s], q[s], acc, 0, 0, 0);
+                            S2[bi] = acc;
+                        }
+                        const bf16x8 pB = softmax_tile(nt, S2[0], S2[1], full, pb, blk0, blk1);
+                        // The V^T operands are rebuilt per tile (32 v_perm): holding all eight
+                        // across the tiles costs 32 registers the accumulators need.
+#pragma unroll
+                        for (int dt = 0; dt < 8; ++dt)
+                            O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand(kv, dt), pB, O[dt][nt], 0, 0, 0);
+                    }
+                }
+                return;
             }
             // S^T tiles: rows = 16 tokens of block bi, columns = 16 query rows of tile nt.
             f32x4 S[2][NTW];
@@ -829,7 +951,6 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv.k[bi][s], qB[nt][s], acc, 0, 0, 0);
                     S[bi][nt] = acc;
                 }
-            const bool full = blk0 >= 0 && blk1 >= 0 && (pb + 2) * kMfmaBS <= full_vis;
             if (!full) {
                 // Tokens past the context (the unused tail of the last block) get V = 0, so that
                 // whatever those cache slots hold cannot reach O through a zero probability.
@@ -841,62 +962,12 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             }
             bf16x8 pB[NTW];
 #pragma unroll
-            for (int nt = 0; nt < NTW; ++nt) {
-                float sv[8];
-#pragma unroll
-                for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) sv[bi * 4 + e] = S[bi][nt][e];
-                if (!full) {
-#pragma unroll
-                    for (int bi = 0; bi < 2; ++bi)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int t = (pb + bi) * kMfmaBS + 4 * g + e;
-                            const bool ok = (bi ? blk1 : blk0) >= 0 && t < vis[nt];
-                            if (!ok) sv[bi * 4 + e] = kNegInf;
-                        }
-                }
-                float mx = sv[0];
-#pragma unroll
-                for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-                mx = fmaxf(mx, shfl_xor_f(mx, 16));
-                mx = fmaxf(mx, shfl_xor_f(mx, 32));
-                const float m_new = fmaxf(m[nt], mx * c);
-                const float mref = (m_new == kNegInf) ? 0.f : m_new;
-                const float alpha = fast_exp2(m[nt] - mref);
-                float ps = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    sv[i] = fast_exp2(__builtin_fmaf(sv[i], c, -mref));
-                    ps += sv[i];
-                }
-                lsum[nt] = lsum[nt] * alpha + ps;
-                if (__any(m_new > m[nt] && m[nt] != kNegInf)) {
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) O[dt][nt] *= alpha;
-                }
-                m[nt] = m_new;
-                uint4 pw;
-                pw.x = pack_bf16x2(sv[0], sv[1]);
-                pw.y = pack_bf16x2(sv[2], sv[3]);
-                pw.z = pack_bf16x2(sv[4], sv[5]);
-                pw.w = pack_bf16x2(sv[6], sv[7]);
-                pB[nt] = __builtin_bit_cast(bf16x8, pw);
-            }
+            for (int nt = 0; nt < NTW; ++nt) pB[nt] = softmax_tile(nt, S[0][nt], S[1][nt], full, pb, blk0, blk1);
 
-            // O^T += V^T P^T. A operand of d-tile dt: lane row r <-> head dim 8 r + dt, k-slots
-            // 8 g .. 8 g + 7 <-> tokens 4 g .. 4 g + 3 of block 0 then of block 1.
+            // O^T += V^T P^T.
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
-                const int w = dt >> 1;
-                uint4 av;
-                av.x = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][1])[w], ((const uint32_t*)&kv.v[0][0])[w], sel);
-                av.y = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][3])[w], ((const uint32_t*)&kv.v[0][2])[w], sel);
-                av.z = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][1])[w], ((const uint32_t*)&kv.v[1][0])[w], sel);
-                av.w = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][3])[w], ((const uint32_t*)&kv.v[1][2])[w], sel);
-                const bf16x8 A = __builtin_bit_cast(bf16x8, av);
+                const bf16x8 A = v_operand(kv, dt);
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt)
                     O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, pB[nt], O[dt][nt], 0, 0, 0);
@@ -960,6 +1031,13 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             }
         }
 
+        if constexpr (QL) {
+            // The frame shares LDS with the K tiles: every wave's last (dropped) prefetch must
+            // have landed, and every wave must be done reading its tiles, before it is written.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
+
         // Row sums: each lane summed its own 8 tokens per pair; fold the four 16-lane groups.
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
@@ -993,6 +1071,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             if (wp == w) {
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
+                    if (QL && nt >= ntile) continue;  // rows past the unit: never stored
                     float* dst = &fr.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 32 * g];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
@@ -1366,19 +1445,39 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
     }
 }
 
+// The LDS merge frames of a workgroup's heads; the many-tile kernel keeps its one frame in its
+// first K-tile array instead.
+template <int NTW, int HP, bool QL>
+struct FrameLds {
+    Frame<NTW * 16, kMfmaD> f[HP];
+};
+template <int NTW, int HP>
+struct FrameLds<NTW, HP, true> {};
+
 // bf16 caches.
 template <int NTW, int HP, int POL, bool PLAN>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
-    __shared__ Frame<NTW * 16, kMfmaD> frame[HP];
+    using Fr = Frame<NTW * 16, kMfmaD>;
+    constexpr bool QL = NTW > 2;
+    __shared__ FrameLds<NTW, HP, QL> s_fr;
     __shared__ int s_blk[kMaxChunkBlocks];
     constexpr int KM = kKModeFor<NTW, PLAN>;
     // Two separate arrays, so that the compiler's wait for one tile's loads does not also wait
-    // for the other's (it tells LDS DMA destinations apart by the object written).
-    __shared__ uint4 s_kstA[KM == kKDma ? kWaves * kKStageChunks : 1];
-    __shared__ uint4 s_kstB[KM == kKDma ? kWaves * kKStageChunks : 1];
+    // for the other's (it tells LDS DMA destinations apart by the object written). The
+    // many-tile kernel keeps its merge frame in the first (the frame is used only after the
+    // streaming, behind a wait for every tile load and a barrier).
+    constexpr int kTileU4 = KM == kKDma ? kWaves * kKStageChunks : 1;
+    constexpr int kFrameU4 = (int)((sizeof(Fr) * HP + 15) / 16);
+    __shared__ uint4 s_kstA[QL && kFrameU4 > kTileU4 ? kFrameU4 : kTileU4];
+    __shared__ uint4 s_kstB[kTileU4];
+    __shared__ uint4 s_q[QL ? NTW * 16 * kQStride : 1];
+    Fr* fp;
+    if constexpr (QL) fp = reinterpret_cast<Fr*>(s_kstA);
+    else fp = s_fr.f;
+    Fr (&frame)[HP] = *reinterpret_cast<Fr(*)[HP]>(fp);
     mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
                                         size_t pbs) {
-        mfma_item<NTW, HP, POL, KM>(a, frame, s_blk, s_kstA, s_kstB, si, ug, rg, bb, be, ns, pb0, pbs);
+        mfma_item<NTW, HP, POL, KM>(a, frame, s_blk, s_kstA, s_kstB, s_q, si, ug, rg, bb, be, ns, pb0, pbs);
     });
 }
 
@@ -1585,7 +1684,8 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA) {
-        const bool rows16 = mfma_rows_per_group(a.rows_cap) == 16;
+        const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0);
+        const bool rows16 = rpg == 16;
 #define KYRO_MFMA_LAUNCH2(K, POL, PLAN)                                                     \
         if (a.hpw == 2) {                                                                   \
             if (rows16) K<1, 2, POL, PLAN><<<grid, block, 0, stream>>>(a);                  \
@@ -1596,7 +1696,8 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
         }
 #define KYRO_MFMA_LAUNCH(POL, PLAN)                                                         \
         if (a.dtype_bf16) {                                                                 \
-            KYRO_MFMA_LAUNCH2(attn_mfma_kernel, POL, PLAN)                                  \
+            if (rpg == kMfmaManyRows) attn_mfma_kernel<kMfmaManyRows / 16, 1, POL, PLAN><<<grid, block, 0, stream>>>(a); \
+            else { KYRO_MFMA_LAUNCH2(attn_mfma_kernel, POL, PLAN) }                         \
         } else {                                                                            \
             KYRO_MFMA_LAUNCH2(attn_mfma_f32_kernel, POL, PLAN)                              \
         }

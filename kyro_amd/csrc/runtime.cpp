@@ -232,16 +232,18 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     const double scale = p->scale > 0 ? (double)p->scale : 1.0 / std::sqrt((double)p->head_dim);
     a.scale_log2 = (float)(scale * 1.4426950408889634);
     a.units = p->batch_size * p->num_kv_heads;
+    // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
+    // (vector) or 16 / 32 / 64 (MFMA) rows that stream the same K/V.
+    const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA
+                                   ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16)
+                                   : kyro::kVectorRowsPerGroup;
     // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
     // waves per head): the workgroup then reads both heads' slabs of each block together, and
-    // the Llama-3-8B step fits the chip in one round of workgroups.
-    a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0) ? 2 : 1;
+    // the Llama-3-8B step fits the chip in one round of workgroups. The 64-row kernel takes one
+    // kv head per workgroup (its four waves and its LDS are that head's).
+    a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0 && rows_per_group <= 32) ? 2 : 1;
     a.ugroups = a.units / a.hpw;
     a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
-    // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
-    // (vector) or 16 / 32 (MFMA) rows that stream the same K/V.
-    const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA ? kyro::mfma_rows_per_group(a.rows_cap)
-                                                                : kyro::kVectorRowsPerGroup;
     a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
     // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
     // of a kv head, or (as the caller says) other sequences holding the same blocks.

@@ -64,6 +64,10 @@ SMALL = [
     ((32, 8), 128, [129, 300, 40, 257], [8, 8, 8, 8]),
     ((64, 8), 128, [260, 50, 9, 700], [9, 1, 4, 6]),
     ((8, 1), 128, [33, 77], [1, 2]),
+    # up to 64 rows per kv head: one four-tile row group (units of 64, 40, 32 and 16 rows)
+    ((16, 2), 128, [100, 33, 700, 16], [8, 5, 4, 2]),
+    # 80 rows: a 64-row group and a 16-row group
+    ((32, 2), 128, [300, 47], [5, 2]),
 ]
 
 
@@ -197,6 +201,7 @@ BALANCED = [
     ((12, 3), [5000, 40, 16, 1500], [2, 5, 1, 3]),
     ((8, 2), [20000, 100], [3, 1]),
     ((32, 8), [64], [8]),
+    ((16, 2), [3000, 40, 0, 900, 17], [8, 5, 3, 8, 1]),
 ]
 
 

@@ -19,7 +19,8 @@ def _ceil(a, b):
 
 
 def _rows_per_group(rows_cap):
-    return 16 if rows_cap <= 16 else 32
+    """Rows per MFMA row group for bf16: one tile, two, or the four-tile kernel's 64."""
+    return 16 if rows_cap <= 16 else 32 if rows_cap <= 32 else 64
 
 
 def _random_batch(g):
@@ -59,9 +60,10 @@ def test_slot_bound_holds_over_random_batches(chunk_div, num_cus):
         assert info["items"] <= info["slot_bound"], (info, ctx.tolist(), ql.tolist(), hkv, group)
         worst = max(worst, info["items"] / info["slot_bound"])
         # Items are sequence x kv head group x split x row group, with the row groups of the
-        # launch's row-group size (16 or 32 rows per group for the MFMA kernel).
-        hp = 2 if hkv % 2 == 0 else 1
+        # launch's row-group size (16, 32 or 64 rows per group for the bf16 MFMA kernels; the
+        # 64-row kernel takes one kv head per workgroup).
         rw = _rows_per_group(group * max(1, int(ql.max())))
+        hp = 2 if hkv % 2 == 0 and rw <= 32 else 1
         r = _ceil(ql.astype(np.int64) * group, rw)
         assert info["items"] == int(np.sum((hkv // hp) * splits.astype(np.int64) * r))
         # Splits: one for a sequence within the chunk; otherwise chunks of C blocks from the start,
