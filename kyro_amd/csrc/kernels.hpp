@@ -25,6 +25,10 @@ enum AttnKernel : int { ATTN_KERNEL_VECTOR = 1, ATTN_KERNEL_MFMA = 2 };
 // policy and 6.8-7.0 TB/s with the hint; data read again by another workgroup then misses L2.
 constexpr int kLoadCached = 0;
 constexpr int kLoadStream = 2;
+// Not a hardware policy: the kernel picks kLoadStream or kLoadCached per unit.
+constexpr int kLoadPerUnit = -1;
+// AttnArgs::stream_kv value that selects kLoadPerUnit (four-tile kernel only).
+constexpr int kKvPerUnit = 2;
 
 // Upper bound on the blocks one attention workgroup streams (its split); the block ids of a
 // split are staged in LDS.
@@ -51,7 +55,7 @@ struct AttnArgs {
     int ugroups;       // units / hpw
     int ugroups_padded;  // ugroups rounded up to a multiple of 8 (the XCD count)
     int row_groups;    // workgroups per (unit group, split), each covering rows_per_group rows
-    int stream_kv;     // MFMA kernel: K/V loads with kLoadStream (1) or kLoadCached (0)
+    int stream_kv;     // MFMA kernel: K/V loads with kLoadStream (1), kLoadCached (0) or per unit (kKvPerUnit)
     // Balanced schedule (MFMA kernel, automatic splits): a persistent grid of plan_grid
     // workgroups computes per-sequence splits from the context lengths and walks the work items
     // largest first. Partial states live in per-item slots of plan_rw rows per kv head;

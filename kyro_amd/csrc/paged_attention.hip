@@ -747,7 +747,8 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 // workgroup then reads both heads' slabs of each block together (8 KiB contiguous of K and of
 // V), and a batch with 2 x 256 units runs as one round of workgroups on 256 CUs instead of two.
 // POL is the cache policy of the K/V loads: kLoadStream when no other workgroup reads the same
-// slabs (the host decides), kLoadCached otherwise.
+// slabs (the host decides), kLoadCached otherwise, or kLoadPerUnit: streaming for units whose
+// rows fit one row group, cached for the others (their row groups share the slabs in L2).
 //
 // mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
 // head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
@@ -1011,22 +1012,32 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 b1 = j + 1 < npairs ? b1 : -1;
             };
             KVPair bufA, bufB;
-            if (npairs > 0) {
-                // The next pair's loads are issued unconditionally: past the last pair they read
-                // the zero slab (and are dropped), so no branch separates a prefetch from the
-                // wait that precedes the computation of the pair before it.
+            // The next pair's loads are issued unconditionally: past the last pair they read
+            // the zero slab (and are dropped), so no branch separates a prefetch from the wait
+            // that precedes the computation of the pair before it. P is the loads' cache policy.
+            auto stream = [&](auto pol) {
+                constexpr int P = decltype(pol)::value;
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<POL, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<P, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<POL, KM>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    load_pair<P, KM>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
                     compute(bufA, ktA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<POL, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    load_pair<P, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                     compute(bufB, ktB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
+                }
+            };
+            if (npairs > 0) {
+                if constexpr (POL == kLoadPerUnit) {
+                    // A unit whose rows fit this row group is read by no other workgroup.
+                    if (si.rows <= RW) stream(std::integral_constant<int, kLoadStream>{});
+                    else stream(std::integral_constant<int, kLoadCached>{});
+                } else {
+                    stream(std::integral_constant<int, POL>{});
                 }
             }
         }
@@ -1701,7 +1712,10 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
         } else {                                                                            \
             KYRO_MFMA_LAUNCH2(attn_mfma_f32_kernel, POL, PLAN)                              \
         }
-        if (a.plan) {
+        if (a.stream_kv == kKvPerUnit) {  // four-tile kernel only (the host decides)
+            if (a.plan) attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, true><<<grid, block, 0, stream>>>(a);
+            else attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, false><<<grid, block, 0, stream>>>(a);
+        } else if (a.plan) {
             if (a.stream_kv) {
                 KYRO_MFMA_LAUNCH(kLoadStream, true)
             } else {

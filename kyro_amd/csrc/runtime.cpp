@@ -246,8 +246,12 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
     a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
     // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
-    // of a kv head, or (as the caller says) other sequences holding the same blocks.
+    // of a kv head, or (as the caller says) other sequences holding the same blocks. The
+    // four-tile kernel decides per unit under AUTO: on a ragged batch only the units with more
+    // than 64 rows have a second row group.
     a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
+    if (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups > 1 && rows_per_group == kyro::kMfmaManyRows)
+        a.stream_kv = kyro::kKvPerUnit;
 
     // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
     const int mb = std::max(1, p->max_blocks_per_seq);
