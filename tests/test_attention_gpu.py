@@ -127,13 +127,15 @@ def test_repeat_calls_are_bitwise_identical(gpu):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("q_len, gqa", [(8, (32, 8)), (9, (64, 8)), (3, (6, 3))])
-def test_kv_reuse_hint_never_changes_the_result(gpu, q_len, gqa):
+@pytest.mark.parametrize("q_lens, gqa", [([8] * 4, (32, 8)), ([9] * 4, (64, 8)), ([9, 4, 8, 1], (64, 8)),
+                                         ([3] * 4, (6, 3))])
+def test_kv_reuse_hint_never_changes_the_result(gpu, q_lens, gqa):
     """The hint only picks the K/V loads' cache policy: 32 rows per kv head (one row group,
-    streamed under "auto"), 72 rows (three row groups, cached under "auto"), and an odd kv head
-    count (one kv head per workgroup) with 6 rows; every hint gives the same bits."""
+    streamed under "auto"), 72 rows (a 64-row and an 8-row group, cached under "auto"), ragged
+    72/32/64/8 rows (under "auto" the first sequence cached, the others streamed), and an odd kv
+    head count (one kv head per workgroup) with 6 rows; every hint gives the same bits."""
     H, Hkv = gqa
-    case = wl.make_attention_case(context_lens=[700, 33, 2048, 16], q_lens=[q_len] * 4, num_heads=H,
+    case = wl.make_attention_case(context_lens=[700, 33, 2048, 16], q_lens=q_lens, num_heads=H,
                                   num_kv_heads=Hkv, shared_prefix_blocks=2, seed=5)
     t = h.attention_tensors(case, gpu)
     attn = make_attention(16, H, 128, Hkv)
@@ -277,18 +279,20 @@ def test_balanced_schedule_large_batches(gpu, batch):
     h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 1023, 1024]), h.ATOL_BF16)
 
 
-def test_balanced_schedule_replays_from_a_graph(gpu):
+@pytest.mark.parametrize("H", [32, 64])
+def test_balanced_schedule_replays_from_a_graph(gpu, H):
     """A balanced launch (plan, per-lane claim counters, combine pass) captured in a HIP graph
     after an eager call on the same stream (so the arena is already large enough): every replay,
     with eager launches of another shape and synchronisations in between, equals the eager
-    result bit for bit."""
+    result bit for bit. GQA 32/8 runs the two-tile kernel, GQA 64/8 (up to 64 rows per kv head)
+    the four-tile one."""
     case = wl.make_attention_case(context_lens=[3000, 17, 0, 900, 5000, 33], q_lens=[8, 8, 3, 1, 5, 8],
-                                  num_heads=32, num_kv_heads=8, dtype="bf16", seed=23)
-    other = wl.make_attention_case(context_lens=[700, 2100], q_lens=[2, 3], num_heads=32, num_kv_heads=8,
+                                  num_heads=H, num_kv_heads=8, dtype="bf16", seed=23)
+    other = wl.make_attention_case(context_lens=[700, 2100], q_lens=[2, 3], num_heads=H, num_kv_heads=8,
                                    dtype="bf16", seed=24)
     t = h.attention_tensors(case, gpu)
     t2 = h.attention_tensors(other, gpu)
-    attn = make_attention(16, 32, 128, 8)
+    attn = make_attention(16, H, 128, 8)
     args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
     args2 = (t2["query"], t2["key_cache"], t2["value_cache"], t2["block_table"], t2["context_lens"])
     s = torch.cuda.Stream(gpu)
