@@ -169,6 +169,34 @@ __device__ float block_sum_f(float v, RowShared& sh) {
     return r;
 }
 
+// Bits every candidate's key shares, counted from the top (32 when all keys are equal), and their
+// value: the first digit of a search over the candidates can start below them.
+__device__ void cand_common_prefix(int n, RowShared& sh, int* bits, uint64_t* prefix) {
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int i = threadIdx.x; i < n; i += kRT) {
+        const uint32_t key = (uint32_t)(sh.cand[i] >> 32);
+        lo = min(lo, key);
+        hi = max(hi, key);
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
+        hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sh.ired[threadIdx.x >> 6] = (int)lo;
+        sh.wsum[threadIdx.x >> 6] = hi;
+    }
+    __syncthreads();
+    for (int w = 0; w < kRW; ++w) {
+        lo = min(lo, (uint32_t)sh.ired[w]);
+        hi = max(hi, (uint32_t)sh.wsum[w]);
+    }
+    __syncthreads();
+    const int b = (n == 0 || lo == hi) ? 32 : __clz((int)(lo ^ hi));
+    *bits = b;
+    *prefix = b == 0 ? 0 : (uint64_t)(lo >> (32 - b));
+}
+
 // First index holding the maximum of v over the block (v = -inf for no candidate).
 __device__ int block_argmax(float v, int i, RowShared& sh) {
     for (int o = 32; o >= 1; o >>= 1) {
@@ -424,20 +452,25 @@ __device__ int first_at_least(const float* c, int n, float x, bool strict, RowSh
 
 // desc_search over the row's candidate list in LDS instead of the row: entries sh.cand[0, n),
 // (key << 32) | ~index. The same order (key descending, then index ascending), the same masses
-// and the same crossing rule, found by mass histograms over the key's digits (11, 11, 10 bits)
-// and, when several members share the found key, over ~index's digits (descending ~index is
-// ascending index). A level that leaves one member settles the search early. Returns the index,
-// or -1 when the members' mass falls short of theta; *key_out gets its key.
+// and the same crossing rule, found by mass histograms over the key's digits (up to 11 bits each,
+// from below the pbits0 top bits every candidate shares, prefix0) and, when several members share
+// the found key, over ~index's digits (descending ~index is ascending index). Starting below the
+// shared bits spreads the first level's candidates over its bins: a top-p row's candidates fall
+// in a handful of 11-bit top bins, and their atomic adds to those few bins serialise. A level that
+// leaves one member settles the search early. Returns the index, or -1 when the members' mass
+// falls short of theta; *key_out gets its key.
 template <class Member, class MassOf>
 __device__ int cand_search(int n, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
-                           u64* before_out, u64* mass_out, uint32_t* key_out) {
+                           u64* before_out, u64* mass_out, uint32_t* key_out, int pbits0 = 0,
+                           uint64_t prefix0 = 0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint64_t prefix = 0;  // fixed high bits of (key << 32 | ~index)
-    int pbits = 0;
+    uint64_t prefix = prefix0;  // fixed high bits of (key << 32 | ~index)
+    int pbits = pbits0;
     u64 before = 0;
     bool single = false;
-    for (int lvl = 0; lvl < 6 && !single; ++lvl) {
-        const int bits = (lvl % 3) < 2 ? 11 : 10;
+    for (int lvl = 0; lvl < 7 && !single && pbits < 64; ++lvl) {
+        // Key digits up to the key's last bit, then ~index digits.
+        const int bits = pbits < 32 ? min(11, 32 - pbits) : min(11, 64 - pbits);
         const int nb = 1 << bits;
         for (int i = tid; i < nb; i += kRT) {
             sh.hist[i] = 0;
@@ -1010,12 +1043,15 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
         const u64* cand = a.cand + (size_t)b * kCap;
         for (int i = tid; i < n; i += kRT) sh.cand[i] = cand[i];
         __syncthreads();
+        int cp_bits;
+        uint64_t cp;
+        cand_common_prefix(n, sh, &cp_bits, &cp);
         auto every = [](uint32_t, int) { return true; };
         auto unit = [](float) -> u64 { return 1; };
         u64 bf, ms;
         uint32_t key;
         if (use_k) {  // the k-th token in descending order bounds the kept set
-            const int kth = cand_search(n, every, unit, (u64)k, false, sh, &bf, &ms, &key);
+            const int kth = cand_search(n, every, unit, (u64)k, false, sh, &bf, &ms, &key, cp_bits, cp);
             if (kth >= 0) {
                 r.kk = key;
                 r.ki = kth;
@@ -1033,7 +1069,7 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
         float rr = u;
         bool settled = true;
         if (use_p) {
-            const int cut = cand_search(n, kept, pmass, (u64)llrint((double)tp * kFix), true, sh, &bf, &ms, &key);
+            const int cut = cand_search(n, kept, pmass, (u64)llrint((double)tp * kFix), true, sh, &bf, &ms, &key, cp_bits, cp);
             if (cut >= 0) {
                 r.ck = key;
                 r.ci = cut;
@@ -1053,9 +1089,9 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
         if (settled) {
             auto in_cut = [&](uint32_t kc, int v) { return r.kept(kc, v) && r.in_cut(kc, v); };
             const u64 theta = fix_mass(rr);
-            int pick = theta == 0 ? cand_search(n, in_cut, unit, 1, false, sh, &bf, &ms, &key)
-                                  : cand_search(n, in_cut, pmass, theta, false, sh, &bf, &ms, &key);
-            if (pick < 0) pick = use_p ? cand_search(n, kept, unit, 1, false, sh, &bf, &ms, &key) : r.ki;
+            int pick = theta == 0 ? cand_search(n, in_cut, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp)
+                                  : cand_search(n, in_cut, pmass, theta, false, sh, &bf, &ms, &key, cp_bits, cp);
+            if (pick < 0) pick = use_p ? cand_search(n, kept, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp) : r.ki;
             if (tid == 0) a.out[b] = (uint32_t)(pick >= 0 && pick < V ? pick : V - 1);
             return;
         }
