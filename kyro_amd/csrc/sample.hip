@@ -716,6 +716,10 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
     if (!use_k && !use_p) return;
     const bool mass = !use_k;  // top-p alone locates its cut by mass, top-k by count
+    // Top-p keeps a token only if p >= (1 - top_p) / V; with log Z >= this chunk's max m, a token
+    // with z <= m - ln(V / (1 - top_p)) is never kept (one nat of margin for rounding), so it
+    // needs no bin. The select pass takes the crossing target from Z itself, not from the bins.
+    const float skip_below = mass ? m - (logf((float)a.V / fmaxf(1.f - tp, 1e-30f)) + 1.f) : -__builtin_huge_valf();
     for (int i = tid; i < kBins; i += kCT) {
         s_cnt[i] = 0;
         s_mass[i] = 0;
@@ -723,7 +727,7 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kCPer; ++i) {
-        if (chunk_index(v0, i, vec4) >= v1) continue;
+        if (chunk_index(v0, i, vec4) >= v1 || x[i] <= skip_below) continue;
         const int bin = (int)(order_key(x[i]) >> 21);
         atomicAdd(&s_cnt[bin], 1u);
         if (mass) {
@@ -899,12 +903,11 @@ __global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
     if (use_k) {
         tb = desc_bin_search(sh.cnt, (u64)k, false, sh);
     } else {
-        u64 tot = 0;
-        for (int i = lane; i < kBins; i += 64) tot += sh.hist[i];
-        tot = wave_sum_u64(tot);
-        // The bin holding the crossing. Its mass is rounded differently from the candidates'
-        // own sums: should the exact cut fall below it, the final pass finds no cut among the
-        // candidates and runs the radix path.
+        // The bin holding the crossing of tp Z (the stats pass leaves out of the bins only tokens
+        // that top-p never keeps, all below the cut). Its mass is rounded differently from the
+        // candidates' own sums: should the exact cut fall below it, the final pass finds no cut
+        // among the candidates and runs the radix path.
+        const u64 tot = (u64)llrint((double)Z * kFixE);
         tb = desc_bin_search(sh.hist, (u64)llrint((double)tp * (double)tot), true, sh);
     }
     u64 ncand = ~0ull;
