@@ -732,8 +732,10 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         atomicAdd(&s_cnt[bin], 1u);
         if (mass) {
             const float e = fast_exp2((x[i] - bin_top(bin)) * kLog2e);
-            if (e > 0.f && e <= 1.f) {  // at most 4096 * 2^20 per bin: fits 32 bits
-                const uint32_t f = (uint32_t)__float2uint_rn(e * kFixC);
+            if (e > 0.f && e <= 1.f) {
+                // At most 2^20 - 1 units a token (a token exactly at its bin's top would give
+                // 2^20), so 4096 of them stay below 2^32. The bin masses only choose candidates.
+                const uint32_t f = min((uint32_t)__float2uint_rn(e * kFixC), (uint32_t)kFixC - 1u);
                 if (f) atomicAdd(&s_mass[bin], f);
             }
         }
