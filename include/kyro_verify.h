@@ -205,9 +205,10 @@ int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_para
 /* The balanced schedule's plan for one batch, computed on the host with the chunk and split
  * arithmetic the device plan runs, from host copies of the context lengths and the per-sequence
  * query rows (q_lens NULL: one row each). For analysis and tests; no counterpart in the
- * reference. num_cus 0 means 256; chunk_div 0 means the library's divisor (a sequence longer than
- * the per-workgroup share L of the work splits into chunks of about L / chunk_div blocks; other
- * values model other divisors, the slot bound included). Fails with KYRO_EINVAL when the params
+ * reference. num_cus 0 means 256; chunk_quarters 0 means the library's chunk length (a sequence
+ * longer than the per-workgroup share L of the work splits into chunks of about
+ * L x chunk_quarters / 4 blocks, 3L/2 by default; other values model other chunk lengths, the
+ * slot bound included). Fails with KYRO_EINVAL when the params
  * would run on the grid schedule. out_splits [B] (may be NULL): splits per sequence (0 for a
  * sequence without rows). */
 typedef struct kyro_attention_plan {
@@ -219,7 +220,7 @@ typedef struct kyro_attention_plan {
                               latches KYRO_EINVAL instead of running a plan with more items */
 } kyro_attention_plan;
 
-int kyro_paged_attention_plan(const kyro_paged_attention_params* params, int num_cus, int chunk_div,
+int kyro_paged_attention_plan(const kyro_paged_attention_params* params, int num_cus, int chunk_quarters,
                               const int64_t* context_lens, const int32_t* q_lens, int32_t* out_splits,
                               kyro_attention_plan* out);
 

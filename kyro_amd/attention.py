@@ -140,7 +140,7 @@ class PagedAttention:
 
 def attention_plan(attn: PagedAttention, context_lens, q_lens=None, *, max_blocks_per_seq: int,
                    num_blocks: int = 1, dtype=torch.bfloat16, schedule: str = "balanced",
-                   num_cus: int = 0, chunk_div: int = 0):
+                   num_cus: int = 0, chunk_quarters: int = 0):
     """The balanced schedule's plan of a batch, computed on the host by the library
     (``kyro_paged_attention_plan``) from host arrays of context lengths and per-sequence query
     rows. No GPU is needed. Returns (kyro_attention_plan fields as a dict, splits per sequence)."""
@@ -158,7 +158,7 @@ def attention_plan(attn: PagedAttention, context_lens, q_lens=None, *, max_block
     out = _lib.AttentionPlan()
     splits = np.zeros(batch, np.int32)
     _lib.check(_lib.lib().kyro_paged_attention_plan(
-        ctypes.byref(params), int(num_cus), int(chunk_div), ctx.ctypes.data,
+        ctypes.byref(params), int(num_cus), int(chunk_quarters), ctx.ctypes.data,
         ql.ctypes.data if ql is not None else None, splits.ctypes.data, ctypes.byref(out)))
     info = {f: getattr(out, f) for f, _ in _lib.AttentionPlan._fields_}
     return info, splits

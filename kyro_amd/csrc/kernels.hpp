@@ -81,18 +81,20 @@ constexpr int kPlanMaxSeqs = 1024;
 // Shortest split the balanced schedule makes, in blocks.
 constexpr int kPlanMinChunk = 16;
 // A sequence longer than the per-workgroup share L of the work splits into chunks of about
-// L / kPlanChunkDiv blocks. plan_slot_bound takes the same divisor.
-constexpr int kPlanChunkDiv = 2;
+// L x kPlanChunkQuarters / 4 blocks (3L/2: on a batch with one 32k-token prefix among short
+// sequences this beats L/2 by 12%; L/2, 3L/4 and 2L all leave a longer tail, L is within 1%).
+// plan_slot_bound takes the same count.
+constexpr int kPlanChunkQuarters = 6;
 
 // Balanced-schedule chunk length in blocks, from the total work T (kv head groups x row groups x
 // blocks, summed over sequences), the longest sequence maxnb (blocks) and the persistent grid:
-// L = ceil(T / grid); C = L when no sequence is longer than L, else ceil(L / div); then at least
-// kPlanMinChunk, rounded up to even, at most max_chunk (even). The device plan and the host
-// checks share this function.
+// L = ceil(T / grid); C = L when no sequence is longer than L, else ceil(L x quarters / 4); then
+// at least kPlanMinChunk, rounded up to even, at most max_chunk (even). The device plan and the
+// host checks share this function.
 __host__ __device__ inline int plan_chunk_blocks(long long T, int maxnb, int grid, int max_chunk,
-                                                 int div = kPlanChunkDiv) {
+                                                 int quarters = kPlanChunkQuarters) {
     const long long L = (T + grid - 1) / grid;
-    long long CL = maxnb <= L ? L : (L + div - 1) / div;
+    long long CL = maxnb <= L ? L : (L * quarters + 3) / 4;
     CL = CL < kPlanMinChunk ? kPlanMinChunk : CL;
     CL = (CL + 1) & ~1ll;
     return (int)(CL > max_chunk ? max_chunk : CL);
@@ -111,15 +113,16 @@ __host__ __device__ inline void plan_split(int nb, int C, int& ns, int& ch) {
 
 // Upper bound on the partial-state slots of a balanced-schedule launch (one slot per item:
 // sequence x kv head group x split x row group). Every split but one per item group is at least
-// C >= min(L / div, max_chunk) blocks long, so the extra splits number at most div x grid (or
-// work / max_chunk), plus one per (kv head group, row group) of every sequence. The device plan
-// compares its slot total with this bound and latches ERR_PLAN instead of writing past it.
+// C >= min(L x quarters / 4, max_chunk) blocks long and the work is at most L x grid blocks, so
+// the extra splits number at most ceil(4 x grid / quarters) (or work / max_chunk), plus one per
+// (kv head group, row group) of every sequence. The device plan compares its slot total with
+// this bound and latches ERR_PLAN instead of writing past it.
 __host__ __device__ inline long long plan_slot_bound(long long B, long long ugroups_per_seq, long long row_groups,
                                                      long long max_blocks, long long max_chunk, long long grid,
-                                                     int div = kPlanChunkDiv) {
+                                                     int quarters = kPlanChunkQuarters) {
     const long long s = B * ugroups_per_seq * row_groups;
     const long long by_chunk = (s * max_blocks + max_chunk - 1) / max_chunk;
-    const long long by_share = (long long)div * grid;
+    const long long by_share = (4 * grid + quarters - 1) / quarters;
     return s + (by_chunk > by_share ? by_chunk : by_share);
 }
 

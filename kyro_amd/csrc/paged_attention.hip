@@ -410,7 +410,7 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //  * work of sequence b: W_b = kv head groups x row groups x blocks; per-workgroup share
 //    L = ceil(sum W / grid);
 //  * chunk C = L when no sequence is longer than L (nothing splits, so a uniform batch keeps one
-//    item per (sequence, kv head group)), else ceil(L / kPlanChunkDiv) (L / 2), within
+//    item per (sequence, kv head group)), else ceil(L x kPlanChunkQuarters / 4) (3L / 2), within
 //    [kPlanMinChunk, max chunk];
 //  * a longer sequence splits into chunks of C blocks from its start, the last one shorter;
 //  * item groups (sequence, chunk, kv head group) come in two phases: first every chunk but the

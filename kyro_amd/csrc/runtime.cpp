@@ -158,7 +158,7 @@ struct AttnSetup {
 };
 
 int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int num_cus, AttnSetup& s,
-                    int chunk_div = kyro::kPlanChunkDiv) {
+                    int chunk_quarters = kyro::kPlanChunkQuarters) {
     if (!p) return fail(KYRO_EINVAL, "paged_attention: params is null");
     if (p->block_size <= 0 || p->num_heads <= 0 || p->head_dim <= 0 || p->num_kv_heads <= 0)
         return fail(KYRO_EINVAL, "paged_attention: block_size/num_heads/head_dim/num_kv_heads must be > 0");
@@ -296,7 +296,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
         a.plan_max_chunk = max_chunk / 2 * 2;
         a.splits = 1;
         s.plan_slots = (size_t)kyro::plan_slot_bound(a.B, a.ugroups / a.B, a.row_groups, mb, a.plan_max_chunk,
-                                                     a.plan_grid, chunk_div);
+                                                     a.plan_grid, chunk_quarters);
         // KYRO_TEST_PLAN_SLOT_CAP lowers the slots sized, so that a test can drive the device
         // plan's overflow check (ERR_PLAN, no item runs) without a plan/bound mismatch.
         if (const char* cap = std::getenv("KYRO_TEST_PLAN_SLOT_CAP")) {
@@ -630,16 +630,16 @@ int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_para
     });
 }
 
-int kyro_paged_attention_plan(const kyro_paged_attention_params* p, int num_cus, int chunk_div,
+int kyro_paged_attention_plan(const kyro_paged_attention_params* p, int num_cus, int chunk_quarters,
                               const int64_t* context_lens, const int32_t* q_lens, int32_t* out_splits,
                               kyro_attention_plan* out) {
     return guarded([&]() -> int {
         if (!out) return fail(KYRO_EINVAL, "paged_attention_plan: out is null");
         *out = kyro_attention_plan{};
         if (num_cus <= 0) num_cus = kDefaultCUs;
-        if (chunk_div <= 0) chunk_div = kyro::kPlanChunkDiv;
+        if (chunk_quarters <= 0) chunk_quarters = kyro::kPlanChunkQuarters;
         AttnSetup s;
-        if (int rc = attention_setup(p, q_lens != nullptr, num_cus, s, chunk_div)) return rc;
+        if (int rc = attention_setup(p, q_lens != nullptr, num_cus, s, chunk_quarters)) return rc;
         const kyro::AttnArgs& a = s.a;
         if (s.empty) return KYRO_OK;
         if (!context_lens) return fail(KYRO_EINVAL, "paged_attention_plan: context_lens is null");
@@ -662,7 +662,7 @@ int kyro_paged_attention_plan(const kyro_paged_attention_params* p, int num_cus,
             T += (long long)U * r[b] * nb[b];
             if (r[b] > 0) maxnb = std::max(maxnb, nb[b]);
         }
-        const int C = kyro::plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk, chunk_div);
+        const int C = kyro::plan_chunk_blocks(T, maxnb, a.plan_grid, a.plan_max_chunk, chunk_quarters);
         long long items = 0;
         for (int b = 0; b < a.B; ++b) {
             int ns, ch;

@@ -4,8 +4,9 @@ partial-state slots than a launch sizes, over seeded random batches.
 
 A launch sizes its workspace from the params alone (plan_slot_bound), before the context lengths
 are known; the device plan then latches KYRO_EINVAL instead of running a plan with more items.
-An experimental chunk divisor of 3 once ran against a bound derived for 2 and wrote past the
-workspace: test_a_bound_for_another_divisor_is_exceeded shows this check catches that mismatch.
+An experimental chunk length once ran against a bound derived for another and wrote past the
+workspace: test_a_bound_for_another_chunk_length_is_exceeded shows this check catches that
+mismatch.
 """
 import numpy as np
 import pytest
@@ -43,16 +44,17 @@ def _random_batch(g):
     return ctx.astype(np.int64), ql.astype(np.int32), hkv, group
 
 
-@pytest.mark.parametrize("chunk_div", [2, 3, 4])
+@pytest.mark.parametrize("chunk_quarters", [0, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("num_cus", [256, 80, 32])
-def test_slot_bound_holds_over_random_batches(chunk_div, num_cus):
-    g = np.random.default_rng(1000 * chunk_div + num_cus)
+def test_slot_bound_holds_over_random_batches(chunk_quarters, num_cus):
+    g = np.random.default_rng(1000 * chunk_quarters + num_cus)
     worst = 0.0
     for _ in range(400):
         ctx, ql, hkv, group = _random_batch(g)
         attn = PagedAttention(16, hkv * group, 128, hkv)
         mb = max(1, int(_ceil(ctx.max(), 16)) + int(g.integers(0, 3)))
-        info, splits = attention_plan(attn, ctx, ql, max_blocks_per_seq=mb, num_cus=num_cus, chunk_div=chunk_div)
+        info, splits = attention_plan(attn, ctx, ql, max_blocks_per_seq=mb, num_cus=num_cus,
+                                      chunk_quarters=chunk_quarters)
         if ql.sum() == 0:  # no query rows: nothing is launched
             assert info["items"] == 0 and info["grid"] == 0
             continue
@@ -87,17 +89,18 @@ def test_a_uniform_batch_keeps_one_item_per_kv_head_group():
     assert (splits == 1).all() and info["items"] == 64 * 4
 
 
-def test_a_bound_for_another_divisor_is_exceeded():
-    """The Llama-2-7B batch (MHA 32/32, B 16, ctx 512-2048, 5 rows) planned with chunks of L/3
-    needs more slots than a bound derived for L/2 allows: the check above has the power to catch
-    the mismatch that once wrote past the workspace, and the shared divisor keeps them consistent."""
+def test_a_bound_for_another_chunk_length_is_exceeded():
+    """The Llama-2-7B batch (MHA 32/32, B 16, ctx 512-2048, 5 rows) planned with chunks of L/2
+    needs more slots than a bound derived for the library's 3L/2 allows: the check above has the
+    power to catch a plan/bound mismatch (one once wrote past the workspace), and the shared chunk
+    constant keeps them consistent."""
     ctx = wl.rng(0, wl.S_CTX).integers(512, 2049, size=16)
     attn = PagedAttention(16, 32, 128, 32)
-    three, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_div=3)
-    two, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_div=2)
-    assert two["items"] <= two["slot_bound"]
-    assert three["items"] <= three["slot_bound"]
-    assert three["items"] > two["slot_bound"]
+    half, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_quarters=2)
+    lib, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128)
+    assert lib["items"] <= lib["slot_bound"]
+    assert half["items"] <= half["slot_bound"]
+    assert half["items"] > lib["slot_bound"]
 
 
 def test_grid_schedule_params_are_refused():
