@@ -230,31 +230,22 @@ struct UploadArgs {
 hipError_t launch_upload_scatter(const UploadArgs& a, hipStream_t stream);
 
 // Plain-decode sampling with logit processors.
-// One non-empty histogram bin of a vocabulary chunk: count, and for top-p the sum of
-// exp(z - top of the bin) in 2^-20 units.
-struct SampleBin {
-    uint32_t bin, count, mass;
-};
-enum SampleMode : int { SAMPLE_DONE = 0, SAMPLE_CAND = 1, SAMPLE_RADIX = 2 };
-// A row's plan after the select pass: settled, candidates in bins >= tb, or radix selects.
-struct SamplePlan {
-    int mode, tb;
-    float m, z;      // max z and sum exp(z - m) over the row
-    int ncand, count;  // candidates expected, and gathered so far
-};
-constexpr int kSampleChunk = 4096;    // vocabulary entries per workgroup of the chunked passes
-constexpr int kSampleListCap = 256;   // non-empty bins a chunk may report (more: radix path)
-constexpr int kSampleCand = 8192;     // candidates a row may sort in LDS
+constexpr int kSampleChunk = 4096;      // vocabulary entries per workgroup of the chunked passes
+constexpr int kSampleCand = 8192;       // candidates a row holds in LDS (the chunks' lists together)
+constexpr int kSampleChunkCand = 256;   // most candidates one chunk lists
 constexpr int kSampleMaxChunks = 1024;  // chunks per row (one per thread of the select pass)
 
 struct SampleArgs {
     const float* logits;        // [B, V]
     float* ws;                  // [B, V] processed rows (rows that have a processor)
     float2* cstat;              // [B, C]: per chunk {max z, sum exp(z - max)} or {max y, index}
-    SampleBin* clist;           // [B, C, kSampleListCap]
-    int* clist_n;               // [B, C]: bins listed, -1 when they did not fit
-    SamplePlan* plan;           // [B]
-    unsigned long long* cand;   // [B, kSampleCand]: (key << 32) | ~index
+    // Top-k / top-p rows: chunk c of row b lists every entry with z >= cthr[b, C + c] (-inf: every
+    // finite entry), ccount[b, C + c] of them (-1: no threshold kept the list within ccap), at
+    // cand[b, c ccap ...] as (key << 32) | ~index.
+    float* cthr;                // [B, C]
+    int* ccount;                // [B, C]
+    unsigned long long* cand;   // [B, kSampleCand]
+    int ccap;                   // list slots per chunk: min(kSampleChunkCand, kSampleCand / C)
     int C;                      // chunks per row
     const float* temperature;   // [B]
     const float* top_p;         // [B] or nullptr (1.0)

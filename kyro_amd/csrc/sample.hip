@@ -21,23 +21,26 @@
 //   sample_prepare_kernel  (rows with a processor; grid chunk x row) copies the row into the
 //                          workspace with the mask, then the bias, then the penalty applied.
 //   sample_stats_kernel    (grid chunk x row) per chunk: {max z, sum exp(z - max z)}, or the first
-//                          maximum at T <= 0; with top-k / top-p also the chunk's non-empty bins
-//                          of the top 11 bits of an order-preserving key of z (counts, and for
-//                          top-p alone exp(z - top of the bin) sums in 2^-20 units).
+//                          maximum at T <= 0. Top-k / top-p rows also list the chunk's
+//                          candidates: every entry at or above a threshold t chosen by block-wide
+//                          counts (wave ballots, no atomics) on a grid of 1/64 nat below the
+//                          chunk's max: for top-k the highest t with k entries above it, for top-p
+//                          alone the lowest t whose list fits (ccap entries), or the bound below
+//                          which top-p never keeps a token.
 //   sample_select_kernel   (one workgroup per row) settles greedy and plain rows: the first
 //                          maximum, or Z, the chunk where the running mass reaches u Z and the
-//                          walk inside it. Top-k / top-p rows get the candidate bins: down to the
-//                          bin holding the k-th token, or the bin holding the top-p crossing.
-//   sample_gather_kernel   (grid chunk x row) appends the candidates to the row's list.
-//   sample_final_kernel    (one workgroup per row) cuts and walks the candidates in descending
-//                          order (key descending, index ascending): up to kSortMax of them sorted
-//                          in LDS with running sums; more searched in LDS with the mass
-//                          histograms of the row path below (a sort of ~2000 took 38 us of the
-//                          76 us of a top-p 0.9 batch of 64 rows). Rows whose candidates did not
-//                          fit (or did not settle the cut) run exact radix selects over the whole
+//                          walk inside it. Top-k / top-p rows gather the chunks' lists into LDS.
+//                          For top-k they hold the row's k largest; for top-p alone every token
+//                          at or above the largest threshold. The row is then cut and walked in
+//                          descending order (key descending, index ascending): up to kSortMax
+//                          candidates sorted with running sums; more searched with mass
+//                          histograms over the key's digits. Rows whose lists do not cover the
+//                          kept set (or the top-p cut) run exact radix selects over the whole
 //                          row instead: three passes (11 + 11 + 10 bits) of mass histograms in LDS
 //                          (64-bit fixed point, 2^-52 resolution, so the sums do not depend on
 //                          thread order), then a pass in index order for ties between equal keys.
+#include <cfloat>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -46,15 +49,21 @@ namespace {
 
 constexpr int kRT = 1024;  // threads of the row kernel
 constexpr int kRW = kRT / 64;
+#ifndef KYRO_COUNT_LANE
+#define KYRO_COUNT_LANE 0
+#endif
+// Top-p alone: the most candidates a chunk lists below its skip bound (fewer candidates search
+// faster; lists too short to reach the cut send the row to the radix path).
+#ifndef KYRO_SAMPLE_P_TARGET
+#define KYRO_SAMPLE_P_TARGET 128
+#endif
 constexpr int kBins = 2048;
+static_assert(kBins >= 2 * kSampleMaxChunks, "the select pass keeps list lengths and offsets in RowShared::cnt");
 constexpr int kCap = kSampleCand;            // candidates held in LDS
 // Up to this many candidates are sorted (bitonic, in LDS); more are searched by mass histograms,
 // whose per-level cost does not grow with the count.
 constexpr int kSortMax = 512;
-constexpr int kListCap = kSampleListCap;
 constexpr double kFix = 4503599627370496.0;  // 2^52: fixed-point unit of probability mass
-constexpr double kFixE = 1099511627776.0;    // 2^40: unit of exp(z - max) in a row's bin masses
-constexpr float kFixC = 1048576.0f;          // 2^20: unit of exp(z - top of the bin) in a chunk's bins
 constexpr float kLog2e = 1.4426950408889634f;
 using u64 = unsigned long long;
 
@@ -99,6 +108,15 @@ __device__ __forceinline__ float wave_incl_scan_f(float x) {
     return x;
 }
 
+__device__ __forceinline__ int wave_incl_scan_i(int x) {
+    const int lane = threadIdx.x & 63;
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
 struct RowShared {
     u64 hist[kBins];
     uint32_t cnt[kBins];
@@ -111,6 +129,8 @@ struct RowShared {
     u64 before;      // mass before the found bin / element
     u64 mass;        // its mass
     int count;
+    int nsmall;           // members of a search's last bin, gathered for one wave to sort
+    int sidx[64];
 };
 
 // Calls f(v, y[v]) for the elements this thread owns (strided over the block), with four 16-byte
@@ -149,7 +169,7 @@ __device__ __forceinline__ void row_for_each(const float* y, int V, bool vec4, F
     }
 }
 
-__device__ float block_max_f(float v, RowShared& sh) {
+__device__ __forceinline__ float block_max_f(float v, RowShared& sh) {
     v = wave_max(v);
     if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -159,7 +179,7 @@ __device__ float block_max_f(float v, RowShared& sh) {
     return r;
 }
 
-__device__ float block_sum_f(float v, RowShared& sh) {
+__device__ __forceinline__ float block_sum_f(float v, RowShared& sh) {
     v = wave_sum(v);
     if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -169,15 +189,20 @@ __device__ float block_sum_f(float v, RowShared& sh) {
     return r;
 }
 
-// Bits every candidate's key shares, counted from the top (32 when all keys are equal), and their
-// value: the first digit of a search over the candidates can start below them.
-__device__ void cand_common_prefix(int n, RowShared& sh, int* bits, uint64_t* prefix) {
-    uint32_t lo = 0xffffffffu, hi = 0u;
-    for (int i = threadIdx.x; i < n; i += kRT) {
-        const uint32_t key = (uint32_t)(sh.cand[i] >> 32);
-        lo = min(lo, key);
-        hi = max(hi, key);
-    }
+__device__ __forceinline__ int block_sum_i(int v, RowShared& sh) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) sh.ired[threadIdx.x >> 6] = v;
+    __syncthreads();
+    int r = 0;
+    for (int w = 0; w < kRW; ++w) r += sh.ired[w];
+    __syncthreads();
+    return r;
+}
+
+// Bits every key in [lo, hi] (each thread's range, merged over the block) shares, counted from
+// the top (32 when all keys are equal), and their value: the first digit of a search over the
+// candidates can start below them.
+__device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowShared& sh, int* bits, uint64_t* prefix) {
     for (int o = 32; o >= 1; o >>= 1) {
         lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
         hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
@@ -192,13 +217,13 @@ __device__ void cand_common_prefix(int n, RowShared& sh, int* bits, uint64_t* pr
         hi = max(hi, (uint32_t)sh.wsum[w]);
     }
     __syncthreads();
-    const int b = (n == 0 || lo == hi) ? 32 : __clz((int)(lo ^ hi));
+    const int b = (lo >= hi) ? 32 : __clz((int)(lo ^ hi));
     *bits = b;
     *prefix = b == 0 ? 0 : (uint64_t)(lo >> (32 - b));
 }
 
 // First index holding the maximum of v over the block (v = -inf for no candidate).
-__device__ int block_argmax(float v, int i, RowShared& sh) {
+__device__ __forceinline__ int block_argmax(float v, int i, RowShared& sh) {
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(v, o, 64);
         const int oi = __shfl_xor(i, o, 64);
@@ -252,7 +277,7 @@ __device__ __forceinline__ u64 fix_mass(float p) { return (u64)llrint((double)p 
 // Returns its index, or -1 when the whole set's mass falls short; *before gets the mass ahead
 // of it and *mass its own.
 template <class Member, class MassOf>
-__device__ int desc_search(const Row& r, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
+__device__ __forceinline__ int desc_search(const Row& r, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
                            u64* before_out, u64* mass_out) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t prefix = 0;
@@ -355,34 +380,11 @@ __device__ __forceinline__ float key_value(uint32_t key) {
     return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
-// Bin (of kBins) where the running total of h, taken from the top bin down, first reaches theta
-// (exceeds it when strict); -1 if it never does. Whole block.
-template <class H>
-__device__ int desc_bin_search(const H* h, u64 theta, bool strict, RowShared& sh) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int j0 = 2 * tid, j1 = 2 * tid + 1;  // descending positions
-    const u64 m0 = (u64)h[kBins - 1 - j0], m1 = (u64)h[kBins - 1 - j1];
-    const u64 incl = wave_incl_scan_u64(m0 + m1);
-    if (lane == 63) sh.wsum[wave] = incl;
-    if (tid == 0) sh.found = -1;
-    __syncthreads();
-    u64 base = 0;
-    for (int w = 0; w < wave; ++w) base += sh.wsum[w];
-    const u64 ex0 = base + incl - (m0 + m1), in0 = ex0 + m0, in1 = in0 + m1;
-    auto crosses = [&](u64 ex, u64 in) { return strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta); };
-    if (m0 && crosses(ex0, in0)) sh.found = kBins - 1 - j0;
-    else if (m1 && crosses(in0, in1)) sh.found = kBins - 1 - j1;
-    __syncthreads();
-    const int d = sh.found;
-    __syncthreads();
-    return d;
-}
-
 // Sorts a[0, n) (n a power of two, at most kCap) into descending order. Whole block. Stages
 // whose pairs lie inside one wave's segment of n / kRW entries run without a block barrier (a
 // wave's LDS accesses are processed in order; the wavefront fence only keeps the compiler from
 // moving them), so only strides of a segment or more pay for __syncthreads.
-__device__ void bitonic_desc(u64* a, int n) {
+__device__ __forceinline__ void bitonic_desc(u64* a, int n) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int seg = max(2, n / kRW);  // entries per wave segment (a power of two)
     auto cswap = [&](int lo, int hi, int size) {
@@ -414,7 +416,7 @@ __device__ void bitonic_desc(u64* a, int n) {
 }
 
 // In-place inclusive scan of a[0, n), n <= kCap: thread t owns 8 consecutive entries.
-__device__ void block_scan_incl(float* a, int n, RowShared& sh) {
+__device__ __forceinline__ void block_scan_incl(float* a, int n, RowShared& sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int i0 = tid * 8;
     float loc[8];
@@ -436,7 +438,7 @@ __device__ void block_scan_incl(float* a, int n, RowShared& sh) {
 }
 
 // First i < n with c[i] >= x (> x when strict) for nondecreasing c; -1 if none. Whole block.
-__device__ int first_at_least(const float* c, int n, float x, bool strict, RowShared& sh) {
+__device__ __forceinline__ int first_at_least(const float* c, int n, float x, bool strict, RowShared& sh) {
     if (threadIdx.x == 0) sh.found = 0x7fffffff;
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += kRT) {
@@ -456,19 +458,20 @@ __device__ int first_at_least(const float* c, int n, float x, bool strict, RowSh
 // from below the pbits0 top bits every candidate shares, prefix0) and, when several members share
 // the found key, over ~index's digits (descending ~index is ascending index). Starting below the
 // shared bits spreads the first level's candidates over its bins: a top-p row's candidates fall
-// in a handful of 11-bit top bins, and their atomic adds to those few bins serialise. A level that
-// leaves one member settles the search early. Returns the index, or -1 when the members' mass
-// falls short of theta; *key_out gets its key.
+// in a handful of 11-bit top bins, and their atomic adds to those few bins serialise. Once the
+// found bin holds at most 64 members, one wave ranks them and sums their masses in that order
+// instead of running further levels. Returns the index, or -1 when the members' mass falls short
+// of theta; *key_out gets its key.
 template <class Member, class MassOf>
-__device__ int cand_search(int n, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
+__device__ __forceinline__ int cand_search(int n, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
                            u64* before_out, u64* mass_out, uint32_t* key_out, int pbits0 = 0,
                            uint64_t prefix0 = 0) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t prefix = prefix0;  // fixed high bits of (key << 32 | ~index)
     int pbits = pbits0;
     u64 before = 0;
-    bool single = false;
-    for (int lvl = 0; lvl < 7 && !single && pbits < 64; ++lvl) {
+    bool few = false;
+    for (int lvl = 0; lvl < 7 && !few && pbits < 64; ++lvl) {
         // Key digits up to the key's last bit, then ~index digits.
         const int bits = pbits < 32 ? min(11, 32 - pbits) : min(11, 64 - pbits);
         const int nb = 1 << bits;
@@ -515,28 +518,67 @@ __device__ int cand_search(int n, Member member, MassOf mass_of, u64 theta, bool
         const int d = sh.found;
         if (d < 0) return -1;
         before = sh.before;
-        single = sh.count == 1;
+        few = sh.count <= 64;
         prefix = (prefix << bits) | (uint64_t)d;
         pbits += bits;
         __syncthreads();
     }
-    // The member in the found bin (a single one, or the one the full 64 bits name).
-    if (tid == 0) sh.found = -1;
+    // The found bin's members with mass, at most 64 (when all 64 bits are fixed, one), sorted
+    // descending in wave 0; the running mass from `before` crosses theta at one of them.
+    if (tid == 0) sh.nsmall = 0;
     __syncthreads();
     for (int i = tid; i < n; i += kRT) {
         const u64 c = sh.cand[i];
         const uint32_t key = (uint32_t)(c >> 32);
         if ((c >> (64 - pbits)) == prefix && member(key, (int)~(uint32_t)c) && mass_of(key_value(key))) {
+            const int slot = atomicAdd(&sh.nsmall, 1);
+            if (slot < 64) sh.sidx[slot] = i;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // Rank by counting (each lane reads every member, broadcast LDS reads), then running
+        // sums by reading the ranked masses: no cross-lane shuffles. sh.hist is free here.
+        const int ns = min(sh.nsmall, 64);
+        u64 c = 0, m = 0;
+        if (lane < ns) {
+            c = sh.cand[sh.sidx[lane]];
+            m = mass_of(key_value((uint32_t)(c >> 32)));
+            sh.hist[lane] = c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        for (int j = 0; j < ns; ++j) rank += sh.hist[j] > c ? 1 : 0;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ns) {
+            sh.hist[64 + rank] = m;
+            sh.hist[128 + rank] = c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        u64 in = before;
+        for (int j = 0; j <= lane && j < ns; ++j) in += sh.hist[64 + j];
+        m = lane < ns ? sh.hist[64 + lane] : 0;
+        c = lane < ns ? sh.hist[128 + lane] : 0;
+        const u64 ex = in - m;
+        const bool hit = m && (strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta));
+        const unsigned long long bal = __ballot(hit);
+        if (bal && lane == __ffsll((long long)bal) - 1) {
             sh.found = (int)~(uint32_t)c;
-            sh.mass = mass_of(key_value(key));
-            sh.before = (u64)key;  // handed over below
+            sh.before = ex;
+            sh.mass = m;
+            sh.wsum[0] = c >> 32;
+        } else if (!bal && lane == 0) {
+            sh.found = -1;
         }
     }
     __syncthreads();
     const int found = sh.found;
-    *key_out = (uint32_t)sh.before;
+    *key_out = (uint32_t)sh.wsum[0];
     *mass_out = sh.mass;
-    *before_out = before;
+    *before_out = sh.before;
     __syncthreads();
     return found;
 }
@@ -606,9 +648,6 @@ __device__ __forceinline__ float cblock_sum(float v, float* red) {
     return r;
 }
 
-// Largest float value whose order_key falls in histogram bin `bin` (the top 11 key bits).
-__device__ __forceinline__ float bin_top(int bin) { return key_value(((uint32_t)bin << 21) | 0x1FFFFFu); }
-
 // Copies rows that have a processor into the workspace: the mask (-inf where disallowed), then
 // the bias entries, then the penalty entries (worker.rs:142-181; the entries of one list name
 // distinct tokens). Grid (chunk, row).
@@ -643,16 +682,13 @@ __global__ __launch_bounds__(kCT) void sample_prepare_kernel(SampleArgs a) {
 
 // Pass 1, grid (chunk, row): per chunk of the processed row, {max z, sum exp(z - max z)} with
 // z = y * f32(1 / T) + 0, or {max y, its first index} for T <= 0. Rows with top-k or top-p also
-// report the chunk's non-empty bins of the top 11 bits of order_key(z): a count and, for top-p
-// alone, the sum of exp(z - bin_top) in 2^-20 units (relative to a fixed value of the bin, so
-// chunks add up without knowing the row's max; 32-bit sums keep the pass at 16 KiB of LDS).
-// These masses only choose the candidate bins: the cut itself is taken on the candidates.
+// list the chunk's candidates (threshold, count and (key << 32) | ~index entries) for the select
+// pass.
 __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
-    __shared__ uint32_t s_cnt[kBins];
-    __shared__ uint32_t s_mass[kBins];
     __shared__ float s_red[kCW];
     __shared__ int s_ired[kCW];
-    __shared__ uint32_t s_wn[kCW];
+    __shared__ uint32_t s_wn[3 * kCW];
+    __shared__ __align__(16) int s_wn4[32];
     const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* y = row_ptr(a, b);
     const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
@@ -715,306 +751,172 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
 
     const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
     if (!use_k && !use_p) return;
-    const bool mass = !use_k;  // top-p alone locates its cut by mass, top-k by count
-    // Top-p keeps a token only if p >= (1 - top_p) / V; with log Z >= this chunk's max m, a token
-    // with z <= m - ln(V / (1 - top_p)) is never kept (one nat of margin for rounding), so it
-    // needs no bin. The select pass takes the crossing target from Z itself, not from the bins.
-    const float skip_below = mass ? m - (logf((float)a.V / fmaxf(1.f - tp, 1e-30f)) + 1.f) : -__builtin_huge_valf();
-    for (int i = tid; i < kBins; i += kCT) {
-        s_cnt[i] = 0;
-        s_mass[i] = 0;
-    }
-    __syncthreads();
+    // The chunk's candidate list: every entry with z >= t, for a t that keeps the list within
+    // ccap entries. Counts over the block come from wave ballots (no atomics), two LDS slots per
+    // wave alternating so that each count needs one barrier.
+    int buf = 0;
+#if KYRO_COUNT_LANE
+    auto count_ge = [&](float t) -> int {
+        int n = 0;
 #pragma unroll
-    for (int i = 0; i < kCPer; ++i) {
-        if (chunk_index(v0, i, vec4) >= v1 || x[i] <= skip_below) continue;
-        const int bin = (int)(order_key(x[i]) >> 21);
-        atomicAdd(&s_cnt[bin], 1u);
-        if (mass) {
-            const float e = fast_exp2((x[i] - bin_top(bin)) * kLog2e);
-            if (e > 0.f && e <= 1.f) {
-                // At most 2^20 - 1 units a token (a token exactly at its bin's top would give
-                // 2^20), so 4096 of them stay below 2^32. The bin masses only choose candidates.
-                const uint32_t f = min((uint32_t)__float2uint_rn(e * kFixC), (uint32_t)kFixC - 1u);
-                if (f) atomicAdd(&s_mass[bin], f);
+        for (int i = 0; i < kCPer; ++i) n += x[i] >= t ? 1 : 0;
+        n += __builtin_amdgcn_update_dpp(0, n, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        n += __builtin_amdgcn_update_dpp(0, n, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        n += __builtin_amdgcn_update_dpp(0, n, 0x141, 0xF, 0xF, false);  // row_half_mirror
+        n += __builtin_amdgcn_update_dpp(0, n, 0x140, 0xF, 0xF, false);  // row_mirror
+        if ((lane & 15) == 0) s_wn4[buf * 16 + wave * 4 + (lane >> 4)] = n;
+        __syncthreads();
+        const int4* q = reinterpret_cast<const int4*>(s_wn4 + buf * 16);
+        const int4 q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+        const int tot = (q0.x + q0.y + q0.z + q0.w) + (q1.x + q1.y + q1.z + q1.w) + (q2.x + q2.y + q2.z + q2.w) +
+                        (q3.x + q3.y + q3.z + q3.w);
+        buf ^= 1;
+        return __builtin_amdgcn_readfirstlane(tot);
+    };
+#else
+    auto count_ge = [&](float t) -> int {
+        int n = 0;
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i) n += (int)__popcll(__ballot(x[i] >= t));
+        if (lane == 0) s_wn[buf * kCW + wave] = (uint32_t)n;
+        __syncthreads();
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) tot += (int)s_wn[buf * kCW + w];
+        buf ^= 1;
+        return __builtin_amdgcn_readfirstlane(tot);  // the same in every lane: keeps the searches scalar
+    };
+#endif
+    const float ninf = -__builtin_huge_valf();
+    const int cap = a.ccap;
+    // Thresholds on a grid below the chunk's max: t_j = m - j / 8, j < npts (at most 512: 64 nats).
+    auto grid_t = [&](int j) { return m - (float)j * 0.125f; };
+    // Largest j in [-1, npts) with count_ge(t_j) <= lim (count(t_-1) = 0); *c_lo / *c_hi get the
+    // counts at j and j + 1 (-1 when j + 1 = npts was never counted).
+    auto bisect = [&](int lim, int npts, int* c_lo, int* c_hi) {
+        int lo = -1, hi = npts, clo = 0, chi = -1;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            const int cm = count_ge(grid_t(mid));
+            if (cm <= lim) {
+                lo = mid;
+                clo = cm;
+            } else {
+                hi = mid;
+                chi = cm;
             }
         }
-    }
-    __syncthreads();
-    // The non-empty bins in bin order: thread t owns bins 8t .. 8t+7.
-    constexpr int kPerT = kBins / kCT;
-    uint32_t nz = 0;
-#pragma unroll
-    for (int j = 0; j < kPerT; ++j) nz += s_cnt[tid * kPerT + j] ? 1u : 0u;
-    uint32_t incl = nz;
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
-    if (lane == 63) s_wn[wave] = incl;
-    __syncthreads();
-    uint32_t pos = incl - nz, total = 0;
-    for (int w = 0; w < kCW; ++w) {
-        if (w < wave) pos += s_wn[w];
-        total += s_wn[w];
-    }
-    int* n_out = a.clist_n + (size_t)b * a.C + c;
-    if (total > (uint32_t)kListCap) {  // more distinct bins than a chunk may report
-        if (tid == 0) *n_out = -1;
-        return;
-    }
-    SampleBin* list = a.clist + ((size_t)b * a.C + c) * kListCap;
-#pragma unroll
-    for (int j = 0; j < kPerT; ++j) {
-        const int bin = tid * kPerT + j;
-        if (s_cnt[bin]) {
-            list[pos] = SampleBin{(uint32_t)bin, s_cnt[bin], s_mass[bin]};
-            ++pos;
+        *c_lo = clo;
+        *c_hi = chi;
+        return lo;
+    };
+    float thr = ninf;  // -inf: every finite entry (a complete list)
+    int cnt = -1;      // -1: no threshold keeps the list within cap
+    if (m == ninf) {
+        cnt = 0;  // nothing finite in the chunk
+    } else if (use_k) {
+        // Top-k (with or without top-p): the chunk's own k largest must be listed, so t is the
+        // highest grid threshold with at least k entries at or above it; a chunk with fewer
+        // than k entries that far up lists every finite entry.
+        const int fin = count_ge(-FLT_MAX);  // finite entries
+        int clo, chi;
+        const int j = bisect(k - 1, 512, &clo, &chi) + 1;
+        if (j < 512 && chi <= cap) {
+            thr = grid_t(j);
+            cnt = chi;
+        } else if (fin <= cap) {
+            cnt = fin;  // complete
         }
-    }
-    if (tid == 0) *n_out = (int)total;
-}
-
-// Pass 2, one workgroup per row: merges the chunk statistics. T <= 0: the first maximum. Plain
-// sampling: Z, the chunk where the running mass in index order reaches u Z, and the walk inside
-// it (worker.rs:352-360). Top-k / top-p: the row histogram, the candidate bins (down to the bin
-// holding the k-th token, or the bin holding the top-p crossing), and the row's plan for the
-// gather and final passes.
-__global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
-    __shared__ RowShared sh;
-    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int C = a.C;
-    const float T = a.temperature[b];
-    SamplePlan* plan = a.plan + b;
-    const float2 st = tid < C ? a.cstat[(size_t)b * C + tid] : make_float2(-__builtin_huge_valf(), 0.f);
-    // Bin-list lengths, loaded with the statistics (used by top-k / top-p rows only).
-    const int listn = (a.clist_n && tid < C) ? a.clist_n[(size_t)b * C + tid] : 0;
-    if (!(T > 0.f)) {
-        const int best = block_argmax(st.x, tid < C ? __float_as_int(st.y) : 0x7fffffff, sh);
-        if (tid == 0) {
-            a.out[b] = (uint32_t)(best == 0x7fffffff ? 0 : best);
-            plan->mode = SAMPLE_DONE;
-        }
-        return;
-    }
-    const float M = block_max_f(st.x, sh);
-    if (M == -__builtin_huge_valf()) {  // every token disallowed
-        if (tid == 0) {
-            a.out[b] = (uint32_t)(a.V - 1);
-            plan->mode = SAMPLE_DONE;
-        }
-        return;
-    }
-    // Chunk masses exp(z - M) in chunk order: thread t holds chunk t; inclusive scan gives Z.
-    const float w = (tid < C && st.x != -__builtin_huge_valf()) ? st.y * fast_exp2((st.x - M) * kLog2e) : 0.f;
-    const float winc = wave_incl_scan_f(w);
-    if (lane == 63) sh.fred[wave] = winc;
-    __syncthreads();
-    float cbase = 0.f, Z = 0.f;
-    for (int q = 0; q < kRW; ++q) {
-        if (q < wave) cbase += sh.fred[q];
-        Z += sh.fred[q];
-    }
-    const float cum = cbase + winc;  // running mass through chunk tid
-    __syncthreads();
-    const int k = a.top_k ? a.top_k[b] : 0;
-    const float tp = a.top_p ? a.top_p[b] : 1.0f;
-    const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
-    const float sc = (float)(1.0 / (double)T);
-    if (!use_k && !use_p) {
-        const float rr = a.u[b] * Z;
-        if (tid == 0) sh.found = 0x7fffffff;
-        __syncthreads();
-        if (tid < C && cum >= rr && (tid == 0 || cum - w < rr)) atomicMin(&sh.found, tid);
-        __syncthreads();
-        const int cs = sh.found == 0x7fffffff ? C - 1 : sh.found;
-        __syncthreads();
-        if (tid == cs) sh.fred[0] = cum - w;  // mass before the crossing chunk
-        __syncthreads();
-        const float rem = rr - sh.fred[0];
-        // Walk chunk cs in index order: thread t owns the 4 consecutive entries 4t .. 4t+3.
-        const float* y = row_ptr(a, b);
-        const int v0 = cs * kChunk, v1 = min(a.V, v0 + kChunk);
-        const int v = v0 + 4 * tid;
-        float e[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = v + j < v1 ? fast_exp2((y[v + j] * sc + 0.0f - M) * kLog2e) : 0.f;
-        const float mine = (e[0] + e[1]) + (e[2] + e[3]);
-        const float inc = wave_incl_scan_f(mine);
-        if (lane == 63) sh.fred[wave] = inc;
-        __syncthreads();
-        float base = inc - mine;
-        for (int q = 0; q < wave; ++q) base += sh.fred[q];
-        if (tid == 0) sh.found = 0x7fffffff;
-        __syncthreads();
-        if (v < v1 && base < rem && base + mine >= rem) {  // this thread's four hold the crossing
-            float run = base;
-            int pick = -1;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                run += e[j];
-                if (pick < 0 && v + j < v1 && run >= rem) pick = v + j;
-            }
-            atomicMin(&sh.found, pick >= 0 ? pick : min(v + 3, v1 - 1));  // rounding can make two threads claim it
-        } else if (tid == 0 && rem <= 0.f) {
-            atomicMin(&sh.found, v0);
-        }
-        __syncthreads();
-        if (tid == 0 && sh.found == 0x7fffffff) sh.found = -1;
-        __syncthreads();
-        if (tid == 0) {
-            a.out[b] = (uint32_t)(sh.found >= 0 ? sh.found : a.V - 1);
-            plan->mode = SAMPLE_DONE;
-        }
-        return;
-    }
-    // Row histogram from the chunks' bin lists; masses are converted to exp(z - M) units per bin.
-    for (int i = tid; i < kBins; i += kRT) {
-        sh.cnt[i] = 0;
-        sh.hist[i] = 0;
-    }
-    if (tid == 0) sh.count = 0;
-    // Wave w merges the lists of chunks w, w + 16, ...
-    int* s_n = reinterpret_cast<int*>(sh.cum);
-    if (tid < C) {
-        s_n[tid] = listn;
-        if (listn < 0) sh.count = 1;  // a chunk overflowed its list
-    }
-    __syncthreads();
-    for (int c = wave; c < C; c += kRW) {
-        const int n = s_n[c];
-        const SampleBin* list = a.clist + ((size_t)b * C + c) * kListCap;
-        for (int j = lane; j < n; j += 64) {
-            const SampleBin e = list[j];
-            atomicAdd(&sh.cnt[e.bin], e.count);
-            if (e.mass) atomicAdd(&sh.hist[e.bin], (u64)e.mass);
-        }
-    }
-    __syncthreads();
-    const bool overflow = sh.count != 0;
-    const bool mass = !use_k;
-    if (mass) {  // to exp(z - M) in 2^-40 units
-        for (int i = tid; i < kBins; i += kRT)
-            if (sh.hist[i]) {
-                const float f = fast_exp2((bin_top(i) - M) * kLog2e);
-                sh.hist[i] = (u64)llrint((double)sh.hist[i] * (double)f * (kFixE / (double)kFixC));
-            }
-        __syncthreads();
-    }
-    int tb;
-    if (use_k) {
-        tb = desc_bin_search(sh.cnt, (u64)k, false, sh);
     } else {
-        // The bin holding the crossing of tp Z (the stats pass leaves out of the bins only tokens
-        // that top-p never keeps, all below the cut). Its mass is rounded differently from the
-        // candidates' own sums: should the exact cut fall below it, the final pass finds no cut
-        // among the candidates and runs the radix path.
-        const u64 tot = (u64)llrint((double)Z * kFixE);
-        tb = desc_bin_search(sh.hist, (u64)llrint((double)tp * (double)tot), true, sh);
-    }
-    u64 ncand = ~0ull;
-    if (tb >= 0) {
-        u64 cn = 0;
-        for (int i = tb + lane; i < kBins; i += 64) cn += sh.cnt[i];
-        ncand = wave_sum_u64(cn);
+        // Top-p alone keeps a token only if p >= (1 - top_p) / V; with log Z >= this chunk's
+        // max m, a token with z < m - ln(V / (1 - top_p)) is never kept (one nat of margin for
+        // rounding), so the list starts there if it fits, else at the lowest grid threshold
+        // that fits. The select pass checks that the lists reach below the cut.
+        const float span = logf((float)a.V / fmaxf(1.f - tp, 1e-30f)) + 1.f;
+        const float skip = m - span;
+        const int cs = count_ge(skip);
+        if (cs <= cap) {
+            thr = skip;
+            cnt = cs;
+        } else {
+            int clo, chi;
+            // grid points above the skip bound only: below it every count exceeds the cap
+            const int j = bisect(min(cap, KYRO_SAMPLE_P_TARGET), min(512, (int)ceilf(span * 8.f)), &clo, &chi);
+            if (j >= 0) {
+                thr = grid_t(j);
+                cnt = clo;
+            }
+        }
     }
     if (tid == 0) {
-        SamplePlan pl;
-        pl.mode = (overflow || tb < 0 || ncand > (u64)kCap) ? SAMPLE_RADIX : SAMPLE_CAND;
-        pl.tb = tb;
-        pl.m = M;
-        pl.z = Z;
-        pl.ncand = (int)(ncand > (u64)kCap ? kCap + 1 : ncand);
-        pl.count = 0;
-        *plan = pl;
+        a.cthr[(size_t)b * a.C + c] = thr;
+        a.ccount[(size_t)b * a.C + c] = cnt;
     }
-}
-
-// Pass 3, grid (chunk, row): rows on the candidate path append their tokens in the candidate
-// bins to the row's list (one atomic per workgroup; the list's order is settled by the sort).
-__global__ __launch_bounds__(kCT) void sample_gather_kernel(SampleArgs a) {
-    __shared__ uint32_t s_wn[kCW];
-    __shared__ int s_base;
-    const int c = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float* y = row_ptr(a, b);
-    const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
-    const bool vec4 = a.vec4;
-    float x[kCPer];
-    load_chunk(y, v0, v1, vec4, x);  // issued with the plan's load; dropped when not needed
-    SamplePlan* plan = a.plan + b;
-    if (plan->mode != SAMPLE_CAND) return;
-    const uint32_t tb = (uint32_t)plan->tb;
-    const float sc = (float)(1.0 / (double)a.temperature[b]);
-    uint32_t keys[kCPer];
-    uint32_t hits = 0;  // bit i: entry i is a candidate
+    if (cnt <= 0) return;
+    // Write the list: a block scan of the per-thread hits places every entry.
+    const float tw = thr == ninf ? -FLT_MAX : thr;
+    uint32_t hits = 0;
 #pragma unroll
-    for (int i = 0; i < kCPer; ++i) {
-        keys[i] = order_key(x[i] * sc + 0.0f);
-        if (chunk_index(v0, i, vec4) < v1 && (keys[i] >> 21) >= tb) hits |= 1u << i;
-    }
-    // One atomic per workgroup: a block scan of the per-thread counts places every candidate.
+    for (int i = 0; i < kCPer; ++i)
+        if (x[i] >= tw) hits |= 1u << i;
     const uint32_t mine = (uint32_t)__popc(hits);
     uint32_t incl = mine;
     for (int o = 1; o < 64; o <<= 1) {
         const uint32_t t = __shfl_up(incl, o, 64);
         if (lane >= o) incl += t;
     }
-    if (lane == 63) s_wn[wave] = incl;
+    if (lane == 63) s_wn[2 * kCW + wave] = incl;
     __syncthreads();
-    uint32_t off = incl - mine, total = 0;
-    for (int w = 0; w < kCW; ++w) {
-        if (w < wave) off += s_wn[w];
-        total += s_wn[w];
-    }
-    if (total == 0) return;
-    if (threadIdx.x == 0) s_base = atomicAdd(&plan->count, (int)total);
-    __syncthreads();
-    u64* cand = a.cand + (size_t)b * kCap;
-    int slot = s_base + (int)off;
+    uint32_t off = incl - mine;
+    for (int w = 0; w < wave; ++w) off += s_wn[2 * kCW + w];
+    u64* list = a.cand + (size_t)b * kCap + (size_t)c * cap;
 #pragma unroll
     for (int i = 0; i < kCPer; ++i)
         if (hits & (1u << i)) {
-            if (slot < kCap) cand[slot] = ((u64)keys[i] << 32) | (uint32_t)~(uint32_t)chunk_index(v0, i, vec4);
-            ++slot;
+            list[off] = ((u64)order_key(x[i]) << 32) | (uint32_t)~(uint32_t)chunk_index(v0, i, vec4);
+            ++off;
         }
 }
 
-// Pass 4, one workgroup per row on the candidate or radix path: sorts the candidates (key
-// descending, index ascending), applies top-k / top-p in that order and walks the kept set; rows
-// whose candidates do not settle the cut run exact radix selects over the whole row.
-__global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
-    __shared__ RowShared sh;
-    const int b = blockIdx.x, tid = threadIdx.x;
-    const SamplePlan pl = a.plan[b];
-    if (pl.mode == SAMPLE_DONE) return;
+// Settles a top-k / top-p row (worker.rs:300-360) from n candidates in sh.cand (n < 0: none):
+// the k largest for top-k, or for top-p alone every token with key >= kmin (more below it may be
+// present). Candidates sort or are searched in descending order (key descending, index
+// ascending); a row whose candidates do not settle the cut runs exact radix selects over the
+// whole row: three passes (11 + 11 + 10 bits) of mass histograms in LDS (64-bit fixed point,
+// 2^-52 resolution, so the sums do not depend on thread order), then a pass in index order for
+// ties between equal keys.
+__device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared& sh, int n, float M, float Z, uint32_t kmin,
+                           float T, int k, float tp, float u, int cp_bits, uint64_t cp) {
+    const int tid = threadIdx.x;
     const int V = a.V;
-    const float T = a.temperature[b];
     Row r;
     r.y = row_ptr(a, b);
     r.V = V;
     r.vec4 = a.vec4;
     r.s = (float)(1.0 / (double)T);
-    r.m = pl.m;
-    r.z_sum = pl.z;
+    r.m = M;
+    r.z_sum = Z;
     r.kk = 0;
     r.ki = V;
     r.ck = 0;
     r.ci = V;
-    const int k = a.top_k ? a.top_k[b] : 0;
-    const float tp = a.top_p ? a.top_p[b] : 1.0f;
     const bool use_k = k > 0 && k < V;
     const bool use_p = tp < 1.0f;
-    const float u = a.u[b];
-    if (pl.mode == SAMPLE_CAND && min(pl.count, kCap) <= kSortMax) {
+    if (n >= 0 && n <= kSortMax) {
         // Few candidates: sorted in LDS, then cut and walked with running sums.
-        const int n = min(pl.count, kCap);
         int np2 = 2;
         while (np2 < n) np2 <<= 1;
-        const u64* cand = a.cand + (size_t)b * kCap;
-        for (int i = tid; i < np2; i += kRT) sh.cand[i] = i < n ? cand[i] : 0;
+        for (int i = n + tid; i < np2; i += kRT) sh.cand[i] = 0;
         __syncthreads();
         bitonic_desc(sh.cand, np2);
-        const int ns = use_k ? min(k, n) : n;
+        // Top-p alone: the lists are complete only at keys >= kmin (sorted to the front).
+        int ncov = n;
+        if (kmin) {
+            int nb = 0;
+            for (int i = tid; i < n; i += kRT) nb += (uint32_t)(sh.cand[i] >> 32) < kmin ? 1 : 0;
+            ncov = n - block_sum_i(nb, sh);
+        }
+        const int ns = use_k ? min(k, n) : ncov;
         auto cz = [&](int i) { return key_value((uint32_t)(sh.cand[i] >> 32)); };
         float zsum = r.z_sum;
         if (use_k) {  // the kept set is the first k candidates
@@ -1031,7 +933,7 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
             cut = first_at_least(sh.cum, ns, tp, true, sh);  // first running sum above top_p
             if (cut < 0) cut = ns;
             else cut += 1;
-            if (!use_k && cut == ns && n < V) cut = -1;  // the cut lies past the candidates
+            if (!use_k && cut == ns && ncov < V) cut = -1;  // the cut may lie past the candidates
             if (cut > 0) rr = u * sh.cum[cut - 1];
         }
         if (cut > 0) {
@@ -1041,16 +943,10 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
             return;
         }
     }
-    if (pl.mode == SAMPLE_CAND && min(pl.count, kCap) > kSortMax) {
+    if (n > kSortMax) {
         // The same searches as the row path below, over the candidates: they hold the row's k
-        // largest (top-k) or every token at or above the bin of the top-p crossing.
-        const int n = min(pl.count, kCap);
-        const u64* cand = a.cand + (size_t)b * kCap;
-        for (int i = tid; i < n; i += kRT) sh.cand[i] = cand[i];
-        __syncthreads();
-        int cp_bits;
-        uint64_t cp;
-        cand_common_prefix(n, sh, &cp_bits, &cp);
+        // largest (top-k) or, for top-p alone, every token with key >= kmin; cp_bits / cp is the
+        // prefix the keys of every candidate at or above kmin share.
         auto every = [](uint32_t, int) { return true; };
         auto unit = [](float) -> u64 { return 1; };
         u64 bf, ms;
@@ -1068,7 +964,7 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
             }
             r.z_sum = block_sum_f(zs, sh);
         }
-        auto kept = [&](uint32_t kc, int v) { return r.kept(kc, v); };
+        auto kept = [&](uint32_t kc, int v) { return kc >= kmin && r.kept(kc, v); };
         auto pmass = [&](float zv) -> u64 { return fix_mass(r.prob(zv)); };
         u64 total = (u64)llrint(kFix);
         float rr = u;
@@ -1079,8 +975,8 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
                 r.ck = key;
                 r.ci = cut;
                 total = bf + ms;
-            } else if (!use_k && n < V) {
-                settled = false;  // the cut lies past the candidates: the row path finds it
+            } else if (!use_k) {
+                settled = false;  // the cut may lie past the candidates: the row path finds it
             } else {  // the running sum never exceeds top_p: the whole kept set
                 float ts = 0.f;
                 for (int i = tid; i < n; i += kRT) {
@@ -1104,7 +1000,7 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
         r.ki = V;
         r.ck = 0;
         r.ci = V;
-        r.z_sum = pl.z;
+        r.z_sum = Z;
     }
     // Radix selects over the whole row (candidates did not fit in LDS, or did not settle the cut).
     auto all = [](uint32_t, int) { return true; };
@@ -1161,6 +1057,156 @@ __global__ __launch_bounds__(kRT) void sample_final_kernel(SampleArgs a) {
     if (tid == 0) a.out[b] = (uint32_t)(pick >= 0 && pick < V ? pick : V - 1);
 }
 
+// Pass 2, one workgroup per row: merges the chunk statistics. T <= 0: the first maximum. Plain
+// sampling: Z, the chunk where the running mass in index order reaches u Z, and the walk inside
+// it (worker.rs:352-360). Top-k / top-p: the chunks' candidate lists, gathered into LDS when they
+// cover the kept set, then finish_row.
+__global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
+    __shared__ RowShared sh;
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int C = a.C;
+    // Every per-row input in one round of loads, issued with the chunk statistics.
+    const float T = a.temperature[b];
+    const int k = a.top_k ? a.top_k[b] : 0;
+    const float tp = a.top_p ? a.top_p[b] : 1.0f;
+    const float u = a.u[b];
+    const float2 st = tid < C ? a.cstat[(size_t)b * C + tid] : make_float2(-__builtin_huge_valf(), 0.f);
+    // List lengths and thresholds, loaded with the statistics (top-k / top-p rows only).
+    const int listn = (a.ccount && tid < C) ? a.ccount[(size_t)b * C + tid] : 0;
+    const float thr = (a.cthr && tid < C) ? a.cthr[(size_t)b * C + tid] : 0.f;
+    if (!(T > 0.f)) {
+        const int best = block_argmax(st.x, tid < C ? __float_as_int(st.y) : 0x7fffffff, sh);
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(best == 0x7fffffff ? 0 : best);
+        }
+        return;
+    }
+    const float M = block_max_f(st.x, sh);
+    if (M == -__builtin_huge_valf()) {  // every token disallowed
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(a.V - 1);
+        }
+        return;
+    }
+    // Chunk masses exp(z - M) in chunk order: thread t holds chunk t; inclusive scan gives Z.
+    const float w = (tid < C && st.x != -__builtin_huge_valf()) ? st.y * fast_exp2((st.x - M) * kLog2e) : 0.f;
+    const float winc = wave_incl_scan_f(w);
+    if (lane == 63) sh.fred[wave] = winc;
+    __syncthreads();
+    float cbase = 0.f, Z = 0.f;
+    for (int q = 0; q < kRW; ++q) {
+        if (q < wave) cbase += sh.fred[q];
+        Z += sh.fred[q];
+    }
+    const float cum = cbase + winc;  // running mass through chunk tid
+    __syncthreads();
+    const bool use_k = k > 0 && k < a.V, use_p = tp < 1.0f;
+    const float sc = (float)(1.0 / (double)T);
+    if (!use_k && !use_p) {
+        const float rr = u * Z;
+        if (tid == 0) sh.found = 0x7fffffff;
+        __syncthreads();
+        if (tid < C && cum >= rr && (tid == 0 || cum - w < rr)) atomicMin(&sh.found, tid);
+        __syncthreads();
+        const int cs = sh.found == 0x7fffffff ? C - 1 : sh.found;
+        __syncthreads();
+        if (tid == cs) sh.fred[0] = cum - w;  // mass before the crossing chunk
+        __syncthreads();
+        const float rem = rr - sh.fred[0];
+        // Walk chunk cs in index order: thread t owns the 4 consecutive entries 4t .. 4t+3.
+        const float* y = row_ptr(a, b);
+        const int v0 = cs * kChunk, v1 = min(a.V, v0 + kChunk);
+        const int v = v0 + 4 * tid;
+        float e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = v + j < v1 ? fast_exp2((y[v + j] * sc + 0.0f - M) * kLog2e) : 0.f;
+        const float mine = (e[0] + e[1]) + (e[2] + e[3]);
+        const float inc = wave_incl_scan_f(mine);
+        if (lane == 63) sh.fred[wave] = inc;
+        __syncthreads();
+        float base = inc - mine;
+        for (int q = 0; q < wave; ++q) base += sh.fred[q];
+        if (tid == 0) sh.found = 0x7fffffff;
+        __syncthreads();
+        if (v < v1 && base < rem && base + mine >= rem) {  // this thread's four hold the crossing
+            float run = base;
+            int pick = -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                run += e[j];
+                if (pick < 0 && v + j < v1 && run >= rem) pick = v + j;
+            }
+            atomicMin(&sh.found, pick >= 0 ? pick : min(v + 3, v1 - 1));  // rounding can make two threads claim it
+        } else if (tid == 0 && rem <= 0.f) {
+            atomicMin(&sh.found, v0);
+        }
+        __syncthreads();
+        if (tid == 0 && sh.found == 0x7fffffff) sh.found = -1;
+        __syncthreads();
+        if (tid == 0) {
+            a.out[b] = (uint32_t)(sh.found >= 0 ? sh.found : a.V - 1);
+        }
+        return;
+    }
+    // Top-k / top-p: the chunks' candidate lists (offsets in sh.cnt[kSampleMaxChunks + c]).
+    const int cnt = tid < C ? listn : 0;
+    const bool ok = tid >= C || (cnt >= 0 && (!use_k || thr == -__builtin_huge_valf() || cnt >= k));
+    const bool all_ok = __syncthreads_and(ok) != 0;
+    const int cpos = cnt > 0 ? cnt : 0;
+    const int cinc = wave_incl_scan_i(cpos);
+    if (lane == 63) sh.ired[wave] = cinc;
+    __syncthreads();
+    int coff = cinc - cpos, n = 0;
+    for (int q = 0; q < kRW; ++q) {
+        if (q < wave) coff += sh.ired[q];
+        n += sh.ired[q];
+    }
+    if (tid < C) {
+        sh.cnt[tid] = (uint32_t)cpos;
+        sh.cnt[kSampleMaxChunks + tid] = (uint32_t)coff;
+    }
+    // Top-p alone: every list reaches down to its threshold, so all of them hold every token at
+    // or above the largest one.
+    const float tmax = use_k ? -__builtin_huge_valf() : block_max_f(tid < C ? thr : -__builtin_huge_valf(), sh);
+    const bool covered = all_ok && n <= kCap && (!use_k || n >= k);
+    const uint32_t kmin = (!use_k && tmax != -__builtin_huge_valf()) ? order_key(tmax) : 0u;
+    // Copy the lists into LDS: kRT / C threads per chunk, each with at most 16 entries (C x ccap
+    // <= kCap), loaded eight at a time before any is stored. The keys at or above kmin give the
+    // searches their shared prefix.
+    uint32_t klo = 0xffffffffu, khi = 0u;
+    if (covered) {
+        const int tpc = kRT / C, c = tid / tpc, sub = tid - c * tpc;
+        if (c < C) {
+            const int nc = (int)sh.cnt[c], oc = (int)sh.cnt[kSampleMaxChunks + c];
+            const u64* src = a.cand + (size_t)b * kCap + (size_t)c * a.ccap;
+            for (int q0 = 0; q0 < 16 && sub + q0 * tpc < nc; q0 += 8) {
+                u64 e[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int j = sub + (q0 + q) * tpc;
+                    e[q] = j < nc ? src[j] : 0;
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int j = sub + (q0 + q) * tpc;
+                    if (j < nc) {
+                        sh.cand[oc + j] = e[q];
+                        const uint32_t key = (uint32_t)(e[q] >> 32);
+                        if (key >= kmin) {
+                            klo = min(klo, key);
+                            khi = max(khi, key);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    int cp_bits;
+    uint64_t cp;
+    key_range_prefix(klo, khi, sh, &cp_bits, &cp);  // its barriers also order the copies
+    finish_row(a, b, sh, covered ? n : -1, M, Z, kmin, T, k, tp, u, cp_bits, cp);
+}
+
 }  // namespace
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
@@ -1169,10 +1215,6 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.bias_off || a.pen_off || a.mask_row) sample_prepare_kernel<<<grid, kCT, 0, stream>>>(a);
     sample_stats_kernel<<<grid, kCT, 0, stream>>>(a);
     sample_select_kernel<<<dim3((unsigned)a.B), kRT, 0, stream>>>(a);
-    if (a.top_k || a.top_p) {
-        sample_gather_kernel<<<grid, kCT, 0, stream>>>(a);
-        sample_final_kernel<<<dim3((unsigned)a.B), kRT, 0, stream>>>(a);
-    }
     return hipGetLastError();
 }
 

@@ -1,5 +1,6 @@
 // C ABI of the plain-decode sampler (include/kyro_sample.h): argument checks, the workspace for
 // processed rows, and the host-side penalty vector.
+#include <algorithm>
 #include <cmath>
 #include <map>
 
@@ -55,28 +56,30 @@ int kyro_sample_tokens(kyro_ctx ctx, const kyro_sample_params* p, const float* l
             return fail(KYRO_EUNSUPPORTED, "sample_tokens: vocab_size %d > %d", p->vocab_size,
                         kyro::kSampleMaxChunks * kyro::kSampleChunk);
         // Arena: processed rows (when a processor is given), chunk statistics, and for top-k /
-        // top-p the chunks' bin lists, the row plans and the candidate lists.
+        // top-p the chunks' thresholds, counts and candidate lists.
         const bool filtered = top_p || top_k;
         const size_t ws_b = (bias_offsets || penalty_offsets || mask_row) ? align_up((size_t)a.B * a.V * sizeof(float), 256) : 0;
         const size_t cstat_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
-        const size_t plan_b = align_up((size_t)a.B * sizeof(kyro::SamplePlan), 256);
-        const size_t list_b = filtered ? align_up((size_t)a.B * a.C * kyro::kSampleListCap * sizeof(kyro::SampleBin), 256) : 0;
-        const size_t listn_b = filtered ? align_up((size_t)a.B * a.C * sizeof(int), 256) : 0;
+        const size_t thr_b = filtered ? align_up((size_t)a.B * a.C * sizeof(float), 256) : 0;
+        const size_t cnt_b = filtered ? align_up((size_t)a.B * a.C * sizeof(int), 256) : 0;
         const size_t cand_b = filtered ? align_up((size_t)a.B * kyro::kSampleCand * sizeof(unsigned long long), 256) : 0;
+        a.ccap = std::min(kyro::kSampleChunkCand, kyro::kSampleCand / a.C);
+        // The select pass copies a chunk's list with 1024 / C threads, at most 16 entries each
+        // (true for every C up to kSampleMaxChunks).
+        if ((a.ccap + 1024 / a.C - 1) / (1024 / a.C) > 16)
+            return fail(KYRO_EUNSUPPORTED, "sample_tokens: %d chunks leave too few copy threads", a.C);
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        if (int rc = ensure_arena(ctx, ws_b + cstat_b + plan_b + list_b + listn_b + cand_b)) return rc;
+        if (int rc = ensure_arena(ctx, ws_b + cstat_b + thr_b + cnt_b + cand_b)) return rc;
         char* base = static_cast<char*>(ctx->arena);
         a.ws = ws_b ? reinterpret_cast<float*>(base) : nullptr;
         base += ws_b;
         a.cstat = reinterpret_cast<float2*>(base);
         base += cstat_b;
-        a.plan = reinterpret_cast<kyro::SamplePlan*>(base);
-        base += plan_b;
-        a.clist = list_b ? reinterpret_cast<kyro::SampleBin*>(base) : nullptr;
-        base += list_b;
-        a.clist_n = listn_b ? reinterpret_cast<int*>(base) : nullptr;
-        base += listn_b;
+        a.cthr = thr_b ? reinterpret_cast<float*>(base) : nullptr;
+        base += thr_b;
+        a.ccount = cnt_b ? reinterpret_cast<int*>(base) : nullptr;
+        base += cnt_b;
         a.cand = cand_b ? reinterpret_cast<unsigned long long*>(base) : nullptr;
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_sample(a, ctx->stream));
