@@ -73,24 +73,33 @@ __device__ __forceinline__ uint32_t order_key(float z) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ u64 shfl_up_u64(u64 x, int o) {
-    const uint32_t lo = __shfl_up((uint32_t)x, o, 64);
-    const uint32_t hi = __shfl_up((uint32_t)(x >> 32), o, 64);
-    return ((u64)hi << 32) | lo;
-}
-
 __device__ __forceinline__ u64 shfl_xor_u64(u64 x, int o) {
     const uint32_t lo = __shfl_xor((uint32_t)x, o, 64);
     const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), o, 64);
     return ((u64)hi << 32) | lo;
 }
 
+// Inclusive wave scans with DPP: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast:15
+// (rows 1 and 3 add lane 15 of the row before) and row_bcast:31 (rows 2 and 3 add lane 31).
+// Lanes a DPP source does not reach add 0. STEP(ctrl, row_mask) adds one shifted copy.
+#define KYRO_DPP(v, ctrl, rmask) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rmask), 0xf, false)
+#define KYRO_DPP_SCAN(STEP) \
+    STEP(0x111, 0xf);       \
+    STEP(0x112, 0xf);       \
+    STEP(0x114, 0xf);       \
+    STEP(0x118, 0xf);       \
+    STEP(0x142, 0xa);       \
+    STEP(0x143, 0xc)
+
 __device__ __forceinline__ u64 wave_incl_scan_u64(u64 x) {
-    const int lane = threadIdx.x & 63;
-    for (int o = 1; o < 64; o <<= 1) {
-        const u64 y = shfl_up_u64(x, o);
-        if (lane >= o) x += y;
+#define KYRO_STEP_U64(ctrl, rmask)                                                   \
+    {                                                                                \
+        const uint32_t lo = (uint32_t)KYRO_DPP((int)(uint32_t)x, ctrl, rmask);       \
+        const uint32_t hi = (uint32_t)KYRO_DPP((int)(uint32_t)(x >> 32), ctrl, rmask); \
+        x += ((u64)hi << 32) | lo;                                                   \
     }
+    KYRO_DPP_SCAN(KYRO_STEP_U64);
+#undef KYRO_STEP_U64
     return x;
 }
 
@@ -100,20 +109,16 @@ __device__ __forceinline__ u64 wave_sum_u64(u64 x) {
 }
 
 __device__ __forceinline__ float wave_incl_scan_f(float x) {
-    const int lane = threadIdx.x & 63;
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+#define KYRO_STEP_F(ctrl, rmask) x += __int_as_float(KYRO_DPP(__float_as_int(x), ctrl, rmask))
+    KYRO_DPP_SCAN(KYRO_STEP_F);
+#undef KYRO_STEP_F
     return x;
 }
 
 __device__ __forceinline__ int wave_incl_scan_i(int x) {
-    const int lane = threadIdx.x & 63;
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o, 64);
-        if (lane >= o) x += y;
-    }
+#define KYRO_STEP_I(ctrl, rmask) x += KYRO_DPP(x, ctrl, rmask)
+    KYRO_DPP_SCAN(KYRO_STEP_I);
+#undef KYRO_STEP_I
     return x;
 }
 
@@ -860,11 +865,7 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     for (int i = 0; i < kCPer; ++i)
         if (x[i] >= tw) hits |= 1u << i;
     const uint32_t mine = (uint32_t)__popc(hits);
-    uint32_t incl = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
-    }
+    const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
     if (lane == 63) s_wn[2 * kCW + wave] = incl;
     __syncthreads();
     uint32_t off = incl - mine;
