@@ -42,14 +42,53 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// DPP copy of v from another lane (ctrl: a DPP control code, rmask: the 16-lane rows written);
+// lanes whose source lies outside the row, or rows outside rmask, get 0.
+#define KYRO_DPP(v, ctrl, rmask) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rmask), 0xf, false)
+
+// Inclusive wave scans with DPP: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast:15
+// (rows 1 and 3 add lane 15 of the row before) and row_bcast:31 (rows 2 and 3 add lane 31).
+// STEP(ctrl, rmask) adds one shifted copy.
+#define KYRO_DPP_SCAN(STEP) \
+    STEP(0x111, 0xf);       \
+    STEP(0x112, 0xf);       \
+    STEP(0x114, 0xf);       \
+    STEP(0x118, 0xf);       \
+    STEP(0x142, 0xa);       \
+    STEP(0x143, 0xc)
+
+__device__ __forceinline__ float wave_incl_scan_f(float x) {
+#define KYRO_STEP_F(ctrl, rmask) x += __int_as_float(KYRO_DPP(__float_as_int(x), ctrl, rmask))
+    KYRO_DPP_SCAN(KYRO_STEP_F);
+#undef KYRO_STEP_F
+    return x;
+}
+
+__device__ __forceinline__ int wave_incl_scan_i(int x) {
+#define KYRO_STEP_I(ctrl, rmask) x += KYRO_DPP(x, ctrl, rmask)
+    KYRO_DPP_SCAN(KYRO_STEP_I);
+#undef KYRO_STEP_I
+    return x;
+}
+
+// Lane l's float as a scalar (the builtin is typed int: the bits move, not a converted value).
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Wave reductions: the 16-lane rows with DPP, then the four row results read as scalars (every
+// lane gets the same value).
 __device__ __forceinline__ float wave_max(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
+    v = fmaxf(v, __int_as_float(KYRO_DPP(__float_as_int(v), 0xB1, 0xF)));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, __int_as_float(KYRO_DPP(__float_as_int(v), 0x4E, 0xF)));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, __int_as_float(KYRO_DPP(__float_as_int(v), 0x141, 0xF)));  // row_half_mirror
+    v = fmaxf(v, __int_as_float(KYRO_DPP(__float_as_int(v), 0x140, 0xF)));  // row_mirror
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
+    v = row16_sum(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 __device__ __forceinline__ uint4 load16(const void* p) { return *reinterpret_cast<const uint4*>(p); }

@@ -73,24 +73,7 @@ __device__ __forceinline__ uint32_t order_key(float z) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ u64 shfl_xor_u64(u64 x, int o) {
-    const uint32_t lo = __shfl_xor((uint32_t)x, o, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), o, 64);
-    return ((u64)hi << 32) | lo;
-}
-
-// Inclusive wave scans with DPP: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast:15
-// (rows 1 and 3 add lane 15 of the row before) and row_bcast:31 (rows 2 and 3 add lane 31).
-// Lanes a DPP source does not reach add 0. STEP(ctrl, row_mask) adds one shifted copy.
-#define KYRO_DPP(v, ctrl, rmask) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rmask), 0xf, false)
-#define KYRO_DPP_SCAN(STEP) \
-    STEP(0x111, 0xf);       \
-    STEP(0x112, 0xf);       \
-    STEP(0x114, 0xf);       \
-    STEP(0x118, 0xf);       \
-    STEP(0x142, 0xa);       \
-    STEP(0x143, 0xc)
-
+// Inclusive u64 wave scan with the DPP steps of wave_incl_scan_f (both halves move together).
 __device__ __forceinline__ u64 wave_incl_scan_u64(u64 x) {
 #define KYRO_STEP_U64(ctrl, rmask)                                                   \
     {                                                                                \
@@ -103,23 +86,62 @@ __device__ __forceinline__ u64 wave_incl_scan_u64(u64 x) {
     return x;
 }
 
+// Wave sum: the 16-lane rows with DPP, then the four row totals read as scalars.
 __device__ __forceinline__ u64 wave_sum_u64(u64 x) {
-    for (int o = 32; o >= 1; o >>= 1) x += shfl_xor_u64(x, o);
-    return x;
+#define KYRO_RSTEP_U64(ctrl)                                                         \
+    {                                                                                \
+        const uint32_t lo = (uint32_t)KYRO_DPP((int)(uint32_t)x, ctrl, 0xf);         \
+        const uint32_t hi = (uint32_t)KYRO_DPP((int)(uint32_t)(x >> 32), ctrl, 0xf); \
+        x += ((u64)hi << 32) | lo;                                                   \
+    }
+    KYRO_RSTEP_U64(0xB1);   // quad_perm [1,0,3,2]
+    KYRO_RSTEP_U64(0x4E);   // quad_perm [2,3,0,1]
+    KYRO_RSTEP_U64(0x141);  // row_half_mirror
+    KYRO_RSTEP_U64(0x140);  // row_mirror
+#undef KYRO_RSTEP_U64
+    auto lane_u64 = [&](int l) {
+        return ((u64)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), l) << 32) |
+               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, l);
+    };
+    return (lane_u64(0) + lane_u64(16)) + (lane_u64(32) + lane_u64(48));
 }
 
-__device__ __forceinline__ float wave_incl_scan_f(float x) {
-#define KYRO_STEP_F(ctrl, rmask) x += __int_as_float(KYRO_DPP(__float_as_int(x), ctrl, rmask))
-    KYRO_DPP_SCAN(KYRO_STEP_F);
-#undef KYRO_STEP_F
-    return x;
+// Wave reductions of 32-bit values with op: the 16-lane rows with DPP, then the four row
+// results read as scalars (every lane gets the same value).
+template <class Op>
+__device__ __forceinline__ int wave_reduce_i(int x, Op op) {
+    x = op(x, KYRO_DPP(x, 0xB1, 0xf));   // quad_perm [1,0,3,2]
+    x = op(x, KYRO_DPP(x, 0x4E, 0xf));   // quad_perm [2,3,0,1]
+    x = op(x, KYRO_DPP(x, 0x141, 0xf));  // row_half_mirror
+    x = op(x, KYRO_DPP(x, 0x140, 0xf));  // row_mirror
+    return op(op(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+              op(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
 }
 
-__device__ __forceinline__ int wave_incl_scan_i(int x) {
-#define KYRO_STEP_I(ctrl, rmask) x += KYRO_DPP(x, ctrl, rmask)
-    KYRO_DPP_SCAN(KYRO_STEP_I);
-#undef KYRO_STEP_I
-    return x;
+// Wave argmax over (v, i) pairs: larger v, then lower i; every lane gets the result.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+    auto take = [&](float ov, int oi) {
+        if (ov > v || (ov == v && oi < i)) {
+            v = ov;
+            i = oi;
+        }
+    };
+#define KYRO_ASTEP(ctrl) take(__int_as_float(KYRO_DPP(__float_as_int(v), ctrl, 0xf)), KYRO_DPP(i, ctrl, 0xf))
+    KYRO_ASTEP(0xB1);
+    KYRO_ASTEP(0x4E);
+    KYRO_ASTEP(0x141);
+    KYRO_ASTEP(0x140);
+#undef KYRO_ASTEP
+    const float v0 = readlane_f(v, 0);
+    const int i0 = __builtin_amdgcn_readlane(i, 0);
+    const float v16 = readlane_f(v, 16), v32 = readlane_f(v, 32), v48 = readlane_f(v, 48);
+    const int i16 = __builtin_amdgcn_readlane(i, 16), i32 = __builtin_amdgcn_readlane(i, 32),
+              i48 = __builtin_amdgcn_readlane(i, 48);
+    v = v0;
+    i = i0;
+    take(v16, i16);
+    take(v32, i32);
+    take(v48, i48);
 }
 
 struct RowShared {
@@ -195,7 +217,7 @@ __device__ __forceinline__ float block_sum_f(float v, RowShared& sh) {
 }
 
 __device__ __forceinline__ int block_sum_i(int v, RowShared& sh) {
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = wave_reduce_i(v, [](int x, int y) { return x + y; });
     if ((threadIdx.x & 63) == 0) sh.ired[threadIdx.x >> 6] = v;
     __syncthreads();
     int r = 0;
@@ -208,10 +230,8 @@ __device__ __forceinline__ int block_sum_i(int v, RowShared& sh) {
 // the top (32 when all keys are equal), and their value: the first digit of a search over the
 // candidates can start below them.
 __device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowShared& sh, int* bits, uint64_t* prefix) {
-    for (int o = 32; o >= 1; o >>= 1) {
-        lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
-        hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
-    }
+    lo = (uint32_t)wave_reduce_i((int)lo, [](int x, int y) { return (int)min((uint32_t)x, (uint32_t)y); });
+    hi = (uint32_t)wave_reduce_i((int)hi, [](int x, int y) { return (int)max((uint32_t)x, (uint32_t)y); });
     if ((threadIdx.x & 63) == 0) {
         sh.ired[threadIdx.x >> 6] = (int)lo;
         sh.wsum[threadIdx.x >> 6] = hi;
@@ -229,14 +249,7 @@ __device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowSh
 
 // First index holding the maximum of v over the block (v = -inf for no candidate).
 __device__ __forceinline__ int block_argmax(float v, int i, RowShared& sh) {
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const int oi = __shfl_xor(i, o, 64);
-        if (ov > v || (ov == v && oi < i)) {
-            v = ov;
-            i = oi;
-        }
-    }
+    wave_argmax(v, i);
     if ((threadIdx.x & 63) == 0) {
         sh.fred[threadIdx.x >> 6] = v;
         sh.ired[threadIdx.x >> 6] = i;
@@ -715,14 +728,7 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
                 bi = v;
             }
         }
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        wave_argmax(bv, bi);
         if (lane == 0) {
             s_red[wave] = bv;
             s_ired[wave] = bi;

@@ -453,10 +453,13 @@ __device__ void accept_sequence(const SpecArgs& a, int b, int avail, bool writer
         if (a.out_p) a.out_p[(size_t)b * a.kmax + lane] = lane <= j ? p : __builtin_nanf("");
         if (a.out_q) a.out_q[(size_t)b * a.kmax + lane] = lane <= j ? q : __builtin_nanf("");
     }
-    // Row j's statistics (uniform source lane, so every lane shuffles).
-    const int jt = greedy ? row_arg(j) : 0;
-    const float mj = row_val(m0, m1, j), izj = row_val(iz0, iz1, j);
-    const float mdj = row_val(m0, m1, a.kmax + 1 + j), izdj = row_val(iz0, iz1, a.kmax + 1 + j);
+    // Row j's statistics: the source lanes are uniform, so they are read as scalars.
+    auto lane_val = [&](float v0, float v1, int rho) {
+        return rho < 64 ? readlane_f(v0, rho & 63) : readlane_f(v1, rho & 63);
+    };
+    const int jt = greedy ? (j < 64 ? __builtin_amdgcn_readlane(g0.i, j & 63) : __builtin_amdgcn_readlane(g1.i, j & 63)) : 0;
+    const float mj = lane_val(m0, m1, j), izj = lane_val(iz0, iz1, j);
+    const float mdj = lane_val(m0, m1, a.kmax + 1 + j), izdj = lane_val(iz0, iz1, a.kmax + 1 + j);
     if (lane != 0) return;
     SpecPlan pl;
     pl.row = j;
@@ -516,11 +519,7 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
     const bool use_res = (pl.mode == SPEC_RESIDUAL) && R > 0.f;
     const float target = pl.u * (use_res ? R : P);
     const float mine = use_res ? my_r : my_p;
-    float inc = mine;
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += y;
-    }
+    const float inc = wave_incl_scan_f(mine);
     if (lane == 63) ds.wsum[wave] = inc;
     __syncthreads();
     float ex = inc - mine;
@@ -571,11 +570,7 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
         if (w[i] > 0.f) my_last = contig_index(v0, i);
     }
     // Exclusive scan of the per-thread sums in thread (= index) order.
-    float inc2 = ts;
-    for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(inc2, o, 64);
-        if (lane >= o) inc2 += y;
-    }
+    const float inc2 = wave_incl_scan_f(ts);
     if (lane == 63) ds.wsum[wave] = inc2;
     __syncthreads();
     float ex2 = inc2 - ts;
@@ -651,11 +646,7 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
     for (int t = 0; t < kTiles; ++t) {
         if (t * kT >= a.B) break;
         const int i = t * kT + (int)threadIdx.x;
-        int inc = ti[t].x;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += y;
-        }
+        const int inc = wave_incl_scan_i(ti[t].x);
         if (lane == 63) s_wsum[wave] = inc;
         __syncthreads();
         int before = carry;
