@@ -470,6 +470,119 @@ __device__ __forceinline__ int first_at_least(const float* c, int n, float x, bo
     return f == 0x7fffffff ? -1 : f;
 }
 
+// A search's position after its histogram levels: the found bin's prefix (pbits fixed high bits
+// of (key << 32) | ~index), the mass ahead of the bin, and for the first level its bin and
+// width, whose histogram sh.hist / sh.cnt still holds when levels == 1.
+struct SearchState {
+    uint64_t prefix;
+    int pbits;
+    u64 before;
+    int levels;
+    int d1, bits1;
+    u64 before1;
+};
+
+// The bin (of nb in sh.hist, mass before it `before`) where the running mass from the top bin
+// down first reaches theta (exceeds it when strict): -1 if none. *before_bin gets the mass ahead
+// of it and *count its members (sh.cnt). Whole block.
+__device__ __forceinline__ int bin_scan(int nb, u64 before, u64 theta, bool strict, RowShared& sh, u64* before_bin,
+                                        int* count) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Running mass over the bins from the top: thread t owns descending positions 2t, 2t+1.
+    const int j0 = 2 * tid, j1 = 2 * tid + 1;
+    const u64 m0 = j0 < nb ? sh.hist[nb - 1 - j0] : 0;
+    const u64 m1 = j1 < nb ? sh.hist[nb - 1 - j1] : 0;
+    const u64 incl = wave_incl_scan_u64(m0 + m1);
+    if (lane == 63) sh.wsum[wave] = incl;
+    if (tid == 0) sh.found = -1;
+    __syncthreads();
+    u64 base = before;
+    for (int w = 0; w < wave; ++w) base += sh.wsum[w];
+    const u64 ex0 = base + incl - (m0 + m1), in0 = ex0 + m0, in1 = in0 + m1;
+    auto crosses = [&](u64 ex, u64 in) { return strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta); };
+    if (j0 < nb && m0 && crosses(ex0, in0)) {
+        sh.found = nb - 1 - j0;
+        sh.before = ex0;
+        sh.count = (int)sh.cnt[nb - 1 - j0];
+    } else if (j1 < nb && m1 && crosses(in0, in1)) {
+        sh.found = nb - 1 - j1;
+        sh.before = in0;
+        sh.count = (int)sh.cnt[nb - 1 - j1];
+    }
+    __syncthreads();
+    const int d = sh.found;
+    *before_bin = sh.before;
+    *count = sh.count;
+    __syncthreads();
+    return d;
+}
+
+// The members of the bin named by (prefix, pbits) with mass, at most 64, ranked in wave 0 (each
+// lane counts the members above its own, broadcast LDS reads) and summed in that order from
+// `before`; the first whose running mass reaches theta (exceeds it when strict). Scratch in
+// sh.cum, so that sh.hist survives. Returns its index, or -1.
+template <class Member, class MassOf>
+__device__ __forceinline__ int bin_resolve(int n, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
+                                           uint64_t prefix, int pbits, u64 before, u64* before_out, u64* mass_out,
+                                           uint32_t* key_out) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) sh.nsmall = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kRT) {
+        const u64 c = sh.cand[i];
+        const uint32_t key = (uint32_t)(c >> 32);
+        if ((c >> (64 - pbits)) == prefix && member(key, (int)~(uint32_t)c) && mass_of(key_value(key))) {
+            const int slot = atomicAdd(&sh.nsmall, 1);
+            if (slot < 64) sh.sidx[slot] = i;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        u64* scr = reinterpret_cast<u64*>(sh.cum);
+        const int ns = min(sh.nsmall, 64);
+        u64 c = 0, m = 0;
+        if (lane < ns) {
+            c = sh.cand[sh.sidx[lane]];
+            m = mass_of(key_value((uint32_t)(c >> 32)));
+            scr[lane] = c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        for (int j = 0; j < ns; ++j) rank += scr[j] > c ? 1 : 0;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ns) {
+            scr[64 + rank] = m;
+            scr[128 + rank] = c;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        u64 in = before;
+        for (int j = 0; j <= lane && j < ns; ++j) in += scr[64 + j];
+        m = lane < ns ? scr[64 + lane] : 0;
+        c = lane < ns ? scr[128 + lane] : 0;
+        const u64 ex = in - m;
+        const bool hit = m && (strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta));
+        const unsigned long long bal = __ballot(hit);
+        if (bal && lane == __ffsll((long long)bal) - 1) {
+            sh.found = (int)~(uint32_t)c;
+            sh.before = ex;
+            sh.mass = m;
+            sh.wsum[0] = c >> 32;
+        } else if (!bal && lane == 0) {
+            sh.found = -1;
+        }
+    }
+    __syncthreads();
+    const int found = sh.found;
+    *key_out = (uint32_t)sh.wsum[0];
+    *mass_out = sh.mass;
+    *before_out = sh.before;
+    __syncthreads();
+    return found;
+}
+
 // desc_search over the row's candidate list in LDS instead of the row: entries sh.cand[0, n),
 // (key << 32) | ~index. The same order (key descending, then index ascending), the same masses
 // and the same crossing rule, found by mass histograms over the key's digits (up to 11 bits each,
@@ -477,18 +590,18 @@ __device__ __forceinline__ int first_at_least(const float* c, int n, float x, bo
 // the found key, over ~index's digits (descending ~index is ascending index). Starting below the
 // shared bits spreads the first level's candidates over its bins: a top-p row's candidates fall
 // in a handful of 11-bit top bins, and their atomic adds to those few bins serialise. Once the
-// found bin holds at most 64 members, one wave ranks them and sums their masses in that order
-// instead of running further levels. Returns the index, or -1 when the members' mass falls short
-// of theta; *key_out gets its key.
+// found bin holds at most 64 members, bin_resolve settles it. Returns the index, or -1 when the
+// members' mass falls short of theta; *key_out gets its key, *st the levels' state.
 template <class Member, class MassOf>
 __device__ __forceinline__ int cand_search(int n, Member member, MassOf mass_of, u64 theta, bool strict, RowShared& sh,
-                           u64* before_out, u64* mass_out, uint32_t* key_out, int pbits0 = 0,
-                           uint64_t prefix0 = 0) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    uint64_t prefix = prefix0;  // fixed high bits of (key << 32 | ~index)
+                                           u64* before_out, u64* mass_out, uint32_t* key_out, int pbits0 = 0,
+                                           uint64_t prefix0 = 0, SearchState* st = nullptr) {
+    const int tid = threadIdx.x;
+    uint64_t prefix = prefix0;
     int pbits = pbits0;
     u64 before = 0;
     bool few = false;
+    SearchState s{};
     for (int lvl = 0; lvl < 7 && !few && pbits < 64; ++lvl) {
         // Key digits up to the key's last bit, then ~index digits.
         const int bits = pbits < 32 ? min(11, 32 - pbits) : min(11, 64 - pbits);
@@ -511,94 +624,26 @@ __device__ __forceinline__ int cand_search(int n, Member member, MassOf mass_of,
             }
         }
         __syncthreads();
-        // Running mass over the bins from the top: thread t owns descending positions 2t, 2t+1.
-        const int j0 = 2 * tid, j1 = 2 * tid + 1;
-        const u64 m0 = j0 < nb ? sh.hist[nb - 1 - j0] : 0;
-        const u64 m1 = j1 < nb ? sh.hist[nb - 1 - j1] : 0;
-        const u64 incl = wave_incl_scan_u64(m0 + m1);
-        if (lane == 63) sh.wsum[wave] = incl;
-        if (tid == 0) sh.found = -1;
-        __syncthreads();
-        u64 base = before;
-        for (int w = 0; w < wave; ++w) base += sh.wsum[w];
-        const u64 ex0 = base + incl - (m0 + m1), in0 = ex0 + m0, in1 = in0 + m1;
-        auto crosses = [&](u64 ex, u64 in) { return strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta); };
-        if (j0 < nb && m0 && crosses(ex0, in0)) {
-            sh.found = nb - 1 - j0;
-            sh.before = ex0;
-            sh.count = (int)sh.cnt[nb - 1 - j0];
-        } else if (j1 < nb && m1 && crosses(in0, in1)) {
-            sh.found = nb - 1 - j1;
-            sh.before = in0;
-            sh.count = (int)sh.cnt[nb - 1 - j1];
-        }
-        __syncthreads();
-        const int d = sh.found;
+        u64 bb;
+        int cnt;
+        const int d = bin_scan(nb, before, theta, strict, sh, &bb, &cnt);
         if (d < 0) return -1;
-        before = sh.before;
-        few = sh.count <= 64;
+        if (lvl == 0) {
+            s.d1 = d;
+            s.bits1 = bits;
+            s.before1 = bb;
+        }
+        s.levels = lvl + 1;
+        before = bb;
+        few = cnt <= 64;
         prefix = (prefix << bits) | (uint64_t)d;
         pbits += bits;
-        __syncthreads();
     }
-    // The found bin's members with mass, at most 64 (when all 64 bits are fixed, one), sorted
-    // descending in wave 0; the running mass from `before` crosses theta at one of them.
-    if (tid == 0) sh.nsmall = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += kRT) {
-        const u64 c = sh.cand[i];
-        const uint32_t key = (uint32_t)(c >> 32);
-        if ((c >> (64 - pbits)) == prefix && member(key, (int)~(uint32_t)c) && mass_of(key_value(key))) {
-            const int slot = atomicAdd(&sh.nsmall, 1);
-            if (slot < 64) sh.sidx[slot] = i;
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
-        // Rank by counting (each lane reads every member, broadcast LDS reads), then running
-        // sums by reading the ranked masses: no cross-lane shuffles. sh.hist is free here.
-        const int ns = min(sh.nsmall, 64);
-        u64 c = 0, m = 0;
-        if (lane < ns) {
-            c = sh.cand[sh.sidx[lane]];
-            m = mass_of(key_value((uint32_t)(c >> 32)));
-            sh.hist[lane] = c;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        int rank = 0;
-        for (int j = 0; j < ns; ++j) rank += sh.hist[j] > c ? 1 : 0;
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        if (lane < ns) {
-            sh.hist[64 + rank] = m;
-            sh.hist[128 + rank] = c;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        u64 in = before;
-        for (int j = 0; j <= lane && j < ns; ++j) in += sh.hist[64 + j];
-        m = lane < ns ? sh.hist[64 + lane] : 0;
-        c = lane < ns ? sh.hist[128 + lane] : 0;
-        const u64 ex = in - m;
-        const bool hit = m && (strict ? (ex <= theta && in > theta) : (ex < theta && in >= theta));
-        const unsigned long long bal = __ballot(hit);
-        if (bal && lane == __ffsll((long long)bal) - 1) {
-            sh.found = (int)~(uint32_t)c;
-            sh.before = ex;
-            sh.mass = m;
-            sh.wsum[0] = c >> 32;
-        } else if (!bal && lane == 0) {
-            sh.found = -1;
-        }
-    }
-    __syncthreads();
-    const int found = sh.found;
-    *key_out = (uint32_t)sh.wsum[0];
-    *mass_out = sh.mass;
-    *before_out = sh.before;
-    __syncthreads();
-    return found;
+    s.prefix = prefix;
+    s.pbits = pbits;
+    s.before = before;
+    if (st) *st = s;
+    return bin_resolve(n, member, mass_of, theta, strict, sh, prefix, pbits, before, before_out, mass_out, key_out);
 }
 
 __device__ __forceinline__ bool row_has_proc(const SampleArgs& a, int b) {
@@ -976,8 +1021,10 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared
         u64 total = (u64)llrint(kFix);
         float rr = u;
         bool settled = true;
+        SearchState cst{};
+        int cut = -1;
         if (use_p) {
-            const int cut = cand_search(n, kept, pmass, (u64)llrint((double)tp * kFix), true, sh, &bf, &ms, &key, cp_bits, cp);
+            cut = cand_search(n, kept, pmass, (u64)llrint((double)tp * kFix), true, sh, &bf, &ms, &key, cp_bits, cp, &cst);
             if (cut >= 0) {
                 r.ck = key;
                 r.ci = cut;
@@ -997,8 +1044,23 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared
         if (settled) {
             auto in_cut = [&](uint32_t kc, int v) { return r.kept(kc, v) && r.in_cut(kc, v); };
             const u64 theta = fix_mass(rr);
-            int pick = theta == 0 ? cand_search(n, in_cut, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp)
+            int pick;
+            if (theta != 0 && cut >= 0 && cst.levels == 1) {
+                // The cut search's first-level histogram still holds: its bins above the cut's bin
+                // hold only tokens ahead of the cut, so the draw finds its bin there, or in the
+                // cut's own bin once theta passes their mass, without another histogram pass.
+                int d = cst.d1, cnt = 0;
+                u64 bb = cst.before1;
+                if (theta <= cst.before1) d = bin_scan(1 << cst.bits1, 0, theta, false, sh, &bb, &cnt);
+                if (d >= 0 && cnt <= 64)
+                    pick = bin_resolve(n, in_cut, pmass, theta, false, sh, (cp << cst.bits1) | (uint64_t)d,
+                                       cp_bits + cst.bits1, bb, &bf, &ms, &key);
+                else
+                    pick = cand_search(n, in_cut, pmass, theta, false, sh, &bf, &ms, &key, cp_bits, cp);
+            } else {
+                pick = theta == 0 ? cand_search(n, in_cut, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp)
                                   : cand_search(n, in_cut, pmass, theta, false, sh, &bf, &ms, &key, cp_bits, cp);
+            }
             if (pick < 0) pick = use_p ? cand_search(n, kept, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp) : r.ki;
             if (tid == 0) a.out[b] = (uint32_t)(pick >= 0 && pick < V ? pick : V - 1);
             return;
