@@ -49,9 +49,6 @@ namespace {
 
 constexpr int kRT = 1024;  // threads of the row kernel
 constexpr int kRW = kRT / 64;
-#ifndef KYRO_COUNT_LANE
-#define KYRO_COUNT_LANE 0
-#endif
 // Top-p alone: the most candidates a chunk lists below its skip bound (fewer candidates search
 // faster; lists too short to reach the cut send the row to the radix path).
 #ifndef KYRO_SAMPLE_P_TARGET
@@ -751,7 +748,6 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     __shared__ float s_red[kCW];
     __shared__ int s_ired[kCW];
     __shared__ uint32_t s_wn[3 * kCW];
-    __shared__ __align__(16) int s_wn4[32];
     const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* y = row_ptr(a, b);
     const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
@@ -811,25 +807,6 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     // ccap entries. Counts over the block come from wave ballots (no atomics), two LDS slots per
     // wave alternating so that each count needs one barrier.
     int buf = 0;
-#if KYRO_COUNT_LANE
-    auto count_ge = [&](float t) -> int {
-        int n = 0;
-#pragma unroll
-        for (int i = 0; i < kCPer; ++i) n += x[i] >= t ? 1 : 0;
-        n += __builtin_amdgcn_update_dpp(0, n, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
-        n += __builtin_amdgcn_update_dpp(0, n, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-        n += __builtin_amdgcn_update_dpp(0, n, 0x141, 0xF, 0xF, false);  // row_half_mirror
-        n += __builtin_amdgcn_update_dpp(0, n, 0x140, 0xF, 0xF, false);  // row_mirror
-        if ((lane & 15) == 0) s_wn4[buf * 16 + wave * 4 + (lane >> 4)] = n;
-        __syncthreads();
-        const int4* q = reinterpret_cast<const int4*>(s_wn4 + buf * 16);
-        const int4 q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
-        const int tot = (q0.x + q0.y + q0.z + q0.w) + (q1.x + q1.y + q1.z + q1.w) + (q2.x + q2.y + q2.z + q2.w) +
-                        (q3.x + q3.y + q3.z + q3.w);
-        buf ^= 1;
-        return __builtin_amdgcn_readfirstlane(tot);
-    };
-#else
     auto count_ge = [&](float t) -> int {
         int n = 0;
 #pragma unroll
@@ -842,7 +819,6 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         buf ^= 1;
         return __builtin_amdgcn_readfirstlane(tot);  // the same in every lane: keeps the searches scalar
     };
-#endif
     const float ninf = -__builtin_huge_valf();
     const int cap = a.ccap;
     // Thresholds on a grid below the chunk's max: t_j = m - j / 8, j < npts (at most 512: 64 nats).
@@ -904,23 +880,31 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             }
         }
     }
+    // Write the list: a block scan of the per-thread hits places every entry. The list's length
+    // is the scan's total; a total above the cap (the counts above disagreeing with the hits)
+    // sends the row to the fallback instead of writing past the chunk's slots.
+    const float tw = thr == ninf ? -FLT_MAX : thr;
+    uint32_t hits = 0;
+    if (cnt > 0) {
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i)
+            if (x[i] >= tw) hits |= 1u << i;
+    }
+    const uint32_t mine = (uint32_t)__popc(hits);
+    const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
+    if (lane == 63) s_wn[2 * kCW + wave] = incl;
+    __syncthreads();
+    uint32_t off = incl - mine, total = 0;
+    for (int w = 0; w < kCW; ++w) {
+        if (w < wave) off += s_wn[2 * kCW + w];
+        total += s_wn[2 * kCW + w];
+    }
+    if (cnt > 0) cnt = total <= (uint32_t)cap ? (int)total : -1;
     if (tid == 0) {
         a.cthr[(size_t)b * a.C + c] = thr;
         a.ccount[(size_t)b * a.C + c] = cnt;
     }
     if (cnt <= 0) return;
-    // Write the list: a block scan of the per-thread hits places every entry.
-    const float tw = thr == ninf ? -FLT_MAX : thr;
-    uint32_t hits = 0;
-#pragma unroll
-    for (int i = 0; i < kCPer; ++i)
-        if (x[i] >= tw) hits |= 1u << i;
-    const uint32_t mine = (uint32_t)__popc(hits);
-    const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
-    if (lane == 63) s_wn[2 * kCW + wave] = incl;
-    __syncthreads();
-    uint32_t off = incl - mine;
-    for (int w = 0; w < wave; ++w) off += s_wn[2 * kCW + w];
     u64* list = a.cand + (size_t)b * kCap + (size_t)c * cap;
 #pragma unroll
     for (int i = 0; i < kCPer; ++i)
