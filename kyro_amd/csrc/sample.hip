@@ -226,7 +226,8 @@ __device__ __forceinline__ int block_sum_i(int v, RowShared& sh) {
 // Bits every key in [lo, hi] (each thread's range, merged over the block) shares, counted from
 // the top (32 when all keys are equal), and their value: the first digit of a search over the
 // candidates can start below them.
-__device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowShared& sh, int* bits, uint64_t* prefix) {
+__device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowShared& sh, int* bits, uint64_t* prefix,
+                                                 uint32_t* lo_out = nullptr) {
     lo = (uint32_t)wave_reduce_i((int)lo, [](int x, int y) { return (int)min((uint32_t)x, (uint32_t)y); });
     hi = (uint32_t)wave_reduce_i((int)hi, [](int x, int y) { return (int)max((uint32_t)x, (uint32_t)y); });
     if ((threadIdx.x & 63) == 0) {
@@ -242,6 +243,7 @@ __device__ __forceinline__ void key_range_prefix(uint32_t lo, uint32_t hi, RowSh
     const int b = (lo >= hi) ? 32 : __clz((int)(lo ^ hi));
     *bits = b;
     *prefix = b == 0 ? 0 : (uint64_t)(lo >> (32 - b));
+    if (lo_out) *lo_out = lo;
 }
 
 // First index holding the maximum of v over the block (v = -inf for no candidate).
@@ -938,7 +940,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared
     r.ci = V;
     const bool use_k = k > 0 && k < V;
     const bool use_p = tp < 1.0f;
-    if (n >= 0 && n <= kSortMax) {
+    // Settles the row from n candidates in sh.cand (see above); false when they do not settle it.
+    auto from_candidates = [&](int n, uint32_t kmin, int cp_bits, uint64_t cp) -> bool {
+    if (n <= kSortMax) {
         // Few candidates: sorted in LDS, then cut and walked with running sums.
         int np2 = 2;
         while (np2 < n) np2 <<= 1;
@@ -976,7 +980,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared
             int pick = first_at_least(sh.cum, cut, rr, false, sh);
             if (pick < 0) pick = use_p ? 0 : ns - 1;
             if (tid == 0) a.out[b] = ~(uint32_t)sh.cand[pick];
-            return;
+            return true;
         }
     }
     if (n > kSortMax) {
@@ -1047,13 +1051,106 @@ __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared
             }
             if (pick < 0) pick = use_p ? cand_search(n, kept, unit, 1, false, sh, &bf, &ms, &key, cp_bits, cp) : r.ki;
             if (tid == 0) a.out[b] = (uint32_t)(pick >= 0 && pick < V ? pick : V - 1);
-            return;
+            return true;
         }
         r.kk = 0;
         r.ki = V;
         r.ck = 0;
         r.ci = V;
         r.z_sum = Z;
+    }
+    return false;
+    };
+    if (n >= 0 && from_candidates(n, kmin, cp_bits, cp)) return;
+    // Row gather, when the lists did not settle the row: pass A histograms the row in bins of
+    // 1/8 nat below M (64 nats) (counts, and for top-p alone masses exp(z - bin top) in 2^-12 units, so
+    // that a wave's V / 16 tokens stay below 2^32 for every V; one copy per wave in the candidate
+    // array, which is free here), the bins from the top find the
+    // bin where the running count reaches k (top-k) or the running mass passes top_p Z (top-p,
+    // one bin lower for the masses' rounding), and pass B gathers every token in that bin or
+    // above. Both the bin of a token and the gathered set are monotone in z, so every token at
+    // or above the least gathered key is present, and the candidate path settles the row exactly
+    // or leaves it to the radix selects.
+    {
+        constexpr int kGB = 512;  // two arrays of kRW x kGB words fill the candidate array
+        static_assert(2 * kRW * kGB * 4 <= kCap * 8, "row-gather histograms exceed the candidate array");
+        uint32_t* hc = reinterpret_cast<uint32_t*>(sh.cand);
+        uint32_t* hm = hc + kRW * kGB;
+        const bool by_mass = use_p && !use_k;
+        for (int i = tid; i < 2 * kRW * kGB; i += kRT) hc[i] = 0;
+        __syncthreads();
+        auto bin_of = [&](float zv) { return (M - zv) * 8.f; };  // bin = (int) of it, below kGB
+        {
+            uint32_t* myc = hc + (tid >> 6) * kGB;
+            uint32_t* mym = hm + (tid >> 6) * kGB;
+            row_for_each(r.y, V, r.vec4, [&](int, float yv) {
+                const float zv = yv * r.s + 0.0f;
+                const float d = bin_of(zv);
+                if (!(d < (float)kGB)) return;  // below the range, or NaN
+                const int bin = (int)fmaxf(d, 0.f);
+                atomicAdd(&myc[bin], 1u);
+                if (by_mass) {
+                    const float e = fast_exp2((zv - (M - 0.125f * (float)bin)) * kLog2e);
+                    atomicAdd(&mym[bin], (uint32_t)fminf(e * 4096.f, 4096.f));
+                }
+            });
+        }
+        __syncthreads();
+        // Thread t < kGB merges bin t; bins in thread order run from the top down.
+        int bc = 0;
+        float bm = 0.f;
+        if (tid < kGB) {
+            uint32_t sm = 0;
+            for (int w = 0; w < kRW; ++w) {
+                bc += (int)hc[w * kGB + tid];
+                sm += hm[w * kGB + tid];
+            }
+            bm = (float)sm * (1.f / 4096.f) * fast_exp2(-0.125f * (float)tid * kLog2e);
+        }
+        const int cinc = wave_incl_scan_i(bc);
+        const float minc = wave_incl_scan_f(bm);
+        if ((tid & 63) == 63) {
+            sh.ired[tid >> 6] = cinc;
+            sh.fred[tid >> 6] = minc;
+        }
+        if (tid == 0) sh.found = 0x7fffffff;
+        __syncthreads();
+        int cb = cinc;
+        float mb = minc;
+        for (int w = 0; w < (tid >> 6); ++w) {
+            cb += sh.ired[w];
+            mb += sh.fred[w];
+        }
+        const bool reach = by_mass ? mb > tp * Z : cb >= k;
+        if (tid < kGB && reach) atomicMin(&sh.found, tid);
+        __syncthreads();
+        const int bsel = sh.found == 0x7fffffff ? -1 : min(sh.found + (by_mass ? 1 : 0), kGB - 1);
+        if (tid == bsel) sh.count = cb;  // tokens in the bins at or above bsel
+        __syncthreads();
+        const int ng = bsel >= 0 ? sh.count : kCap + 1;
+        __syncthreads();
+        if (ng <= kCap) {
+            if (tid == 0) sh.nsmall = 0;
+            __syncthreads();
+            uint32_t lo = 0xffffffffu, hi = 0u;
+            row_for_each(r.y, V, r.vec4, [&](int v, float yv) {
+                const float zv = yv * r.s + 0.0f;
+                const float d = bin_of(zv);
+                if (!(d < (float)kGB) || (int)fmaxf(d, 0.f) > bsel) return;
+                const uint32_t key = order_key(zv);
+                const int slot = atomicAdd(&sh.nsmall, 1);
+                if (slot < kCap) sh.cand[slot] = ((u64)key << 32) | (uint32_t)~(uint32_t)v;
+                lo = min(lo, key);
+                hi = max(hi, key);
+            });
+            int gbits;
+            uint64_t gp;
+            uint32_t gmin;
+            key_range_prefix(lo, hi, sh, &gbits, &gp, &gmin);  // its barriers order the gather's writes
+            const int got = sh.nsmall;
+            __syncthreads();
+            if (got <= kCap && from_candidates(got, use_k ? 0u : gmin, gbits, gp)) return;
+        }
     }
     // Radix selects over the whole row (candidates did not fit in LDS, or did not settle the cut).
     auto all = [](uint32_t, int) { return true; };
