@@ -80,6 +80,24 @@ def test_wide_dynamic_range(gpu):
     run_both(x, T, u, gpu)
 
 
+@pytest.mark.parametrize("V,scale,kw", [
+    (128256, 3.1, {"top_p": 0.9}),   # nucleus of a few thousand tokens: wider than the chunk lists
+    (128256, 3.0, {"top_p": 0.95}),
+    (32000, 2.0, {"top_k": 1000}),   # k above a chunk list's slots
+    (128256, 3.0, {"top_k": 300, "top_p": 0.9}),
+])
+def test_rows_the_chunk_lists_do_not_cover(gpu, V, scale, kw):
+    """Rows whose kept set the stats pass's per-chunk candidate lists cannot hold: the select pass
+    gathers candidates from the row itself (one workgroup, two passes) and settles them exactly."""
+    rng = np.random.default_rng(V + int(scale * 10))
+    B = 8
+    x = (rng.standard_normal((B, V)) * scale).astype(np.float32)
+    T = np.ones(B, np.float32)
+    u = rng.random(B).astype(np.float32)
+    args = {k: np.full(B, v, np.int32 if k == "top_k" else np.float32) for k, v in kw.items()}
+    run_both(x, T, u, gpu, **args)
+
+
 def test_processors(gpu):
     rng = np.random.default_rng(8)
     B, V = 16, 5000
