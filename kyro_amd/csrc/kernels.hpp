@@ -308,9 +308,12 @@ constexpr int kMaxLazyBatch = 2048;  // larger batches read every row in the fir
 // Default window: batches whose logit rows total at most this many bytes read them all in the
 // first pass (at ~6 TB/s, 64 MB take about as long as the tail pass's fixed cost).
 constexpr long long kSpecEagerBytes = 64ll << 20;
+// Workgroups of the pass over the remaining rows (more when one would hold more than 64 items).
+// On the Llama-3-8B step (~2,900 pending items) 512 measured 246.1-246.5 us cold against
+// 247.3 with 2048, 1024 in between; 384 and 256 were slower (246.6-246.9, 249.5).
 #ifndef KYRO_SPEC_TAIL_WGS
-#define KYRO_SPEC_TAIL_WGS 2048
+#define KYRO_SPEC_TAIL_WGS 512
 #endif
-constexpr int kSpecTailWgs = KYRO_SPEC_TAIL_WGS;  // workgroups of the pass over the remaining rows
+constexpr int kSpecTailWgs = KYRO_SPEC_TAIL_WGS;
 
 }  // namespace kyro
