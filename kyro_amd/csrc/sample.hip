@@ -35,10 +35,12 @@
 //                          descending order (key descending, index ascending): up to kSortMax
 //                          candidates sorted with running sums; more searched with mass
 //                          histograms over the key's digits. Rows whose lists do not cover the
-//                          kept set (or the top-p cut) run exact radix selects over the whole
-//                          row instead: three passes (11 + 11 + 10 bits) of mass histograms in LDS
-//                          (64-bit fixed point, 2^-52 resolution, so the sums do not depend on
-//                          thread order), then a pass in index order for ties between equal keys.
+//                          kept set (or the top-p cut) gather candidates from the row in the same
+//                          workgroup (a binned pass, then a gathering pass); what that leaves
+//                          runs exact radix selects over the whole row: three passes (11 + 11 +
+//                          10 bits) of mass histograms in LDS (64-bit fixed point, 2^-52
+//                          resolution, so the sums do not depend on thread order), then a pass in
+//                          index order for ties between equal keys.
 #include <cfloat>
 
 #include "common.hpp"
@@ -49,8 +51,9 @@ namespace {
 
 constexpr int kRT = 1024;  // threads of the row kernel
 constexpr int kRW = kRT / 64;
-// Top-p alone: the most candidates a chunk lists below its skip bound (fewer candidates search
-// faster; lists too short to reach the cut send the row to the radix path).
+// Top-p alone: the most candidates a chunk lists above its skip bound (fewer candidates search
+// faster; lists too short to reach the cut send the row to the row gather below). 96 lost the
+// cut on the 64-row N(0, 3.75) batch; 160 and 256 cost 1.5 and 2.8 us a call there.
 #ifndef KYRO_SAMPLE_P_TARGET
 #define KYRO_SAMPLE_P_TARGET 128
 #endif
@@ -919,10 +922,11 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
 // Settles a top-k / top-p row (worker.rs:300-360) from n candidates in sh.cand (n < 0: none):
 // the k largest for top-k, or for top-p alone every token with key >= kmin (more below it may be
 // present). Candidates sort or are searched in descending order (key descending, index
-// ascending); a row whose candidates do not settle the cut runs exact radix selects over the
-// whole row: three passes (11 + 11 + 10 bits) of mass histograms in LDS (64-bit fixed point,
-// 2^-52 resolution, so the sums do not depend on thread order), then a pass in index order for
-// ties between equal keys.
+// ascending). A row whose candidates do not settle the cut gathers candidates from the row itself
+// (two passes, below), and what that leaves runs exact radix selects over the whole row: three
+// passes (11 + 11 + 10 bits) of mass histograms in LDS (64-bit fixed point, 2^-52 resolution, so
+// the sums do not depend on thread order), then a pass in index order for ties between equal
+// keys.
 __device__ __forceinline__ void finish_row(const SampleArgs& a, int b, RowShared& sh, int n, float M, float Z, uint32_t kmin,
                            float T, int k, float tp, float u, int cp_bits, uint64_t cp) {
     const int tid = threadIdx.x;
