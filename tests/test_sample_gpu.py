@@ -98,6 +98,27 @@ def test_rows_the_chunk_lists_do_not_cover(gpu, V, scale, kw):
     run_both(x, T, u, gpu, **args)
 
 
+@pytest.mark.parametrize("V", [50001, 200000])
+def test_list_shapes(gpu, V):
+    """Vocabularies whose chunk lists take other shapes: 50001 entries (not a multiple of four:
+    scalar loads, a short last chunk) and 200000 (49 chunks, so 167 list slots a chunk instead of
+    256). Top-k, top-p and both, with one row masked down to fewer allowed tokens than k."""
+    rng = np.random.default_rng(V)
+    B = 12
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    T = np.full(B, 0.8, np.float32)
+    u = rng.random(B).astype(np.float32)
+    masks = np.stack([kyro_amd.grammar_mask(rng.choice(V, size=30, replace=False), V)])
+    mask_row = np.full(B, -1, np.int32)
+    mask_row[3] = 0
+    k = rng.choice([1, 40, 100, 160], size=B).astype(np.int32)
+    k[3] = 50  # more than the 30 allowed tokens
+    tp = rng.choice([0.5, 0.9, 0.99], size=B).astype(np.float32)
+    run_both(x, T, u, gpu, top_k=k, masks=masks, mask_row=mask_row)
+    run_both(x, T, u, gpu, top_p=tp, masks=masks, mask_row=mask_row)
+    run_both(x, T, u, gpu, top_k=k, top_p=tp, masks=masks, mask_row=mask_row)
+
+
 def test_processors(gpu):
     rng = np.random.default_rng(8)
     B, V = 16, 5000
