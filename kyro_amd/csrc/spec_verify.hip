@@ -421,20 +421,15 @@ __device__ void accept_sequence(const SpecArgs& a, int b, int avail, bool writer
         const float w1 = __shfl(v1, rho & 63, 64);
         return rho < 64 ? w0 : w1;
     };
-    auto row_arg = [&](int rho) {
-        const int w0 = __shfl(g0.i, rho & 63, 64);
-        const int w1 = __shfl(g1.i, rho & 63, 64);
-        return rho < 64 ? w0 : w1;
-    };
     bool accept = true;
     const int lim = min(k, avail);     // drafts whose rows were read
     const int dr = a.kmax + 1 + lane;  // this lane's draft row
     float p = __builtin_nanf(""), q = __builtin_nanf("");
     if (greedy) {
-        const int top = row_arg(lane);
+        const int top = g0.i;  // this lane's own row (lane < 64)
         accept = lane >= lim || top == (int)x;
     } else {
-        const float mt = row_val(m0, m1, lane), izt = row_val(iz0, iz1, lane);
+        const float mt = m0, izt = iz0;  // this lane's own row (lane < 64)
         const float md = row_val(m0, m1, dr), izd = row_val(iz0, iz1, dr);
         if (lane < lim) {
             p = fast_exp2((tx - mt) * c2) * izt;
