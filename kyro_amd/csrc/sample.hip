@@ -797,6 +797,7 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         x[i] = x[i] * sc + 0.0f;
         m = fmaxf(m, x[i]);
     }
+    const float lmax = m;  // this lane's largest entry
     m = cblock_max(m, s_red);
     float sum = 0.f;
     if (m != -__builtin_huge_valf()) {
@@ -847,6 +848,27 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         *c_hi = chi;
         return lo;
     };
+    // Lanes whose largest entry is at or above t: one ballot instead of sixteen, and never more
+    // than the entries at or above t. Steers the searches; the thresholds kept are counted exactly.
+    auto lanes_ge = [&](float t) -> int {
+        const int n = (int)__popcll(__ballot(lmax >= t));
+        if (lane == 0) s_wn[buf * kCW + wave] = (uint32_t)n;
+        __syncthreads();
+        int tot = 0;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) tot += (int)s_wn[buf * kCW + w];
+        buf ^= 1;
+        return __builtin_amdgcn_readfirstlane(tot);
+    };
+    auto bisect_lanes = [&](int lim, int npts) {  // largest j in [-1, npts) with lanes_ge(t_j) <= lim
+        int lo = -1, hi = npts;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (lanes_ge(grid_t(mid)) <= lim) lo = mid;
+            else hi = mid;
+        }
+        return lo;
+    };
     float thr = ninf;  // -inf: every finite entry (a complete list)
     int cnt = -1;      // -1: no threshold keeps the list within cap
     if (m == ninf) {
@@ -855,14 +877,23 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         // Top-k (with or without top-p): the chunk's own k largest must be listed, so t is the
         // highest grid threshold with at least k entries at or above it; a chunk with fewer
         // than k entries that far up lists every finite entry.
+        // The highest grid threshold with k lanes at or above it has at least k entries there;
+        // one exact count checks it fits, else the exact search runs.
         const int fin = count_ge(-FLT_MAX);  // finite entries
-        int clo, chi;
-        const int j = bisect(k - 1, 512, &clo, &chi) + 1;
-        if (j < 512 && chi <= cap) {
-            thr = grid_t(j);
-            cnt = chi;
-        } else if (fin <= cap) {
-            cnt = fin;  // complete
+        const int jl = bisect_lanes(k - 1, 512) + 1;
+        const int cl = jl < 512 ? count_ge(grid_t(jl)) : -1;
+        if (cl >= k && cl <= cap) {
+            thr = grid_t(jl);
+            cnt = cl;
+        } else {
+            int clo, chi;
+            const int j = bisect(k - 1, 512, &clo, &chi) + 1;
+            if (j < 512 && chi <= cap) {
+                thr = grid_t(j);
+                cnt = chi;
+            } else if (fin <= cap) {
+                cnt = fin;  // complete
+            }
         }
     } else {
         // Top-p alone keeps a token only if p >= (1 - top_p) / V; with log Z >= this chunk's
@@ -876,12 +907,25 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             thr = skip;
             cnt = cs;
         } else {
-            int clo, chi;
-            // grid points above the skip bound only: below it every count exceeds the cap
-            const int j = bisect(min(cap, KYRO_SAMPLE_P_TARGET), min(512, (int)ceilf(span * 8.f)), &clo, &chi);
-            if (j >= 0) {
+            // Grid points above the skip bound only (below it every count exceeds the cap). The
+            // lowest threshold with at most `target` lanes above it, counted exactly, is kept when
+            // its entries fit the list's slots (a step up, at most twice, when they do not); else
+            // the exact search for at most `target` entries runs.
+            const int target = min(cap, KYRO_SAMPLE_P_TARGET);
+            const int npts = min(512, (int)ceilf(span * 8.f));
+            int j = bisect_lanes(target, npts);
+            int cj = j >= 0 ? count_ge(grid_t(j)) : cap + 1;
+            for (int step = 0; step < 2 && cj > cap && j > 0; ++step) cj = count_ge(grid_t(--j));
+            if (j >= 0 && cj <= cap) {
                 thr = grid_t(j);
-                cnt = clo;
+                cnt = cj;
+            } else {
+                int clo, chi;
+                const int jx = bisect(target, npts, &clo, &chi);
+                if (jx >= 0) {
+                    thr = grid_t(jx);
+                    cnt = clo;
+                }
             }
         }
     }
