@@ -98,11 +98,12 @@ def test_rows_the_chunk_lists_do_not_cover(gpu, V, scale, kw):
     run_both(x, T, u, gpu, **args)
 
 
-@pytest.mark.parametrize("V", [50001, 200000])
+@pytest.mark.parametrize("V", [50001, 200000, 1000003])
 def test_list_shapes(gpu, V):
     """Vocabularies whose chunk lists take other shapes: 50001 entries (not a multiple of four:
     scalar loads, a short last chunk) and 200000 (49 chunks, so 167 list slots a chunk instead of
-    256). Top-k, top-p and both, with one row masked down to fewer allowed tokens than k."""
+    256), 1000003 (245 chunks: 33 slots, fewer than some k). Top-k, top-p and both, with one row
+    masked down to fewer allowed tokens than k."""
     rng = np.random.default_rng(V)
     B = 12
     x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
