@@ -51,11 +51,12 @@ namespace {
 
 constexpr int kRT = 1024;  // threads of the row kernel
 constexpr int kRW = kRT / 64;
-// Top-p alone: the most candidates a chunk lists above its skip bound (fewer candidates search
-// faster; lists too short to reach the cut send the row to the row gather below). 96 lost the
-// cut on the 64-row N(0, 3.75) batch; 160 and 256 cost 1.5 and 2.8 us a call there.
+// Top-p alone: the most lanes a chunk's list threshold leaves above it when the skip bound lists
+// too many (fewer candidates search faster; lists too short to reach the cut send the row to the
+// row gather below). 96 lost the cut on the 64-row N(0, 3.5) batch; 128 kept it at 0.4 us more a
+// call, 160 and 256 at 1.5 and 2.8 us more.
 #ifndef KYRO_SAMPLE_P_TARGET
-#define KYRO_SAMPLE_P_TARGET 128
+#define KYRO_SAMPLE_P_TARGET 112
 #endif
 constexpr int kBins = 2048;
 static_assert(kBins >= 2 * kSampleMaxChunks, "the select pass keeps list lengths and offsets in RowShared::cnt");
