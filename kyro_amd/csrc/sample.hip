@@ -910,22 +910,22 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     } else {
         // Top-p alone keeps a token only if p >= (1 - top_p) / V; with log Z >= this chunk's
         // max m, a token with z < m - ln(V / (1 - top_p)) is never kept (one nat of margin for
-        // rounding), so the list starts there if it fits, else at the lowest grid threshold
-        // that fits. The select pass checks that the lists reach below the cut.
+        // rounding), so the list may start there; else at a grid threshold above it. The select
+        // pass checks that the lists reach below the cut.
         const float span = logf((float)a.V / fmaxf(1.f - tp, 1e-30f)) + 1.f;
         const float skip = m - span;
-        const int cs = count_ge(skip);
+        // The skip bound is counted only when no grid point above it has more than `target` lanes
+        // (t_(npts-1) >= skip); otherwise the lowest grid threshold with at most `target` lanes
+        // above it, counted exactly, is kept when its entries fit the list's slots (a step up, at
+        // most twice, when they do not); else the exact search for at most `target` entries runs.
+        const int target = min(cap, KYRO_SAMPLE_P_TARGET);
+        const int npts = min(512, (int)ceilf(span * 8.f));
+        int j = bisect_lanes(target, npts);
+        const int cs = j == npts - 1 ? count_ge(skip) : cap + 1;
         if (cs <= cap) {
             thr = skip;
             cnt = cs;
         } else {
-            // Grid points above the skip bound only (below it every count exceeds the cap). The
-            // lowest threshold with at most `target` lanes above it, counted exactly, is kept when
-            // its entries fit the list's slots (a step up, at most twice, when they do not); else
-            // the exact search for at most `target` entries runs.
-            const int target = min(cap, KYRO_SAMPLE_P_TARGET);
-            const int npts = min(512, (int)ceilf(span * 8.f));
-            int j = bisect_lanes(target, npts);
             int cj = j >= 0 ? count_ge(grid_t(j)) : cap + 1;
             for (int step = 0; step < 2 && cj > cap && j > 0; ++step) cj = count_ge(grid_t(--j));
             if (j >= 0 && cj <= cap) {
