@@ -891,7 +891,6 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         // than k entries that far up lists every finite entry.
         // The highest grid threshold with k lanes at or above it has at least k entries there;
         // one exact count checks it fits, else the exact search runs.
-        const int fin = count_ge(-FLT_MAX);  // finite entries
         const int jl = bisect_lanes(k - 1, 512) + 1;
         const int cl = jl < 512 ? count_ge(grid_t(jl)) : -1;
         if (cl >= k && cl <= cap) {
@@ -903,8 +902,9 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             if (j < 512 && chi <= cap) {
                 thr = grid_t(j);
                 cnt = chi;
-            } else if (fin <= cap) {
-                cnt = fin;  // complete
+            } else {
+                const int fin = count_ge(-FLT_MAX);  // finite entries
+                if (fin <= cap) cnt = fin;           // complete
             }
         }
     } else {
