@@ -753,7 +753,7 @@ __global__ __launch_bounds__(kCT) void sample_prepare_kernel(SampleArgs a) {
 __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     __shared__ float s_red[kCW];
     __shared__ int s_ired[kCW];
-    __shared__ uint32_t s_wn[2 * kCW];
+    __shared__ uint32_t s_wn[3 * kCW];
     const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* y = row_ptr(a, b);
     const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
@@ -813,29 +813,18 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     // The chunk's candidate list: every entry with z >= t, for a t that keeps the list within
     // ccap entries. Counts over the block come from wave ballots (no atomics), two LDS slots per
     // wave alternating so that each count needs one barrier.
-    // The last count's ballots, threshold, LDS slot and total stay live: the list write reuses
-    // them when the list's threshold was the last one counted.
     int buf = 0;
-    u64 kmask[kCPer];
-    float kt = 0.f;
-    int kslot = 0, ktot = 0;
     auto count_ge = [&](float t) -> int {
         int n = 0;
 #pragma unroll
-        for (int i = 0; i < kCPer; ++i) {
-            kmask[i] = __ballot(x[i] >= t);
-            n += (int)__popcll(kmask[i]);
-        }
+        for (int i = 0; i < kCPer; ++i) n += (int)__popcll(__ballot(x[i] >= t));
         if (lane == 0) s_wn[buf * kCW + wave] = (uint32_t)n;
         __syncthreads();
         int tot = 0;
 #pragma unroll
         for (int w = 0; w < kCW; ++w) tot += (int)s_wn[buf * kCW + w];
-        kt = t;
-        kslot = buf;
         buf ^= 1;
-        ktot = __builtin_amdgcn_readfirstlane(tot);  // the same in every lane: keeps the searches scalar
-        return ktot;
+        return __builtin_amdgcn_readfirstlane(tot);  // the same in every lane: keeps the searches scalar
     };
     const float ninf = -__builtin_huge_valf();
     const int cap = a.ccap;
@@ -941,34 +930,38 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             }
         }
     }
-    // Write the list from the ballots of a count at its threshold (the last count on the usual
-    // paths; the others count again): entry i of a lane goes to the waves before it, plus the
-    // wave's hits at entries before i, plus its rank in entry i's ballot. A total above the cap
+    // Write the list: a block scan of the per-thread hits places every entry. The list's length
+    // is the scan's total; a total above the cap (the counts above disagreeing with the hits)
     // sends the row to the fallback instead of writing past the chunk's slots.
     const float tw = thr == ninf ? -FLT_MAX : thr;
+    uint32_t hits = 0;
     if (cnt > 0) {
-        if (kt != tw) count_ge(tw);
-        cnt = ktot <= cap ? ktot : -1;
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i)
+            if (x[i] >= tw) hits |= 1u << i;
     }
+    const uint32_t mine = (uint32_t)__popc(hits);
+    const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
+    if (lane == 63) s_wn[2 * kCW + wave] = incl;
+    __syncthreads();
+    uint32_t off = incl - mine, total = 0;
+    for (int w = 0; w < kCW; ++w) {
+        if (w < wave) off += s_wn[2 * kCW + w];
+        total += s_wn[2 * kCW + w];
+    }
+    if (cnt > 0) cnt = total <= (uint32_t)cap ? (int)total : -1;
     if (tid == 0) {
         a.cthr[(size_t)b * a.C + c] = thr;
         a.ccount[(size_t)b * a.C + c] = cnt;
     }
     if (cnt <= 0) return;
-    int run = 0;  // the same in every lane
-    for (int w = 0; w < kCW; ++w)
-        if (w < wave) run += (int)s_wn[kslot * kCW + w];
-    run = __builtin_amdgcn_readfirstlane(run);
     u64* list = a.cand + (size_t)b * kCap + (size_t)c * cap;
 #pragma unroll
-    for (int i = 0; i < kCPer; ++i) {
-        const u64 mk = kmask[i];
-        if ((mk >> lane) & 1) {
-            const int pos = run + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
-            list[pos] = ((u64)order_key(x[i]) << 32) | (uint32_t)~(uint32_t)chunk_index(v0, i, vec4);
+    for (int i = 0; i < kCPer; ++i)
+        if (hits & (1u << i)) {
+            list[off] = ((u64)order_key(x[i]) << 32) | (uint32_t)~(uint32_t)chunk_index(v0, i, vec4);
+            ++off;
         }
-        run += (int)__popcll(mk);
-    }
 }
 
 // Settles a top-k / top-p row (worker.rs:300-360) from n candidates in sh.cand (n < 0: none):
