@@ -753,7 +753,7 @@ __global__ __launch_bounds__(kCT) void sample_prepare_kernel(SampleArgs a) {
 __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
     __shared__ float s_red[kCW];
     __shared__ int s_ired[kCW];
-    __shared__ uint32_t s_wn[3 * kCW];
+    __shared__ uint32_t s_wn[2 * kCW];
     const int c = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* y = row_ptr(a, b);
     const int v0 = c * kChunk, v1 = min(a.V, v0 + kChunk);
@@ -826,6 +826,28 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         buf ^= 1;
         return __builtin_amdgcn_readfirstlane(tot);  // the same in every lane: keeps the searches scalar
     };
+    // The list at t: this thread's hits (bit i: entry i >= t), its offset among the block's hits
+    // (a block scan), and the total, which is count_ge(t); shares count_ge's LDS slots.
+    uint32_t hits = 0, off = 0;
+    auto scan_hits = [&](float t) -> int {
+        hits = 0;
+#pragma unroll
+        for (int i = 0; i < kCPer; ++i)
+            if (x[i] >= t) hits |= 1u << i;
+        const uint32_t mine = (uint32_t)__popc(hits);
+        const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
+        if (lane == 63) s_wn[buf * kCW + wave] = incl;
+        __syncthreads();
+        uint32_t o = incl - mine, tot = 0;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) {
+            if (w < wave) o += s_wn[buf * kCW + w];
+            tot += s_wn[buf * kCW + w];
+        }
+        buf ^= 1;
+        off = o;
+        return __builtin_amdgcn_readfirstlane((int)tot);
+    };
     const float ninf = -__builtin_huge_valf();
     const int cap = a.ccap;
     // Thresholds on a grid below the chunk's max: t_j = m - j / 8, j < npts (at most 512: 64 nats).
@@ -870,8 +892,9 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         }
         return lo;
     };
-    float thr = ninf;  // -inf: every finite entry (a complete list)
-    int cnt = -1;      // -1: no threshold keeps the list within cap
+    float thr = ninf;     // -inf: every finite entry (a complete list)
+    int cnt = -1;         // -1: no threshold keeps the list within cap
+    bool listed = false;  // hits and off already hold the list at thr
     if (m == ninf) {
         cnt = 0;  // nothing finite in the chunk
     } else if (use_k) {
@@ -881,10 +904,11 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
         // The highest grid threshold with k lanes at or above it has at least k entries there;
         // one exact count checks it fits, else the exact search runs.
         const int jl = bisect_lanes(k - 1, 512) + 1;
-        const int cl = jl < 512 ? count_ge(grid_t(jl)) : -1;
+        const int cl = jl < 512 ? scan_hits(grid_t(jl)) : -1;
         if (cl >= k && cl <= cap) {
             thr = grid_t(jl);
             cnt = cl;
+            listed = true;
         } else {
             int clo, chi;
             const int j = bisect(k - 1, 512, &clo, &chi) + 1;
@@ -915,11 +939,16 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             thr = skip;
             cnt = cs;
         } else {
-            int cj = j >= 0 ? count_ge(grid_t(j)) : cap + 1;
-            for (int step = 0; step < 2 && cj > cap && j > 0; ++step) cj = count_ge(grid_t(--j));
+            int cj = j >= 0 ? scan_hits(grid_t(j)) : cap + 1;
+            bool at_j = true;
+            for (int step = 0; step < 2 && cj > cap && j > 0; ++step) {
+                cj = count_ge(grid_t(--j));
+                at_j = false;
+            }
             if (j >= 0 && cj <= cap) {
                 thr = grid_t(j);
                 cnt = cj;
+                listed = at_j;
             } else {
                 int clo, chi;
                 const int jx = bisect(target, npts, &clo, &chi);
@@ -930,26 +959,14 @@ __global__ __launch_bounds__(kCT) void sample_stats_kernel(SampleArgs a) {
             }
         }
     }
-    // Write the list: a block scan of the per-thread hits places every entry. The list's length
-    // is the scan's total; a total above the cap (the counts above disagreeing with the hits)
-    // sends the row to the fallback instead of writing past the chunk's slots.
-    const float tw = thr == ninf ? -FLT_MAX : thr;
-    uint32_t hits = 0;
+    // Write the list: a block scan of the per-thread hits places every entry (done above when
+    // the threshold's exact count came from it). The list's length is the scan's total; a total
+    // above the cap (the counts above disagreeing with the hits) sends the row to the fallback
+    // instead of writing past the chunk's slots.
     if (cnt > 0) {
-#pragma unroll
-        for (int i = 0; i < kCPer; ++i)
-            if (x[i] >= tw) hits |= 1u << i;
+        const int total = listed ? cnt : scan_hits(thr == ninf ? -FLT_MAX : thr);
+        cnt = total <= cap ? total : -1;
     }
-    const uint32_t mine = (uint32_t)__popc(hits);
-    const uint32_t incl = (uint32_t)wave_incl_scan_i((int)mine);
-    if (lane == 63) s_wn[2 * kCW + wave] = incl;
-    __syncthreads();
-    uint32_t off = incl - mine, total = 0;
-    for (int w = 0; w < kCW; ++w) {
-        if (w < wave) off += s_wn[2 * kCW + w];
-        total += s_wn[2 * kCW + w];
-    }
-    if (cnt > 0) cnt = total <= (uint32_t)cap ? (int)total : -1;
     if (tid == 0) {
         a.cthr[(size_t)b * a.C + c] = thr;
         a.ccount[(size_t)b * a.C + c] = cnt;
