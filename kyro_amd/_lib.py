@@ -137,6 +137,8 @@ _SIGNATURES = {
     "kyro_ngram_size": ([_P], ctypes.c_int64),
     "kyro_ngram_upload": ([_P, _P], ctypes.c_int),
     "kyro_ngram_draft": ([_P, _P, ctypes.c_int32, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
+    # include/kyro_testing.h
+    "kyro_testing_set_plan_slot_cap": ([ctypes.c_int64], ctypes.c_int64),
 }
 
 

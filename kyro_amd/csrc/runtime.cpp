@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -16,10 +17,14 @@
 
 #include "context.hpp"
 #include "kernels.hpp"
+#include "kyro_testing.h"
 #include "kyro_verify.h"
 
 namespace {
 thread_local std::string g_last_error;
+// Partial-state slots a balanced-schedule launch sizes at most (0: the bound); set only through
+// kyro_testing_set_plan_slot_cap.
+std::atomic<int64_t> g_test_plan_slot_cap{0};
 }  // namespace
 
 struct kyro_buf_s {
@@ -297,12 +302,11 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
         a.splits = 1;
         s.plan_slots = (size_t)kyro::plan_slot_bound(a.B, a.ugroups / a.B, a.row_groups, mb, a.plan_max_chunk,
                                                      a.plan_grid, chunk_quarters);
-        // KYRO_TEST_PLAN_SLOT_CAP lowers the slots sized, so that a test can drive the device
-        // plan's overflow check (ERR_PLAN, no item runs) without a plan/bound mismatch.
-        if (const char* cap = std::getenv("KYRO_TEST_PLAN_SLOT_CAP")) {
-            const long long c = std::atoll(cap);
-            if (c > 0 && (size_t)c < s.plan_slots) s.plan_slots = (size_t)c;
-        }
+        // kyro_testing_set_plan_slot_cap lowers the slots sized, so that a test can drive the
+        // device plan's overflow check (ERR_PLAN, no item runs) without a plan/bound mismatch.
+        // Zero (the state a process starts in) sizes the bound.
+        const int64_t cap = g_test_plan_slot_cap.load(std::memory_order_relaxed);
+        if (cap > 0 && (size_t)cap < s.plan_slots) s.plan_slots = (size_t)cap;
         a.plan_slots = (long long)s.plan_slots;
     }
     // One launch carries at most 2^32 - 1 work items along x.
@@ -433,6 +437,10 @@ const char* kyro_last_error(void) { return g_last_error.c_str(); }
 
 int kyro_abi_version(void) { return KYRO_ABI_VERSION; }
 
+int64_t kyro_testing_set_plan_slot_cap(int64_t cap) {
+    return g_test_plan_slot_cap.exchange(cap < 0 ? 0 : cap, std::memory_order_relaxed);
+}
+
 int kyro_ctx_create(int device, kyro_ctx* out) {
     return guarded([&]() -> int {
         if (!out) return fail(KYRO_EINVAL, "kyro_ctx_create: out is null");
@@ -453,7 +461,12 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device);
         if (e == hipSuccess && ctx->num_cus <= 0) e = hipErrorInvalidDevice;
         // Set-up of kyro_spec_verify_noalloc: the static scratch array's address on this device.
-        if (e == hipSuccess) e = kyro::noalloc_scratch(device, &ctx->noalloc_scratch);
+        // That entry point is optional: when the lookup fails the context is still created,
+        // noalloc_scratch stays null and only kyro_spec_verify_noalloc reports KYRO_EHIP.
+        if (e == hipSuccess && kyro::noalloc_scratch(device, &ctx->noalloc_scratch) != hipSuccess) {
+            ctx->noalloc_scratch = nullptr;
+            (void)hipGetLastError();  // the failed lookup must not surface from a later call
+        }
         if (e == hipSuccess) e = hipStreamSynchronize(0);  // the memsets are done before any launch
         if (e != hipSuccess) {
             if (ctx->err) (void)hipFree(ctx->err);
@@ -623,6 +636,8 @@ int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_para
     return guarded([&]() -> int {
         if (!bytes) return fail(KYRO_EINVAL, "paged_attention_workspace: bytes is null");
         *bytes = 0;
+        // A null context sizes for kDefaultCUs (256) compute units; a device with more needs its
+        // context here, since the balanced schedule's persistent grid follows the CU count.
         AttnSetup s;
         if (int rc = attention_setup(p, has_q_start_loc != 0, ctx ? ctx->num_cus : kDefaultCUs, s)) return rc;
         *bytes = s.ws_bytes;

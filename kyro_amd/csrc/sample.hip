@@ -1381,6 +1381,9 @@ __global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
         sh.cnt[tid] = (uint32_t)cpos;
         sh.cnt[kSampleMaxChunks + tid] = (uint32_t)coff;
     }
+    // Publishes sh.cnt to the copy below, and ends every wave's reads of sh.ired before
+    // key_range_prefix rewrites it. Top-k rows take no other barrier on the way.
+    __syncthreads();
     // Top-p alone: every list reaches down to its threshold, so all of them hold every token at
     // or above the largest one.
     const float tmax = use_k ? -__builtin_huge_valf() : block_max_f(tid < C ? thr : -__builtin_huge_valf(), sh);

@@ -316,19 +316,24 @@ def test_balanced_schedule_replays_from_a_graph(gpu, H):
         assert torch.equal(again, eager2)
 
 
-def test_balanced_schedule_slot_overflow_latches_an_error(gpu, monkeypatch):
+def test_balanced_schedule_slot_overflow_latches_an_error(gpu):
     """With fewer partial-state slots sized than the plan needs (forced from the host through
-    KYRO_TEST_PLAN_SLOT_CAP), the device plan latches an error and runs no item instead of
-    writing past the workspace; the next call, sized normally, gives the oracle's result."""
+    the test-only kyro_testing_set_plan_slot_cap), the device plan latches an error and runs no
+    item instead of writing past the workspace; the next call, sized normally, gives the
+    oracle's result."""
+    from kyro_amd import _lib
+
     case = wl.make_attention_case(context_lens=[5000, 40, 3000, 700], q_lens=[8, 3, 5, 1], num_heads=32,
                                   num_kv_heads=8, dtype="bf16", seed=31)
     t = h.attention_tensors(case, gpu)
     attn = make_attention(16, 32, 128, 8)
     args = (t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"])
-    monkeypatch.setenv("KYRO_TEST_PLAN_SLOT_CAP", "3")
-    with pytest.raises(kyro_amd.KyroError, match="partial-state slots"):
-        attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
-    monkeypatch.delenv("KYRO_TEST_PLAN_SLOT_CAP")
+    assert _lib.lib().kyro_testing_set_plan_slot_cap(3) == 0
+    try:
+        with pytest.raises(kyro_amd.KyroError, match="partial-state slots"):
+            attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
+    finally:
+        assert _lib.lib().kyro_testing_set_plan_slot_cap(0) == 3
     out = attn.forward(*args, q_start_loc=t["q_start_loc"], schedule="balanced")
     h.assert_attention_close(out, case, h.oracle_attention(case), h.ATOL_BF16)
 
