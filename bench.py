@@ -367,14 +367,48 @@ def ngram_draft_workload(warmup, steps):
                                        "table of the oracle"}}), flush=True)
 
 
-def other_workload(name, warmup, steps):
-    """One JSON line for a non-default workload: the attention kernel (when the workload has one)
-    and the sampler (when it has one), each on its algorithmic bytes. Inputs come from
-    kyro_amd.workloads (seeded numpy), uploaded before timing."""
+def _cold_median_us(fn, steps, scratch):
+    """Median per-call time of fn() in µs from HIP events on the current stream, each call after a
+    read of `scratch` (512 MiB) that evicts the L2s and the MALL, as for the headline step."""
+    import numpy as np
+    import torch
+
+    import kyro_amd
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e0, e1 in ev:
+        scratch.sum()
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    kyro_amd.sync(0)
+    return float(np.median([e0.elapsed_time(e1) for e0, e1 in ev])) * 1e3
+
+
+CONFIG_WORKLOADS = {
+    "rejection-b8": "rejection sampling only: batch 8, k 4, V 32000, T 1.0",
+    "mha-llama2-7b": "paged attention, Llama-2-7B layer: MHA 32/32, head_dim 128, batch 16, ctx U[512, 2048], q 5",
+    "skewed-prefix": "skewed long-context verify: batch 32, ctx log-U[128, 32768], 64 shared prefix blocks, "
+                     "GQA 32/8, k 4, V 128256, T 1.0",
+    "mixed-llama3-70b": "mixed batch: 128 sequences, k U{0..8}, ctx U[256, 8192], GQA 64/8, V 128256, "
+                        "half greedy, half T 0.7",
+}
+
+
+def measure_config(name, warmup, steps, detailed=False, scratch=None):
+    """Attention (when the workload has one) and sampler (when it has one) of a non-default
+    workload, each on its algorithmic bytes, as a dict. With `scratch` (a 512 MiB tensor) each
+    part is also timed cold, after a cache-evicting read. `detailed` adds the vector and MFMA
+    paths, the "shared" kv_reuse hint and the CPU oracle. Inputs come from kyro_amd.workloads
+    (seeded numpy), uploaded before timing."""
     import torch
 
     import kyro_amd
     from kyro_amd import workloads as wl
+    from kyro_amd.attention import describe_attention
+    from kyro_amd.speculative import describe_verify
 
     dev = torch.device("cuda", 0)
 
@@ -394,7 +428,7 @@ def other_workload(name, warmup, steps):
         vcase = wl.verify_mixed(k)
     else:
         raise SystemExit(f"unknown workload {name}")
-    line = {"workload": name}
+    line = {"workload": name, "description": CONFIG_WORKLOADS[name]}
     total_us = 0.0
     if acase is not None:
         bf16 = acase.dtype == "bf16"
@@ -407,62 +441,83 @@ def other_workload(name, warmup, steps):
         # The library's default kv_reuse hint (AUTO). Where tables share blocks (a common prefix)
         # the "shared" hint, which keeps K/V loads cacheable, is timed beside it.
         res = {"logical_bytes": logical, "unique_bytes": unique, "context_tokens": int(acase.context_lens.sum()),
-               "kv_reuse": "auto"}
-        runs = [("auto", "auto"), ("vector", "auto"), ("mfma", "auto")]
-        if acase.unique_kv_bytes() < acase.kv_bytes():
-            runs.append(("auto", "shared"))
+               "kv_reuse": "auto",
+               "launch": describe_attention(attn, batch=acase.batch, total_q=int(acase.q_start_loc[-1]),
+                                            max_q_len=acase.max_q_len, max_blocks_per_seq=acase.block_table.shape[1],
+                                            num_blocks=acase.key_cache.shape[0],
+                                            dtype=torch.bfloat16 if bf16 else torch.float32, device=0)}
+        runs = [("auto", "auto")]
+        if detailed:
+            runs += [("vector", "auto"), ("mfma", "auto")]
+            if acase.unique_kv_bytes() < acase.kv_bytes():
+                runs.append(("auto", "shared"))
         for path, reuse in runs:
-            us = _median_us(lambda: attn.forward_async(
+            fn = lambda: attn.forward_async(  # noqa: E731
                 t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"],
-                max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path, kv_reuse=reuse),
-                warmup, steps)
-            res[path if reuse == "auto" else f"{path}_kv_reuse_{reuse}"] = {
-                "us": us, "GB_s_unique": unique / us / 1e3, "frac_unique": unique / us / 1e3 / PEAK_HBM_GBS,
-                "GB_s_logical": logical / us / 1e3}
+                max_q_len=acase.max_q_len, out_dtype=torch.bfloat16, out=out, path=path, kv_reuse=reuse)
+            us = _median_us(fn, warmup, steps)
+            entry = {"us": us, "GB_s_unique": unique / us / 1e3, "frac_unique": unique / us / 1e3 / PEAK_HBM_GBS,
+                     "GB_s_logical": logical / us / 1e3}
+            if scratch is not None and path == "auto" and reuse == "auto":
+                cus = _cold_median_us(fn, steps, scratch)
+                entry.update({"us_cold": cus, "frac_unique_cold": unique / cus / 1e3 / PEAK_HBM_GBS})
+            res[path if reuse == "auto" else f"{path}_kv_reuse_{reuse}"] = entry
         res["roofline"] = _roofline(unique, res["auto"]["us"])
-        # CPU: the oracle's attention (f32 build, 16 threads) on the first two sequences
-        import oracle
+        if detailed:
+            # CPU: the oracle's attention (f32 build, 16 threads) on the first two sequences
+            import oracle
 
-        n2 = min(2, acase.batch)
-        nb2 = int(((acase.context_lens[:n2] + acase.block_size - 1) // acase.block_size).max())
-        q2 = int(acase.q_start_loc[n2])
-        sec = _cpu_seconds(lambda: oracle.paged_attention_mq(
-            acase.query[:q2], acase.key_cache, acase.value_cache, acase.block_table[:n2, :nb2],
-            acase.context_lens[:n2], num_heads=acase.num_heads, num_kv_heads=acase.num_kv_heads,
-            head_dim=acase.head_dim, block_size=acase.block_size, q_start_loc=acase.q_start_loc[:n2 + 1],
-            threads=16, precision="f32"), min_seconds=1.0)
-        kv2 = int(acase.context_lens[:n2].sum()) * acase.num_kv_heads * acase.head_dim * 2 * 2
-        res["cpu_baseline"] = {"value": kv2 / sec / 1e9, "unit": "GB/s of KV", "cores": 16, "kind": "port",
-                               "sample": f"the first {n2} sequences, oracle paged attention (f32)"}
+            n2 = min(2, acase.batch)
+            nb2 = int(((acase.context_lens[:n2] + acase.block_size - 1) // acase.block_size).max())
+            q2 = int(acase.q_start_loc[n2])
+            sec = _cpu_seconds(lambda: oracle.paged_attention_mq(
+                acase.query[:q2], acase.key_cache, acase.value_cache, acase.block_table[:n2, :nb2],
+                acase.context_lens[:n2], num_heads=acase.num_heads, num_kv_heads=acase.num_kv_heads,
+                head_dim=acase.head_dim, block_size=acase.block_size, q_start_loc=acase.q_start_loc[:n2 + 1],
+                threads=16, precision="f32"), min_seconds=1.0)
+            kv2 = int(acase.context_lens[:n2].sum()) * acase.num_kv_heads * acase.head_dim * 2 * 2
+            res["cpu_baseline"] = {"value": kv2 / sec / 1e9, "unit": "GB/s of KV", "cores": 16, "kind": "port",
+                                   "sample": f"the first {n2} sequences, oracle paged attention (f32)"}
         line["attention"] = res
         total_us += res["auto"]["us"]
     if vcase is not None:
         vt = dict(target_logits=up(vcase.target), draft_logits=up(vcase.draft),
                   draft_tokens=up(vcase.draft_tokens.astype("int32")), num_draft=up(vcase.num_draft),
                   temperature=up(vcase.temperature), u_accept=up(vcase.u_accept), u_resample=up(vcase.u_resample))
-        us = _median_us(lambda: kyro_amd.verify_drafts_async(**vt), warmup, steps)
+        fn = lambda: kyro_amd.verify_drafts_async(**vt)  # noqa: E731
+        us = _median_us(fn, warmup, steps)
         r = kyro_amd.verify_drafts(**vt)
         emitted = int((r.accepted.cpu() + 1).sum().item())
         s_bytes = vcase.logit_bytes(r.accepted.cpu().numpy())
-        line["sampler"] = {"us": us, "algorithmic_bytes": s_bytes, "GB_s": s_bytes / us / 1e3,
-                           "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1,
-                           "roofline": _roofline(s_bytes, us)}
-        # CPU: the oracle's acceptance (f32 build, one thread) on up to 8 sequences
-        import oracle
+        line["sampler"] = {"us": us, "algorithmic_bytes": s_bytes, "all_rows_bytes": int(vcase.target.nbytes + vcase.draft.nbytes),
+                           "GB_s": s_bytes / us / 1e3, "tokens": emitted, "mean_accepted": emitted / vcase.batch - 1,
+                           "roofline": _roofline(s_bytes, us),
+                           "launch": describe_verify(vcase.batch, vcase.draft_tokens.shape[1], vcase.target.shape[2])}
+        if scratch is not None:
+            line["sampler"]["us_cold"] = _cold_median_us(fn, steps, scratch)
+        if detailed:
+            # CPU: the oracle's acceptance (f32 build, one thread) on up to 8 sequences
+            import oracle
 
-        n8 = min(8, vcase.batch)
-        sec = _cpu_seconds(lambda: oracle.spec_verify(
-            vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8], vcase.num_draft[:n8],
-            vcase.temperature[:n8], vcase.u_accept[:n8], vcase.u_resample[:n8], precision="f32"), min_seconds=1.0)
-        r8 = oracle.spec_verify(vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8],
-                                vcase.num_draft[:n8], vcase.temperature[:n8], vcase.u_accept[:n8],
-                                vcase.u_resample[:n8], precision="f32")
-        line["sampler"]["cpu_baseline"] = {"value": float((r8["accepted"] + 1).sum()) / sec, "unit": "tok/s",
-                                           "cores": 1, "kind": "port",
-                                           "sample": f"the first {n8} sequences, oracle acceptance (f32)"}
+            n8 = min(8, vcase.batch)
+            sec = _cpu_seconds(lambda: oracle.spec_verify(
+                vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8], vcase.num_draft[:n8],
+                vcase.temperature[:n8], vcase.u_accept[:n8], vcase.u_resample[:n8], precision="f32"), min_seconds=1.0)
+            r8 = oracle.spec_verify(vcase.target[:n8], vcase.draft[:n8], vcase.draft_tokens[:n8],
+                                    vcase.num_draft[:n8], vcase.temperature[:n8], vcase.u_accept[:n8],
+                                    vcase.u_resample[:n8], precision="f32")
+            line["sampler"]["cpu_baseline"] = {"value": float((r8["accepted"] + 1).sum()) / sec, "unit": "tok/s",
+                                               "cores": 1, "kind": "port",
+                                               "sample": f"the first {n8} sequences, oracle acceptance (f32)"}
         total_us += us
         line["verified_tok_s_at_measured_parts"] = emitted / (total_us * 1e-6)
-    print(json.dumps(line), flush=True)
+    return line
+
+
+def other_workload(name, warmup, steps):
+    """One JSON line for a non-default workload (measure_config with the vector and MFMA paths,
+    the "shared" hint and the CPU oracle)."""
+    print(json.dumps(measure_config(name, warmup, steps, detailed=True)), flush=True)
 
 
 def main():
@@ -478,6 +533,8 @@ def main():
                     help="draft positions read before the first acceptance scan (0 = library default)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="sequences in the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other four workloads' figures in the benchmark line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run 5 device-to-device copies of MIB MiB (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings), then exit")
@@ -622,6 +679,38 @@ def main():
             m = re.search(r"^hbm_bytes_per_launch:\s*(\d+)", f.read(), flags=re.M)
         traffic = int(m.group(1)) if m else None
 
+    # The other four workloads of the benchmark's configuration list, timed the same way (cold:
+    # after a cache-evicting read; warm: back to back), so that the one JSON line carries every
+    # configuration. The Llama-3-8B step's inputs are freed first.
+    from kyro_amd.attention import describe_attention
+    from kyro_amd.speculative import describe_verify
+
+    del x
+    torch.cuda.empty_cache()
+    configs = {}
+    if not args.no_configs:
+        scratch = torch.ones(128 << 20, dtype=torch.float32, device=dev)
+        for n in ("rejection-b8", "mha-llama2-7b", "skewed-prefix", "mixed-llama3-70b"):
+            configs[n] = measure_config(n, 10, 50, scratch=scratch)
+            torch.cuda.empty_cache()
+        del scratch
+    configs["llama3-8b"] = {
+        "workload": "llama3-8b",
+        "description": "full verify step, Llama-3-8B: GQA 32/8, head_dim 128, batch 64, ctx 4096, k 7, "
+                       "V 128256, T 0.8 (the headline)",
+        "attention": {"logical_bytes": a_bytes, "unique_bytes": a_bytes, "us": attn_ms * 1e3,
+                      "us_cold": cold["attention_us"]["median"],
+                      "frac_unique": a_bytes / (attn_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                      "frac_unique_cold": a_bytes / (cold["attention_us"]["median"] * 1e-6) / 1e9 / PEAK_HBM_GBS,
+                      "launch": describe_attention(attn, batch=B, total_q=B * (K_DRAFT + 1), max_q_len=K_DRAFT + 1,
+                                                   max_blocks_per_seq=CTX // BS, num_blocks=16384, device=0,
+                                                   path=args.path, num_splits=args.splits)},
+        "sampler": {"us": samp_ms * 1e3, "us_cold": cold["sampler_us"]["median"], "algorithmic_bytes": s_bytes,
+                    "all_rows_bytes": sampler_bytes(), "GB_s": s_bytes / (samp_ms * 1e-3) / 1e9,
+                    "tokens": emitted, "mean_accepted": emitted / B - 1,
+                    "launch": describe_verify(B, K_DRAFT, VOCAB, args.window)},
+    }
+
     baseline = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, os.cpu_count() or 1))
@@ -688,6 +777,12 @@ def main():
             "warm_instrumented": summary(events),
             "cold_cache": cold,
         },
+        "configs_note": "every configuration of the benchmark list: attention (with its combine pass) and "
+                        "sampler timed separately by HIP events, median of 50 calls; us_cold after a 512 MiB "
+                        "cache-evicting read, us back to back; frac_unique on the unique KV + Q + out bytes "
+                        "(shared prefix blocks counted once); sampler bytes are the logit rows the acceptance "
+                        "scan evaluates, each once",
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
 

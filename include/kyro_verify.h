@@ -50,7 +50,7 @@ typedef enum kyro_status {
     KYRO_EINVAL = 1,       /* bad argument, shape, or (latched) bad block id / context length */
     KYRO_EOOM = 2,         /* device allocation failed */
     KYRO_EHIP = 3,         /* a HIP runtime call failed */
-    KYRO_EUNSUPPORTED = 4, /* valid request this build has no kernel for (e.g. head_dim 96) */
+    KYRO_EUNSUPPORTED = 4, /* valid request this build has no kernel for (e.g. head_dim 100) */
     KYRO_ENOSPACE = 5      /* not enough free KV blocks, even after evicting the prefix cache */
 } kyro_status;
 
@@ -155,7 +155,7 @@ typedef enum kyro_attn_schedule {
 typedef struct kyro_paged_attention_params {
     int32_t block_size;          /* tokens per KV block (Kyro uses 16: src/model/llama.rs:46) */
     int32_t num_heads;           /* query heads H */
-    int32_t head_dim;            /* D: 64 or 128 */
+    int32_t head_dim;            /* D: a multiple of 8, at most 256 */
     int32_t num_kv_heads;        /* Hkv; H % Hkv == 0; query head h reads kv head h / (H/Hkv) */
     int32_t batch_size;          /* B */
     int32_t total_q;             /* rows of `query`: B when q_start_loc is NULL */
@@ -201,6 +201,13 @@ int kyro_paged_attention_mq(kyro_ctx ctx, const kyro_paged_attention_params* par
  * per op). */
 int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_params* params,
                                    int has_q_start_loc, size_t* bytes);
+
+/* What a kyro_paged_attention_mq call with these params launches (kernel instance, schedule,
+ * splits, workgroups), as text for logs and benchmarks. Host only, like the workspace query; ctx
+ * may be NULL (a 256-CU device). buf gets at most len bytes (terminated), *needed (may be NULL)
+ * the full length with its terminator. No counterpart in the reference. */
+int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_params* params, int has_q_start_loc,
+                                  char* buf, size_t len, size_t* needed);
 
 /* The balanced schedule's plan for one batch, computed on the host with the chunk and split
  * arithmetic the device plan runs, from host copies of the context lengths and the per-sequence
@@ -274,6 +281,11 @@ int kyro_spec_verify(kyro_ctx ctx, const kyro_spec_verify_params* params,
 /* Scratch bytes a kyro_spec_verify call with these params takes from the context's arena. Host
  * only, no device work. */
 int kyro_spec_verify_workspace(const kyro_spec_verify_params* params, size_t* bytes);
+
+/* What a kyro_spec_verify call with these params launches (window, chunking, kernels), as text
+ * for logs and benchmarks. Host only; buf gets at most len bytes (terminated), *needed (may be
+ * NULL) the full length with its terminator. No counterpart in the reference. */
+int kyro_spec_verify_describe(const kyro_spec_verify_params* params, char* buf, size_t len, size_t* needed);
 
 /* Maximum scratch of kyro_spec_verify_noalloc, in bytes (16 MiB). */
 #define KYRO_SPEC_VERIFY_NOALLOC_SCRATCH_BYTES (16u << 20)

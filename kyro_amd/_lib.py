@@ -103,6 +103,10 @@ _SIGNATURES = {
     "kyro_spec_verify": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
     "kyro_spec_verify_noalloc": ([_P, ctypes.POINTER(SpecVerifyParams)] + [_P] * 11, ctypes.c_int),
     "kyro_spec_verify_workspace": ([ctypes.POINTER(SpecVerifyParams), ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "kyro_spec_verify_describe": ([ctypes.POINTER(SpecVerifyParams), ctypes.c_char_p, ctypes.c_size_t,
+                                   ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "kyro_paged_attention_describe": ([_P, ctypes.POINTER(PagedAttentionParams), ctypes.c_int, ctypes.c_char_p,
+                                       ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "kyro_paged_kv_append": ([_P, ctypes.POINTER(KvAppendParams)] + [_P] * 7, ctypes.c_int),
     # include/kyro_blocks.h
     "kyro_radix_create": ([ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(_P)], ctypes.c_int),
@@ -217,3 +221,13 @@ def context(device: int = 0) -> Context:
     if ctx is None:
         ctx = _contexts[device] = Context(device)
     return ctx
+
+
+def describe_text(fn, *args) -> str:
+    """Calls a kyro_*_describe query (its trailing buf, len, needed arguments supplied here) and
+    returns the text."""
+    needed = ctypes.c_size_t()
+    check(fn(*args, None, 0, ctypes.byref(needed)))
+    buf = ctypes.create_string_buffer(needed.value)
+    check(fn(*args, buf, needed.value, None))
+    return buf.value.decode()

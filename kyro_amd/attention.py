@@ -138,6 +138,20 @@ class PagedAttention:
         return out
 
 
+def describe_attention(attn: PagedAttention, *, batch: int, total_q: int, max_q_len: int, max_blocks_per_seq: int,
+                       num_blocks: int, dtype=torch.bfloat16, out_dtype=torch.bfloat16, causal=True, path="auto",
+                       num_splits=0, kv_reuse="auto", schedule="auto", device=None) -> str:
+    """What ``forward`` with these shapes launches on ``device`` (kernel instance, schedule,
+    splits, workgroups), from the library's own choice (``kyro_paged_attention_describe``).
+    ``device`` None asks the host-only question for a 256-CU device (no GPU needed)."""
+    params = _lib.PagedAttentionParams(
+        attn.block_size, attn.num_heads, attn.head_dim, attn.num_kv_heads, int(batch), int(total_q),
+        int(max_blocks_per_seq), int(num_blocks), _DTYPES[dtype], _DTYPES[out_dtype], 1 if causal else 0, 0.0,
+        _PATHS[path], int(num_splits), int(max_q_len), _KV_REUSE[kv_reuse], _SCHEDULES[schedule])
+    handle = _lib.context(device).handle if device is not None else None
+    return _lib.describe_text(_lib.lib().kyro_paged_attention_describe, handle, ctypes.byref(params), 1)
+
+
 def attention_plan(attn: PagedAttention, context_lens, q_lens=None, *, max_blocks_per_seq: int,
                    num_blocks: int = 1, dtype=torch.bfloat16, schedule: str = "balanced",
                    num_cus: int = 0, chunk_quarters: int = 0):

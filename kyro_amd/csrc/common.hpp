@@ -42,6 +42,14 @@ __device__ __forceinline__ float row16_sum(float v) {
     return v;
 }
 
+// Sum over each 8-lane half-row with DPP; every lane of the half-row gets its total.
+__device__ __forceinline__ float row8_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return v;
+}
+
 // DPP copy of v from another lane (ctrl: a DPP control code, rmask: the 16-lane rows written);
 // lanes whose source lies outside the row, or rows outside rmask, get 0.
 #define KYRO_DPP(v, ctrl, rmask) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (rmask), 0xf, false)

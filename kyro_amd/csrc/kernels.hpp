@@ -130,6 +130,14 @@ __host__ __device__ inline long long plan_slot_bound(long long B, long long ugro
 // 2 * kMfmaMaxPairsPerWave * (kernel waves per head) blocks.
 constexpr int kMfmaMaxPairsPerWave = 128;
 
+// Head dims the attention kernels take: the vector kernel every multiple of 8 up to
+// kMaxHeadDim (X(d) is applied to each), the bf16 MFMA kernel the ones listed below.
+constexpr int kMaxHeadDim = 256;
+#define KYRO_HEAD_DIMS(X)                                                                           \
+    X(8) X(16) X(24) X(32) X(40) X(48) X(56) X(64) X(72) X(80) X(88) X(96) X(104) X(112) X(120)     \
+    X(128) X(136) X(144) X(152) X(160) X(168) X(176) X(184) X(192) X(200) X(208) X(216) X(224)      \
+    X(232) X(240) X(248) X(256)
+
 // Query rows one attention workgroup covers.
 constexpr int kVectorRowsPerGroup = 8;
 // MFMA kernels: one 16-row tile, two (32 rows), or for bf16 units of more than 32 rows four

@@ -236,6 +236,7 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
     if (unit >= a.units) return;
     const SeqInfo si = seq_info(a, unit);
     if (!si.ok) return;
+    if ((int)threadIdx.x >= RPW * Q) return;  // head dims that do not divide the workgroup
     const int n = blockIdx.y * RPW + (int)threadIdx.x / Q;
     if (n >= si.rows) return;
     const int nsplit = num_splits_for(a, si.nblk);
@@ -1508,17 +1509,33 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_f32_kernel(AttnArgs a) {
 
 template <typename T>
 struct Elem;
+// N consecutive elements at p, in the widest loads their alignment allows: a lane's slice starts
+// at a multiple of N elements of a row that starts 16-byte aligned (the head dim is a multiple
+// of 8), so N divisible by 4 (f32) or 8 (bf16) gives 16-byte loads, and smaller powers of two
+// narrower ones.
 template <>
 struct Elem<float> {
     template <int N>
     __device__ static __forceinline__ void load(const float* p, float (&x)[N]) {
+        if constexpr (N % 4 == 0) {
 #pragma unroll
-        for (int i = 0; i < N; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(p + i);
-            x[i] = v.x;
-            x[i + 1] = v.y;
-            x[i + 2] = v.z;
-            x[i + 3] = v.w;
+            for (int i = 0; i < N; i += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(p + i);
+                x[i] = v.x;
+                x[i + 1] = v.y;
+                x[i + 2] = v.z;
+                x[i + 3] = v.w;
+            }
+        } else if constexpr (N % 2 == 0) {
+#pragma unroll
+            for (int i = 0; i < N; i += 2) {
+                const float2 v = *reinterpret_cast<const float2*>(p + i);
+                x[i] = v.x;
+                x[i + 1] = v.y;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) x[i] = p[i];
         }
     }
 };
@@ -1526,34 +1543,61 @@ template <>
 struct Elem<uint16_t> {
     template <int N>
     __device__ static __forceinline__ void load(const uint16_t* p, float (&x)[N]) {
+        if constexpr (N % 8 == 0) {
 #pragma unroll
-        for (int i = 0; i < N; i += 8) {
-            const uint4 v = load16(p + i);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            for (int i = 0; i < N; i += 8) {
+                const uint4 v = load16(p + i);
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int k = 0; k < 4 && i + 2 * k < N; ++k) {
-                x[i + 2 * k] = bf16_lo(w[k]);
-                x[i + 2 * k + 1] = bf16_hi(w[k]);
+                for (int k = 0; k < 4; ++k) {
+                    x[i + 2 * k] = bf16_lo(w[k]);
+                    x[i + 2 * k + 1] = bf16_hi(w[k]);
+                }
             }
+        } else if constexpr (N % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < N; i += 4) {
+                const uint2 v = *reinterpret_cast<const uint2*>(p + i);
+                x[i] = bf16_lo(v.x);
+                x[i + 1] = bf16_hi(v.x);
+                x[i + 2] = bf16_lo(v.y);
+                x[i + 3] = bf16_hi(v.y);
+            }
+        } else if constexpr (N % 2 == 0) {
+#pragma unroll
+            for (int i = 0; i < N; i += 2) {
+                const uint32_t v = *reinterpret_cast<const uint32_t*>(p + i);
+                x[i] = bf16_lo(v);
+                x[i + 1] = bf16_hi(v);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) x[i] = __uint_as_float((uint32_t)p[i] << 16);
         }
     }
 };
-// D = 64 bf16 gives 4 elements (8 bytes) per lane.
-template <>
-__device__ __forceinline__ void Elem<uint16_t>::load<4>(const uint16_t* p, float (&x)[4]) {
-    const uint2 v = *reinterpret_cast<const uint2*>(p);
-    x[0] = bf16_lo(v.x);
-    x[1] = bf16_hi(v.x);
-    x[2] = bf16_lo(v.y);
-    x[3] = bf16_hi(v.y);
-}
 
 constexpr int kVecRows = kVectorRowsPerGroup;
 
+// Lanes that share one token row of the vector kernel: 16 when the head dim is a multiple of
+// 16, else 8 (head dims 8, 24, 40, ...).
+template <int D>
+constexpr int kVecLanesPerRow = D % 16 == 0 ? 16 : 8;
+
+// Sum over the lanes of one token row.
+template <int LPR>
+__device__ __forceinline__ float token_row_sum(float v) {
+    if constexpr (LPR == 16) return row16_sum(v);
+    else return row8_sum(v);
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
+    static_assert(D % 8 == 0 && D <= kMaxHeadDim, "head dim: a multiple of 8, at most kMaxHeadDim");
     constexpr int R = kVecRows;
-    constexpr int DPL = D / 16;  // head-dim elements per lane
+    constexpr int LPR = kVecLanesPerRow<D>;
+    constexpr int DPL = D / LPR;   // head-dim elements per lane
+    constexpr int TPW = 64 / LPR;  // token rows a wave takes per step
     __shared__ Frame<R, D> frame;
 
     int unit, split, rg;
@@ -1567,8 +1611,8 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int r = lane & 15;  // head-dim slice [r * DPL, r * DPL + DPL)
-    const int g = lane >> 4;  // token row within the wave's 4
+    const int r = lane % LPR;  // head-dim slice [r * DPL, r * DPL + DPL)
+    const int g = lane / LPR;  // token row within the wave's TPW
     const T* __restrict__ qp = reinterpret_cast<const T*>(a.q);
     const T* __restrict__ kp = reinterpret_cast<const T*>(a.k);
     const T* __restrict__ vp = reinterpret_cast<const T*>(a.v);
@@ -1600,7 +1644,7 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
             for (int d = 0; d < DPL; ++d) acc[i][d] = 0.f;
         }
 
-        for (int t0 = t_begin + 4 * wave; t0 < t_end; t0 += 4 * kWaves) {
+        for (int t0 = t_begin + TPW * wave; t0 < t_end; t0 += TPW * kWaves) {
             const int t = t0 + g;
             const bool tok_ok = t < t_end;
             int64_t blk = -1;
@@ -1619,7 +1663,7 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
                 float s = 0.f;
 #pragma unroll
                 for (int d = 0; d < DPL; ++d) s += q[i][d] * kx[d];
-                s = row16_sum(s);
+                s = token_row_sum<LPR>(s);
                 s = (blk >= 0 && t < vis[i]) ? s * a.scale_log2 : kNegInf;
                 const float m_new = fmaxf(m[i], s);
                 const float mref = (m_new == kNegInf) ? 0.f : m_new;
@@ -1632,21 +1676,22 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
             }
         }
 
-        // Fold the four token rows of the wave (16-lane groups), then merge waves in LDS.
+        // Fold the wave's TPW token rows (LPR-lane groups), then merge waves in LDS.
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            float M = fmaxf(m[i], shfl_xor_f(m[i], 16));
-            M = fmaxf(M, shfl_xor_f(M, 32));
+            float M = m[i];
+#pragma unroll
+            for (int x = LPR; x < 64; x *= 2) M = fmaxf(M, shfl_xor_f(M, x));
             const float f = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - M);
             l[i] *= f;
-            l[i] += shfl_xor_f(l[i], 16);
-            l[i] += shfl_xor_f(l[i], 32);
+#pragma unroll
+            for (int x = LPR; x < 64; x *= 2) l[i] += shfl_xor_f(l[i], x);
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
-                float x = acc[i][d] * f;
-                x += shfl_xor_f(x, 16);
-                x += shfl_xor_f(x, 32);
-                acc[i][d] = x;
+                float v = acc[i][d] * f;
+#pragma unroll
+                for (int x = LPR; x < 64; x *= 2) v += shfl_xor_f(v, x);
+                acc[i][d] = v;
             }
             m[i] = M;
         }
@@ -1732,12 +1777,16 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
 #undef KYRO_MFMA_LAUNCH2
     } else {
         const bool bf16 = a.dtype_bf16;
-        if (a.D == 128) {
-            if (bf16) attn_vector_kernel<uint16_t, 128><<<grid, block, 0, stream>>>(a);
-            else attn_vector_kernel<float, 128><<<grid, block, 0, stream>>>(a);
-        } else {
-            if (bf16) attn_vector_kernel<uint16_t, 64><<<grid, block, 0, stream>>>(a);
-            else attn_vector_kernel<float, 64><<<grid, block, 0, stream>>>(a);
+        switch (a.D) {  // the host admits multiples of 8 up to kMaxHeadDim
+#define KYRO_VEC_CASE(DD)                                                                  \
+            case DD:                                                                       \
+                if (bf16) attn_vector_kernel<uint16_t, DD><<<grid, block, 0, stream>>>(a); \
+                else attn_vector_kernel<float, DD><<<grid, block, 0, stream>>>(a);         \
+                break;
+            KYRO_HEAD_DIMS(KYRO_VEC_CASE)
+#undef KYRO_VEC_CASE
+            default:
+                return hipErrorInvalidValue;
         }
     }
     if (a.plan) {
@@ -1749,8 +1798,16 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     } else if (a.splits > 1) {
         const int rpw = kThreads / (a.D / 4);
         const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
-        if (a.D == 128) attn_combine_kernel<128><<<cgrid, block, 0, stream>>>(a);
-        else attn_combine_kernel<64><<<cgrid, block, 0, stream>>>(a);
+        switch (a.D) {
+#define KYRO_COMBINE_CASE(DD)                                                   \
+            case DD:                                                            \
+                attn_combine_kernel<DD><<<cgrid, block, 0, stream>>>(a);        \
+                break;
+            KYRO_HEAD_DIMS(KYRO_COMBINE_CASE)
+#undef KYRO_COMBINE_CASE
+            default:
+                return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }

@@ -179,8 +179,9 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (!have_q_start && p->total_q != p->batch_size)
         return fail(KYRO_EINVAL, "paged_attention: total_q %d != batch_size %d without q_start_loc",
                     p->total_q, p->batch_size);
-    if (p->head_dim != 64 && p->head_dim != 128)
-        return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: 64, 128)", p->head_dim);
+    if (p->head_dim % 8 != 0 || p->head_dim > kyro::kMaxHeadDim)
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: head_dim %d (supported: multiples of 8 up to %d)",
+                    p->head_dim, kyro::kMaxHeadDim);
     if (p->path < KYRO_ATTN_AUTO || p->path > KYRO_ATTN_MFMA)
         return fail(KYRO_EINVAL, "paged_attention: path %d unknown", p->path);
     if (p->kv_reuse < KYRO_KV_REUSE_AUTO || p->kv_reuse > KYRO_KV_REUSE_STREAM)
@@ -642,6 +643,70 @@ int kyro_paged_attention_workspace(kyro_ctx ctx, const kyro_paged_attention_para
         if (int rc = attention_setup(p, has_q_start_loc != 0, ctx ? ctx->num_cus : kDefaultCUs, s)) return rc;
         *bytes = s.ws_bytes;
         return KYRO_OK;
+    });
+}
+
+namespace {
+// Writes `text` to buf (at most len bytes with its terminator) and the full length to *needed.
+int put_text(const std::string& text, char* buf, size_t len, size_t* needed) {
+    if (needed) *needed = text.size() + 1;
+    if (buf && len > 0) {
+        const size_t n = std::min(len - 1, text.size());
+        std::memcpy(buf, text.data(), n);
+        buf[n] = '\0';
+    }
+    return KYRO_OK;
+}
+}  // namespace
+
+int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_params* p, int has_q_start_loc,
+                                  char* buf, size_t len, size_t* needed) {
+    return guarded([&]() -> int {
+        AttnSetup s;
+        if (int rc = attention_setup(p, has_q_start_loc != 0, ctx ? ctx->num_cus : kDefaultCUs, s)) return rc;
+        if (s.empty) return put_text("nothing to launch (no sequences or no query rows)", buf, len, needed);
+        const kyro::AttnArgs& a = s.a;
+        char t[512];
+        if (s.kernel == kyro::ATTN_KERNEL_MFMA) {
+            const int rpg = kyro::mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0);
+            const char* pol = a.stream_kv == kyro::kKvPerUnit ? "per-unit" : a.stream_kv ? "stream" : "cached";
+            std::snprintf(t, sizeof t,
+                          "%s<row tiles %d, kv heads per workgroup %d, K/V loads %s> schedule %s, "
+                          "row groups %d, %s %d, workgroups %d%s",
+                          a.dtype_bf16 ? "attn_mfma_kernel" : "attn_mfma_f32_kernel", rpg / 16, a.hpw, pol,
+                          a.plan ? "balanced" : "grid", a.row_groups, a.plan ? "max chunk blocks" : "splits",
+                          a.plan ? a.plan_max_chunk : a.splits,
+                          a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups,
+                          a.plan ? " + attn_combine_plan_kernel" : a.splits > 1 ? " + attn_combine_kernel" : "");
+        } else {
+            std::snprintf(t, sizeof t,
+                          "attn_vector_kernel<%s, head_dim %d> schedule grid, row groups %d, splits %d, "
+                          "workgroups %d%s",
+                          a.dtype_bf16 ? "bf16" : "f32", a.D, a.row_groups, a.splits,
+                          a.ugroups_padded * a.splits * a.row_groups, a.splits > 1 ? " + attn_combine_kernel" : "");
+        }
+        return put_text(t, buf, len, needed);
+    });
+}
+
+int kyro_spec_verify_describe(const kyro_spec_verify_params* p, char* buf, size_t len, size_t* needed) {
+    return guarded([&]() -> int {
+        SpecSetup s;
+        if (int rc = spec_setup(p, s)) return rc;
+        if (s.empty) return put_text("nothing to launch (no sequences)", buf, len, needed);
+        const kyro::SpecArgs& a = s.a;
+        char t[512];
+        const bool tail = a.kmax >= a.win;
+        const std::string first = tail ? "window of " + std::to_string(a.win) + " of " + std::to_string(a.kmax) +
+                                             " draft positions"
+                                       : "every row in the first pass";
+        const std::string tail_k =
+            tail ? ", spec_stats_tail_kernel on " + std::to_string(a.tail_wgs) + " workgroups" : "";
+        std::snprintf(t, sizeof t,
+                      "%s; chunks of %d entries, %d per row; spec_stats_kernel, spec_decide_kernel%s, "
+                      "spec_resample_kernel, spec_pick_kernel",
+                      first.c_str(), a.chunk, a.C, tail_k.c_str());
+        return put_text(t, buf, len, needed);
     });
 }
 

@@ -103,3 +103,10 @@ def verify_drafts(target_logits, draft_logits, draft_tokens, num_draft, temperat
                               allocation_free=allocation_free)
     _lib.context(target_logits.device.index or 0).sync()
     return res
+
+
+def describe_verify(batch: int, max_draft: int, vocab: int, window: int = 0) -> str:
+    """What a verify call with these shapes launches (window, chunking, kernels), from the
+    library's own choice (``kyro_spec_verify_describe``). Host only."""
+    params = _lib.SpecVerifyParams(int(batch), int(max_draft), int(vocab), _lib.KYRO_F32, int(window))
+    return _lib.describe_text(_lib.lib().kyro_spec_verify_describe, ctypes.byref(params))

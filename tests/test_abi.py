@@ -96,3 +96,19 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(ImportError):
         _lib.lib()
+
+
+@pytest.mark.parametrize("D, ok", [(8, True), (72, True), (80, True), (96, True), (256, True), (100, False),
+                                   (4, False), (264, False)])
+def test_head_dim_range(D, ok):
+    """The attention entry points take every head dim that is a multiple of 8 up to 256 (the
+    reference derives it from the model config, src/model/llama.rs:35) and name the range
+    otherwise. Host-only: the workspace query validates the same params as the launch."""
+    params = _lib.PagedAttentionParams(16, 8, D, 2, 2, 2, 4, 8, _lib.KYRO_BF16, _lib.KYRO_F32, 1, 0.0, 0, 0, 1)
+    nbytes = ctypes.c_size_t()
+    rc = _lib.lib().kyro_paged_attention_workspace(None, ctypes.byref(params), 0, ctypes.byref(nbytes))
+    if ok:
+        assert rc == _lib.KYRO_OK, _lib.last_error()
+    else:
+        assert rc == _lib.KYRO_EUNSUPPORTED
+        assert "multiples of 8 up to 256" in _lib.last_error()

@@ -90,6 +90,31 @@ def test_small_parity(gpu, dtype, shape, path, splits):
                              h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
 
 
+# Head dims of the reference's models (head_dim = hidden_size / num_attention_heads,
+# src/model/llama.rs:35, src/model/qwen.rs:31): every multiple of 8 up to 256 runs, including
+# ones that are not multiples of 16 (8 lanes per token row instead of 16).
+HEAD_DIMS = [8, 64, 72, 80, 96, 112, 128, 160, 192, 248, 256]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("D", HEAD_DIMS)
+@pytest.mark.parametrize("heads", [(8, 2), (4, 4)], ids=["gqa8x2", "mha4"])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_head_dims(gpu, dtype, D, heads, splits):
+    H, Hkv = heads
+    case = wl.make_attention_case(context_lens=[70, 5, 33, 130], q_lens=[5, 1, 3, 8], num_heads=H,
+                                  num_kv_heads=Hkv, head_dim=D, dtype=dtype, seed=40 + D, num_blocks=64)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(16, H, D, Hkv)
+    exp = h.oracle_attention(case)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                           t["context_lens"], q_start_loc=t["q_start_loc"], num_splits=splits,
+                           out_dtype=out_dtype)
+        atol = h.ATOL_BF16 if dtype == "bf16" or out_dtype == torch.bfloat16 else h.ATOL_F32
+        h.assert_attention_close(out, case, exp, atol)
+
+
 def test_bf16_output_and_noncausal(gpu):
     case = wl.make_attention_case(context_lens=[90, 31], q_lens=[4, 2], num_heads=16, num_kv_heads=4,
                                   dtype="bf16", seed=8)
@@ -467,6 +492,14 @@ def test_full_gqa_llama3_8b_properties(gpu):
     out2 = attn.forward(t["query"], k2, v2, perm[t["block_table"]], t["context_lens"],
                         q_start_loc=t["q_start_loc"])
     assert torch.equal(out, out2)
+    # The benchmark's exact call: bf16 output, max_q_len 8, AUTO path, schedule and kv_reuse,
+    # into a preallocated output (forward_async, then the synchronising check).
+    outb = torch.empty(out.shape, dtype=torch.bfloat16, device=gpu)
+    attn.forward_async(*args, q_start_loc=t["q_start_loc"], max_q_len=8, out_dtype=torch.bfloat16, out=outb)
+    kyro_amd.sync(0)
+    h.assert_attention_close(outb, case, exp, h.ATOL_BF16)
+    # bf16 rounding of the f32 result, nothing more
+    assert torch.equal(outb, out.to(torch.bfloat16))
 
 
 def test_full_skewed_prefix(gpu):
