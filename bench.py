@@ -514,6 +514,44 @@ def measure_config(name, warmup, steps, detailed=False, scratch=None):
     return line
 
 
+def head_dims_workload(warmup, steps):
+    """One JSON line: the attention at head dims 64, 80, 96, 128 and 256 on the Llama-3-8B verify
+    shape (GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV), AUTO (the MFMA kernel at 64,
+    96, 128 and 256, the vector kernel at 80) and the vector kernel, each on its algorithmic
+    bytes."""
+    import torch
+
+    import kyro_amd
+    from kyro_amd import workloads as wl
+    from kyro_amd.attention import describe_attention
+
+    dev = torch.device("cuda", 0)
+    res = {"workload": "head-dims", "shape": "GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV and out"}
+    for D in (64, 80, 96, 128, 256):
+        case = wl.make_attention_case(context_lens=[4096] * 64, q_lens=[8] * 64, num_heads=32, num_kv_heads=8,
+                                      head_dim=D, dtype="bf16", seed=D)
+        up = lambda x: torch.from_numpy(x).view(torch.bfloat16).to(dev)  # noqa: E731
+        t = dict(q=up(case.query), kc=up(case.key_cache), vc=up(case.value_cache),
+                 table=torch.from_numpy(case.block_table).to(dev), ctx=torch.from_numpy(case.context_lens).to(dev),
+                 qs=torch.from_numpy(case.q_start_loc).to(dev))
+        attn = kyro_amd.PagedAttention(16, 32, D, 8)
+        out = torch.empty(t["q"].shape, dtype=torch.bfloat16, device=dev)
+        nbytes = case.kv_bytes() + case.q_out_bytes(2)
+        entry = {"algorithmic_bytes": nbytes}
+        for path in ("auto", "vector"):
+            us = _median_us(lambda: attn.forward_async(
+                t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"], max_q_len=8,
+                out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
+            entry[path] = {"us": us, "GB_s": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / PEAK_HBM_GBS,
+                           "launch": describe_attention(attn, batch=64, total_q=512, max_q_len=8,
+                                                        max_blocks_per_seq=256, num_blocks=case.key_cache.shape[0],
+                                                        path=path, device=0)}
+        res[f"d{D}"] = entry
+        del t, out
+        torch.cuda.empty_cache()
+    print(json.dumps(res), flush=True)
+
+
 def other_workload(name, warmup, steps):
     """One JSON line for a non-default workload (measure_config with the vector and MFMA paths,
     the "shared" hint and the CPU oracle)."""
@@ -541,13 +579,13 @@ def main():
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
                              "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "ngram-draft",
-                             "others"],
+                             "head-dims", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
         names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables",
-                  "decode-sample", "ngram-draft"] if args.workload == "others" else [args.workload])
+                  "decode-sample", "ngram-draft", "head-dims"] if args.workload == "others" else [args.workload])
         for n in names:
             if n == "kv-append":
                 kv_append_workload(args.warmup, args.steps)
@@ -557,6 +595,8 @@ def main():
                 decode_sample_workload(args.warmup, args.steps)
             elif n == "ngram-draft":
                 ngram_draft_workload(args.warmup, args.steps)
+            elif n == "head-dims":
+                head_dims_workload(args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
         return

@@ -144,12 +144,22 @@ constexpr int kVectorRowsPerGroup = 8;
 // (kMfmaManyRows: one kv head per workgroup, Q read from LDS, only the unit's tiles computed),
 // so that a unit of up to 64 rows streams its K/V once instead of once per 32-row group. (Five
 // tiles need more than the 512 registers a wave can hold.)
+// Head dims other than 128 take at most two tiles (one at 256: its K/V pairs and accumulators
+// fill the register file).
 constexpr int kMfmaManyRows = 64;
-__host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16) {
-    return rows <= 16 ? 16 : (rows <= 32 || !bf16) ? 32 : kMfmaManyRows;
+__host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16, int D) {
+    if (D > 128) return 16;
+    return rows <= 16 ? 16 : (rows <= 32 || !bf16 || D != 128) ? 32 : kMfmaManyRows;
+}
+
+// Head dims the bf16 MFMA kernel is built for (block size 16); f32 caches take it at 128 only.
+__host__ __device__ inline bool mfma_head_dim(int D, bool bf16) {
+    return D == 128 || (bf16 && (D == 64 || D == 96 || D == 256));
 }
 
 hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
+// The bf16 MFMA kernel at head dims 64, 96 and 256 (its own translation unit).
+hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream);
 
 // Per-sequence decision taken after the acceptance scan.
 struct SpecPlan {

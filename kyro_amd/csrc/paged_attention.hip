@@ -245,18 +245,20 @@ __global__ __launch_bounds__(kThreads) void attn_combine_kernel(AttnArgs a) {
                  nsplit);
 }
 
-// Balanced schedule (head_dim 128): the plan lists the combine work, one unit per (kv head,
-// kCombineRows rows) of each split sequence, with per-sequence prefix counts in plan_cw. A grid
-// of any size walks the list; with nothing split every workgroup reads one word and returns.
-constexpr int kCombineRows = kThreads / (128 / 4);
+// Balanced schedule: the plan lists the combine work, one unit per (kv head, kCombineRows rows)
+// of each split sequence, with per-sequence prefix counts in plan_cw. A grid of any size walks
+// the list; with nothing split every workgroup reads one word and returns. A row takes 32
+// threads, each merging the 4-column groups c, c + 32, .. of the row's D / 4.
+constexpr int kCombineRows = kThreads / 32;
+template <int D>
 __global__ __launch_bounds__(kThreads) void attn_combine_plan_kernel(AttnArgs a) {
-    constexpr int D = 128, Q = D / 4;
+    constexpr int Q = D / 4;
     __shared__ int cw[kPlanMaxSeqs + 1];
     const int total = a.plan_cw[a.B];
     if ((int)blockIdx.x >= total) return;
     for (int i = threadIdx.x; i <= a.B; i += kThreads) cw[i] = a.plan_cw[i];
     __syncthreads();
-    const int d = ((int)threadIdx.x % Q) * 4;
+    const int col = (int)threadIdx.x % 32;
     const int upseq = a.ugroups / a.B;
     for (int w = blockIdx.x; w < total; w += gridDim.x) {
         // The last sequence whose work starts at or before w (it has work: see plan_build).
@@ -275,30 +277,35 @@ __global__ __launch_bounds__(kThreads) void attn_combine_plan_kernel(AttnArgs a)
         const int chunks = (si.rows + kCombineRows - 1) / kCombineRows;
         const int local = w - cw[lo];
         si.kvh = local / chunks;
-        const int n = (local - si.kvh * chunks) * kCombineRows + (int)threadIdx.x / Q;
+        const int n = (local - si.kvh * chunks) * kCombineRows + (int)threadIdx.x / 32;
         if (n >= si.rows) continue;
         const int nrg = ps.y, first = ps.z;
         const int rg = n / a.plan_rw;
         const size_t slot = (size_t)first + (size_t)(si.kvh / a.hpw) * nrg + rg;
-        merge_row<D>(a, si, n, d, (slot * a.hpw + si.kvh % a.hpw) * a.plan_rw + (n - rg * a.plan_rw),
-                     (size_t)upseq * nrg * a.hpw * a.plan_rw, ps.x);
+        for (int c = col; c < Q; c += 32)
+            merge_row<D>(a, si, n, 4 * c, (slot * a.hpw + si.kvh % a.hpw) * a.plan_rw + (n - rg * a.plan_rw),
+                         (size_t)upseq * nrg * a.hpw * a.plan_rw, ps.x);
     }
 }
 
 // ------------------------------------------------------------------------------ MFMA kernel
 
-constexpr int kMfmaD = 128;
+constexpr int kMfmaD = 128;  // the head dim of the f32 MFMA kernel and of the LDS-staged K forms
 constexpr int kMfmaBS = 16;
 // One (block, kv head) slab of zeros, read in place of a missing block (static device memory is
 // zero-initialised when the code object loads, and nothing writes it).
-__device__ uint16_t kZeroSlab[kMfmaBS * kMfmaD];
+__device__ uint16_t kZeroSlab[kMfmaBS * kMaxHeadDim];
 
 // K and V of one pair of 16-token blocks, in MFMA operand layout (K: loaded so under kKDirect,
 // read from the wave's LDS tile just before the products under kKDma) or ready for the
-// in-register transpose (V). 64 VGPRs (32 live across a prefetch under kKDma).
+// in-register transpose (V). With T = D / 16 head dims per lane for V: D / 2 VGPRs (64 at
+// D = 128; 32 live across a prefetch under kKDma).
+template <int D>
 struct KVPair {
-    bf16x8 k[2][4];  // [block][head-dim step]: token r, head dims 32 s + 8 g .. + 7
-    uint4 v[2][4];   // [block][e]: token 4 g + e, head dims 8 r .. 8 r + 7
+    static constexpr int kSteps = D / 32;  // head-dim steps of the S^T product
+    static constexpr int kVW = D / 32;     // V words per lane and token (T bf16)
+    bf16x8 k[2][kSteps];    // [block][head-dim step]: token r, head dims 32 s + 8 g .. + 7
+    uint32_t v[2][4][kVW];  // [block][e]: token 4 g + e, head dims T r .. T r + T - 1
 };
 
 // How K reaches the MFMA A-operand layout:
@@ -332,13 +339,15 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
 // addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
 // a prefetched pair in flight. POL is the loads' cache policy (kLoadCached or kLoadStream).
-template <int POL, int KM>
-__device__ __forceinline__ void load_pair(KVPair& p, uint4* __restrict__ kt, const uint16_t* __restrict__ kp,
+template <int POL, int KM, int D>
+__device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t block_stride, size_t kv_off, int r, int g) {
-    constexpr int kSlabBytes = kMfmaBS * kMfmaD * 2;
-    const int koff = (r * kMfmaD + 8 * g) * 2;        // bytes; + 64 s for head-dim slot s
-    const int voff = (4 * g * kMfmaD + 8 * r) * 2;    // bytes; + 256 e for token 4 g + e
+    static_assert(KM != kKDma || D == kMfmaD, "the LDS-staged K tiles hold 256-byte token rows");
+    constexpr int kSlabBytes = kMfmaBS * D * 2;
+    constexpr int T = D / 16;
+    const int koff = (r * D + 8 * g) * 2;        // bytes; + 64 s for head-dim slot s
+    const int voff = (4 * g * D + T * r) * 2;    // bytes; + 2 D e for token 4 g + e
     __amdgpu_buffer_rsrc_t kr[2], vr[2];
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
@@ -365,15 +374,41 @@ __device__ __forceinline__ void load_pair(KVPair& p, uint4* __restrict__ kt, con
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int s = 0; s < KVPair<D>::kSteps; ++s)
                 p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], koff, 64 * s, POL));
         }
     }
+    // V: T consecutive bf16 of one token row per lane (16 bytes at D = 128, 8 at 64, 12 at 96,
+    // 32 at 256), in the widest loads that many bytes allow.
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            p.v[bi][e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 256 * e, POL));
+        for (int e = 0; e < 4; ++e) {
+            uint32_t* w = p.v[bi][e];
+            if constexpr (KVPair<D>::kVW % 4 == 0) {
+#pragma unroll
+                for (int q = 0; q < KVPair<D>::kVW; q += 4) {
+                    const auto x = __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 2 * D * e + 4 * q, POL);
+                    w[q] = x[0];
+                    w[q + 1] = x[1];
+                    w[q + 2] = x[2];
+                    w[q + 3] = x[3];
+                }
+            } else if constexpr (KVPair<D>::kVW == 3) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr[bi], voff, 2 * D * e, POL);
+                w[0] = x[0];
+                w[1] = x[1];
+                w[2] = x[2];
+            } else if constexpr (KVPair<D>::kVW == 2) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b64(vr[bi], voff, 2 * D * e, POL);
+                w[0] = x[0];
+                w[1] = x[1];
+            } else {
+#pragma unroll
+                for (int q = 0; q < KVPair<D>::kVW; ++q)
+                    w[q] = __builtin_amdgcn_raw_buffer_load_b32(vr[bi], voff, 2 * D * e + 4 * q, POL);
+            }
+        }
 }
 
 // One wave's LDS tile for the K of one block pair: [block][token][16-byte chunk], the chunk
@@ -386,7 +421,7 @@ constexpr int kQStride = kMfmaD / 8 + 1;
 
 // K of a pair in MFMA A-operand layout (register s: token r, chunk 4 s + g) from a swizzled tile
 // (token t's chunk c at slot c ^ t). The tile belongs to the calling wave alone.
-__device__ __forceinline__ void read_k_tile(KVPair& p, const uint4* __restrict__ tile, int r, int g) {
+__device__ __forceinline__ void read_k_tile(KVPair<kMfmaD>& p, const uint4* __restrict__ tile, int r, int g) {
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
@@ -754,17 +789,19 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 // mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
 // head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
 // workspace rows pb0 + h * pbstep + n for head h of the group.
-template <int NTW, int HP, int POL, int KM>
-__device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMfmaD> (&frame)[HP], int* s_blk,
+template <int NTW, int HP, int POL, int KM, int D>
+__device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> (&frame)[HP], int* s_blk,
                                           uint4* kstA, uint4* kstB, uint4* sq, const SeqInfo& si, int ug, int rg,
                                           int blk_begin, int blk_end, int nsplit, size_t pb0, size_t pbstep) {
-    constexpr int D = kMfmaD;
+    static_assert(D % 32 == 0 && D <= kMaxHeadDim, "the bf16 MFMA kernel takes head dims that are multiples of 32");
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
+    constexpr int KS = D / 32;        // head-dim steps of S^T = K Q^T
+    constexpr int T = D / 16;         // d-tiles of O^T (lane row r <-> head dims T r + dt)
     constexpr int WPH = kWaves / HP;  // waves per kv head
     // More than two tiles: Q is read from LDS per tile (sq, staged once per item) and only the
     // tiles that hold rows of this unit are computed.
     constexpr bool QL = NTW > 2;
-    static_assert(!QL || (HP == 1 && KM == kKDma), "the many-tile form needs one kv head and K in LDS");
+    static_assert(!QL || (HP == 1 && KM == kKDma && D == kMfmaD), "the many-tile form needs one kv head and K in LDS");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int hw = wave / WPH;  // this wave's kv head within the group
     const int wp = wave % WPH;  // and its place among that head's waves
@@ -800,7 +837,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
     {
         // Q^T operands: lane holds row n = row0 + 16 nt + r, head-dim slots 32 s + 8 g .. + 7.
         // Padding rows (n >= rows) get Q = 0 and full visibility; they are never stored.
-        bf16x8 qB[QL ? 1 : NTW][4];
+        bf16x8 qB[QL ? 1 : NTW][KS];
         int vis[NTW];
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
@@ -810,27 +847,27 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 if constexpr (!QL) {
                     const size_t qrow = out_row(a, si, n);
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                    for (int s = 0; s < KS; ++s)
                         qB[nt][s] = __builtin_bit_cast(bf16x8, load16(qp + qrow * D + 32 * s + 8 * g));
                 }
                 vis[nt] = a.causal ? si.ctx - si.q_len + j + 1 : si.ctx;
             } else {
                 if constexpr (!QL) {
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+                    for (int s = 0; s < KS; ++s) qB[nt][s] = __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
                 }
                 vis[nt] = si.ctx;
             }
         }
 
         float m[NTW], lsum[NTW];  // running max (log2 units, scaled) and this lane's partial sum
-        f32x4 O[8][NTW];
+        f32x4 O[T][NTW];
 #pragma unroll
         for (int nt = 0; nt < NTW; ++nt) {
             m[nt] = kNegInf;
             lsum[nt] = 0.f;
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int dt = 0; dt < T; ++dt) O[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
         // Online softmax of row tile nt over one pair (S^T fragments s0, s1 of its two blocks):
@@ -871,7 +908,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             lsum[nt] = lsum[nt] * alpha + ps;
             if (__any(m_new > m[nt] && m[nt] != kNegInf)) {
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) O[dt][nt] *= alpha;
+                for (int dt = 0; dt < T; ++dt) O[dt][nt] *= alpha;
             }
             m[nt] = m_new;
             uint4 pw;
@@ -881,16 +918,16 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
             pw.w = pack_bf16x2(sv[6], sv[7]);
             return __builtin_bit_cast(bf16x8, pw);
         };
-        // V^T operand of d-tile dt: lane row r <-> head dim 8 r + dt, k-slots 8 g .. 8 g + 7 <->
+        // V^T operand of d-tile dt: lane row r <-> head dim T r + dt, k-slots 8 g .. 8 g + 7 <->
         // tokens 4 g .. 4 g + 3 of block 0 then of block 1.
-        auto v_operand = [&](const KVPair& kv, int dt) -> bf16x8 {
+        auto v_operand = [&](const KVPair<D>& kv, int dt) -> bf16x8 {
             const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
             const int w = dt >> 1;
             uint4 av;
-            av.x = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][1])[w], ((const uint32_t*)&kv.v[0][0])[w], sel);
-            av.y = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[0][3])[w], ((const uint32_t*)&kv.v[0][2])[w], sel);
-            av.z = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][1])[w], ((const uint32_t*)&kv.v[1][0])[w], sel);
-            av.w = __builtin_amdgcn_perm(((const uint32_t*)&kv.v[1][3])[w], ((const uint32_t*)&kv.v[1][2])[w], sel);
+            av.x = __builtin_amdgcn_perm(kv.v[0][1][w], kv.v[0][0][w], sel);
+            av.y = __builtin_amdgcn_perm(kv.v[0][3][w], kv.v[0][2][w], sel);
+            av.z = __builtin_amdgcn_perm(kv.v[1][1][w], kv.v[1][0][w], sel);
+            av.w = __builtin_amdgcn_perm(kv.v[1][3][w], kv.v[1][2][w], sel);
             return __builtin_bit_cast(bf16x8, av);
         };
 
@@ -898,7 +935,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
         // The wave's K tiles under kKDma, one per register buffer.
         uint4* const ktA = KM == kKDma ? kstA + wave * kKStageChunks : kstA;
         uint4* const ktB = KM == kKDma ? kstB + wave * kKStageChunks : kstB;
-        auto compute = [&](KVPair& kv, const uint4* kt, int pb, int blk0, int blk1) {
+        auto compute = [&](KVPair<D>& kv, const uint4* kt, int pb, int blk0, int blk1) {
             if constexpr (KM == kKDma) {
                 // Keep the next pair's loads (issued just before) ahead of this pair's tile
                 // reads, which then wait for this pair's K only; without the barrier the
@@ -913,7 +950,9 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx) kv.v[bi][e] = make_uint4(0, 0, 0, 0);
+                            if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx)
+#pragma unroll
+                                for (int q = 0; q < KVPair<D>::kVW; ++q) kv.v[bi][e][q] = 0u;
                 }
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
@@ -927,7 +966,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                         for (int bi = 0; bi < 2; ++bi) {
                             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                            for (int s = 0; s < 4; ++s)
+                            for (int s = 0; s < KS; ++s)
                                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv.k[bi][s], q[s], acc, 0, 0, 0);
                             S2[bi] = acc;
                         }
@@ -935,7 +974,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                         // The V^T operands are rebuilt per tile (32 v_perm): holding all eight
                         // across the tiles costs 32 registers the accumulators need.
 #pragma unroll
-                        for (int dt = 0; dt < 8; ++dt)
+                        for (int dt = 0; dt < T; ++dt)
                             O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand(kv, dt), pB, O[dt][nt], 0, 0, 0);
                     }
                 }
@@ -949,7 +988,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 for (int nt = 0; nt < NTW; ++nt) {
                     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int s = 0; s < 4; ++s)
+                    for (int s = 0; s < KS; ++s)
                         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv.k[bi][s], qB[nt][s], acc, 0, 0, 0);
                     S[bi][nt] = acc;
                 }
@@ -960,7 +999,9 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx) kv.v[bi][e] = make_uint4(0, 0, 0, 0);
+                        if ((pb + bi) * kMfmaBS + 4 * g + e >= si.ctx)
+#pragma unroll
+                            for (int q = 0; q < KVPair<D>::kVW; ++q) kv.v[bi][e][q] = 0u;
             }
             bf16x8 pB[NTW];
 #pragma unroll
@@ -968,7 +1009,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
 
             // O^T += V^T P^T.
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
+            for (int dt = 0; dt < T; ++dt) {
                 const bf16x8 A = v_operand(kv, dt);
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt)
@@ -1012,7 +1053,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 b0 = j + 1 < npairs ? b0 : -1;
                 b1 = j + 1 < npairs ? b1 : -1;
             };
-            KVPair bufA, bufB;
+            KVPair<D> bufA, bufB;
             // The next pair's loads are issued unconditionally: past the last pair they read
             // the zero slab (and are dropped), so no branch separates a prefetch from the wait
             // that precedes the computation of the pair before it. P is the loads' cache policy.
@@ -1020,14 +1061,14 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
                 constexpr int P = decltype(pol)::value;
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<P, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<P, KM>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    load_pair<P, KM, D>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
                     compute(bufA, ktA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<P, KM>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
                     compute(bufB, ktB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
@@ -1059,7 +1100,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
 
         // Merge each kv head's waves in its frame: common max, then the rescaled accumulators
         // are added into LDS in a fixed order (the head's first wave stores), so the result is
-        // bitwise reproducible. Lane (r, g) owns head dims 32 g + 8 e + dt of row 16 nt + r.
+        // bitwise reproducible. Lane (r, g) owns head dims T (4 g + e) + dt of row 16 nt + r.
         Frame<RW, D>& fr = frame[hw];
         if (g == 0) {
 #pragma unroll
@@ -1084,13 +1125,13 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, kMf
 #pragma unroll
                 for (int nt = 0; nt < NTW; ++nt) {
                     if (QL && nt >= ntile) continue;  // rows past the unit: never stored
-                    float* dst = &fr.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 32 * g];
+                    float* dst = &fr.acc[(nt * 16 + r) * Frame<RW, D>::kStride + 4 * T * g];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
 #pragma unroll
-                        for (int dt = 0; dt < 8; ++dt) {
+                        for (int dt = 0; dt < T; ++dt) {
                             const float v = O[dt][nt][e] * f[nt];
-                            dst[8 * e + dt] = (w == 0) ? v : dst[8 * e + dt] + v;
+                            dst[T * e + dt] = (w == 0) ? v : dst[T * e + dt] + v;
                         }
                 }
             }
@@ -1459,21 +1500,23 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
 
 // The LDS merge frames of a workgroup's heads; the many-tile kernel keeps its one frame in its
 // first K-tile array instead.
-template <int NTW, int HP, bool QL>
+template <int NTW, int HP, bool QL, int D>
 struct FrameLds {
-    Frame<NTW * 16, kMfmaD> f[HP];
+    Frame<NTW * 16, D> f[HP];
 };
-template <int NTW, int HP>
-struct FrameLds<NTW, HP, true> {};
+template <int NTW, int HP, int D>
+struct FrameLds<NTW, HP, true, D> {};
 
-// bf16 caches.
-template <int NTW, int HP, int POL, bool PLAN>
+// bf16 caches. Head dims other than 128 load K straight into operand layout and take at most
+// two row tiles per wave (the LDS-staged K tiles and the many-tile form are built for 256-byte
+// token rows).
+template <int NTW, int HP, int POL, bool PLAN, int D = kMfmaD>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
-    using Fr = Frame<NTW * 16, kMfmaD>;
+    using Fr = Frame<NTW * 16, D>;
     constexpr bool QL = NTW > 2;
-    __shared__ FrameLds<NTW, HP, QL> s_fr;
+    __shared__ FrameLds<NTW, HP, QL, D> s_fr;
     __shared__ int s_blk[kMaxChunkBlocks];
-    constexpr int KM = kKModeFor<NTW, PLAN>;
+    constexpr int KM = D == kMfmaD ? kKModeFor<NTW, PLAN> : kKDirect;
     // Two separate arrays, so that the compiler's wait for one tile's loads does not also wait
     // for the other's (it tells LDS DMA destinations apart by the object written). The
     // many-tile kernel keeps its merge frame in the first (the frame is used only after the
@@ -1489,7 +1532,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     Fr (&frame)[HP] = *reinterpret_cast<Fr(*)[HP]>(fp);
     mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
                                         size_t pbs) {
-        mfma_item<NTW, HP, POL, KM>(a, frame, s_blk, s_kstA, s_kstB, s_q, si, ug, rg, bb, be, ns, pb0, pbs);
+        mfma_item<NTW, HP, POL, KM, D>(a, frame, s_blk, s_kstA, s_kstB, s_q, si, ug, rg, bb, be, ns, pb0, pbs);
     });
 }
 
@@ -1731,16 +1774,78 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------------ launcher
+
+#ifdef KYRO_ATTN_HD_UNIT
+// The bf16 MFMA kernel at head dims other than 128 (64, 96, 256), in a translation unit of its
+// own so that its instances compile in parallel with the rest: at most two row tiles per wave
+// (one at 256, whose K/V pairs and accumulators fill the register file), one or two kv heads per
+// workgroup, streaming or cached K/V loads, grid or balanced schedule.
+template <int D>
+hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream) {
+    const dim3 block(kThreads);
+    const int rpg = mfma_rows_per_group(a.rows_cap, true, D);
+#define KYRO_HD_LAUNCH(NT, POL, PLAN)                                                       \
+    {                                                                                       \
+        if (a.hpw == 2) attn_mfma_kernel<NT, 2, POL, PLAN, D><<<grid, block, 0, stream>>>(a); \
+        else attn_mfma_kernel<NT, 1, POL, PLAN, D><<<grid, block, 0, stream>>>(a);          \
+    }
+#define KYRO_HD_POL(NT, PLAN)                                                               \
+    {                                                                                       \
+        if (a.stream_kv) KYRO_HD_LAUNCH(NT, kLoadStream, PLAN)                              \
+        else KYRO_HD_LAUNCH(NT, kLoadCached, PLAN)                                          \
+    }
+    if constexpr (D > kMfmaD) {  // one row tile
+        if (a.plan) KYRO_HD_POL(1, true)
+        else KYRO_HD_POL(1, false)
+    } else {
+        if (rpg == 16) {
+            if (a.plan) KYRO_HD_POL(1, true)
+            else KYRO_HD_POL(1, false)
+        } else {
+            if (a.plan) KYRO_HD_POL(2, true)
+            else KYRO_HD_POL(2, false)
+        }
+    }
+#undef KYRO_HD_POL
+#undef KYRO_HD_LAUNCH
+    if (a.plan) {
+        constexpr long long kCombineMaxGrid = 2048;
+        const long long units = (long long)a.units * ((a.rows_cap + kCombineRows - 1) / kCombineRows);
+        attn_combine_plan_kernel<D><<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0,
+                                       stream>>>(a);
+    } else if (a.splits > 1) {
+        const int rpw = kThreads / (D / 4);
+        const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
+        attn_combine_kernel<D><<<cgrid, block, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
-// ------------------------------------------------------------------------------ launcher
+hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
+    if (grid.x == 0) return hipSuccess;
+    switch (a.D) {
+        case 64: return launch_mfma_hd<64>(a, grid, stream);
+        case 96: return launch_mfma_hd<96>(a, grid, stream);
+        case 256: return launch_mfma_hd<256>(a, grid, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+#else  // KYRO_ATTN_HD_UNIT
+
+}  // namespace
 
 hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t stream) {
     const dim3 block(kThreads);
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
+    if (path == ATTN_KERNEL_MFMA && a.D != kMfmaD) return launch_paged_attention_mfma_hd(a, stream);
     if (path == ATTN_KERNEL_MFMA) {
-        const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0);
+        const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
         const bool rows16 = rpg == 16;
 #define KYRO_MFMA_LAUNCH2(K, POL, PLAN)                                                     \
         if (a.hpw == 2) {                                                                   \
@@ -1794,7 +1899,7 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
         // (each then walks several units).
         constexpr long long kCombineMaxGrid = 2048;
         const long long units = (long long)a.units * ((a.rows_cap + kCombineRows - 1) / kCombineRows);
-        attn_combine_plan_kernel<<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0, stream>>>(a);
+        attn_combine_plan_kernel<kMfmaD><<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0, stream>>>(a);
     } else if (a.splits > 1) {
         const int rpw = kThreads / (a.D / 4);
         const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
@@ -1811,5 +1916,7 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     }
     return hipGetLastError();
 }
+
+#endif  // KYRO_ATTN_HD_UNIT
 
 }  // namespace kyro

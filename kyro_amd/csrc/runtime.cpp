@@ -202,11 +202,12 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (max_q_len <= 0) max_q_len = have_q_start ? p->total_q : 1;
     if (!have_q_start) max_q_len = 1;
 
-    const bool mfma_ok = p->head_dim == 128 && p->block_size == 16;  // bf16 or f32 caches
+    const bool mfma_ok = p->block_size == 16 && kyro::mfma_head_dim(p->head_dim, p->dtype == KYRO_BF16);
     int kernel;
     if (p->path == KYRO_ATTN_MFMA) {
         if (!mfma_ok)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs head_dim 128, block_size 16");
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs block_size 16 and head_dim 128 "
+                        "(bf16 caches: 64, 96, 128 or 256)");
         kernel = kyro::ATTN_KERNEL_MFMA;
     } else if (p->path == KYRO_ATTN_VECTOR) {
         kernel = kyro::ATTN_KERNEL_VECTOR;
@@ -218,7 +219,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     }
     if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
         return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
-                    "(head_dim 128, block_size 16)");
+                    "(block_size 16; head_dim 128, or 64, 96, 256 with bf16 caches)");
 
     kyro::AttnArgs& a = s.a;
     a.B = p->batch_size;
@@ -241,7 +242,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
     // (vector) or 16 / 32 / 64 (MFMA) rows that stream the same K/V.
     const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA
-                                   ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16)
+                                   ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16, p->head_dim)
                                    : kyro::kVectorRowsPerGroup;
     // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
     // waves per head): the workgroup then reads both heads' slabs of each block together, and
@@ -668,7 +669,7 @@ int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_param
         const kyro::AttnArgs& a = s.a;
         char t[512];
         if (s.kernel == kyro::ATTN_KERNEL_MFMA) {
-            const int rpg = kyro::mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0);
+            const int rpg = kyro::mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
             const char* pol = a.stream_kv == kyro::kKvPerUnit ? "per-unit" : a.stream_kv ? "stream" : "cached";
             std::snprintf(t, sizeof t,
                           "%s<row tiles %d, kv heads per workgroup %d, K/V loads %s> schedule %s, "

@@ -77,8 +77,8 @@ SMALL = [
 @pytest.mark.parametrize("splits", [1, 3])
 def test_small_parity(gpu, dtype, shape, path, splits):
     (H, Hkv), D, ctx, ql = shape
-    if path == "mfma" and D != 128:
-        pytest.skip("the MFMA kernels take head_dim 128 only")
+    if path == "mfma" and D != 128 and not (dtype == "bf16" and D in MFMA_HEAD_DIMS):
+        pytest.skip("the f32 MFMA kernel takes head_dim 128 only")
     case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
                                   head_dim=D, dtype=dtype, seed=21, num_blocks=200)
     t = h.attention_tensors(case, gpu)
@@ -96,23 +96,52 @@ def test_small_parity(gpu, dtype, shape, path, splits):
 HEAD_DIMS = [8, 64, 72, 80, 96, 112, 128, 160, 192, 248, 256]
 
 
+# bf16 head dims the MFMA kernel takes besides 128 (block size 16)
+MFMA_HEAD_DIMS = (64, 96, 256)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("D", HEAD_DIMS)
-@pytest.mark.parametrize("heads", [(8, 2), (4, 4)], ids=["gqa8x2", "mha4"])
+@pytest.mark.parametrize("heads", [(8, 2), (4, 4), (32, 4)], ids=["gqa8x2", "mha4", "gqa32x4"])
 @pytest.mark.parametrize("splits", [1, 3])
 def test_head_dims(gpu, dtype, D, heads, splits):
+    """Every path that takes the head dim, against the oracle: AUTO (the MFMA kernel where it
+    applies), the vector kernel, and for the MFMA head dims the MFMA kernel on the grid and under
+    the balanced schedule. 32/4 heads give 64 rows per kv head (several row groups)."""
     H, Hkv = heads
     case = wl.make_attention_case(context_lens=[70, 5, 33, 130], q_lens=[5, 1, 3, 8], num_heads=H,
                                   num_kv_heads=Hkv, head_dim=D, dtype=dtype, seed=40 + D, num_blocks=64)
     t = h.attention_tensors(case, gpu)
     attn = make_attention(16, H, D, Hkv)
     exp = h.oracle_attention(case)
-    for out_dtype in (torch.float32, torch.bfloat16):
-        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
-                           t["context_lens"], q_start_loc=t["q_start_loc"], num_splits=splits,
-                           out_dtype=out_dtype)
-        atol = h.ATOL_BF16 if dtype == "bf16" or out_dtype == torch.bfloat16 else h.ATOL_F32
-        h.assert_attention_close(out, case, exp, atol)
+    runs = [dict(num_splits=splits), dict(num_splits=splits, path="vector")]
+    if D == 128 or (dtype == "bf16" and D in MFMA_HEAD_DIMS):
+        runs.append(dict(num_splits=splits, path="mfma"))
+        if splits == 1:
+            runs.append(dict(schedule="balanced"))
+    for kw in runs:
+        for out_dtype in (torch.float32, torch.bfloat16):
+            out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"],
+                               t["context_lens"], q_start_loc=t["q_start_loc"], out_dtype=out_dtype, **kw)
+            atol = h.ATOL_BF16 if dtype == "bf16" or out_dtype == torch.bfloat16 else h.ATOL_F32
+            h.assert_attention_close(out, case, exp, atol)
+
+
+@pytest.mark.parametrize("D", MFMA_HEAD_DIMS)
+def test_mfma_head_dims_long_and_uneven(gpu, D):
+    """MFMA head dims on long, uneven contexts (balanced schedule with splits, partial last
+    blocks, causal rows) and on a uniform GQA 32/8 verify shape, against the oracle."""
+    for ctx, ql, heads in (([3000, 17, 900, 5000], [8, 8, 1, 5], (32, 8)), ([1024] * 8, [8] * 8, (32, 8)),
+                           ([2000, 333], [5, 5], (16, 16))):
+        case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=heads[0], num_kv_heads=heads[1],
+                                      head_dim=D, dtype="bf16", seed=D + len(ctx))
+        t = h.attention_tensors(case, gpu)
+        attn = make_attention(16, heads[0], D, heads[1])
+        exp = h.oracle_attention(case)
+        for kw in (dict(), dict(schedule="grid"), dict(schedule="balanced")):
+            out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                               q_start_loc=t["q_start_loc"], out_dtype=torch.bfloat16, **kw)
+            h.assert_attention_close(out, case, exp, h.ATOL_BF16)
 
 
 def test_bf16_output_and_noncausal(gpu):
