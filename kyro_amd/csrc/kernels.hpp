@@ -84,7 +84,10 @@ constexpr int kPlanMinChunk = 16;
 // L x kPlanChunkQuarters / 4 blocks (3L/2: on a batch with one 32k-token prefix among short
 // sequences this beats L/2 by 12%; L/2, 3L/4 and 2L all leave a longer tail, L is within 1%).
 // plan_slot_bound takes the same count.
-constexpr int kPlanChunkQuarters = 6;
+#ifndef KYRO_PLAN_CHUNK_QUARTERS
+#define KYRO_PLAN_CHUNK_QUARTERS 6
+#endif
+constexpr int kPlanChunkQuarters = KYRO_PLAN_CHUNK_QUARTERS;
 
 // Balanced-schedule chunk length in blocks, from the total work T (kv head groups x row groups x
 // blocks, summed over sequences), the longest sequence maxnb (blocks) and the persistent grid:
@@ -333,5 +336,6 @@ constexpr long long kSpecEagerBytes = 64ll << 20;
 #define KYRO_SPEC_TAIL_WGS 512
 #endif
 constexpr int kSpecTailWgs = KYRO_SPEC_TAIL_WGS;
+
 
 }  // namespace kyro

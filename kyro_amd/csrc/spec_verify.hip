@@ -100,18 +100,17 @@ __device__ ArgMax block_argmax(ArgMax x, float* shv, int* shi) {
     return r;
 }
 
-// A chunk [v0, v1) of a row is shared by the workgroup in one of two layouts. Strided (the
-// streaming passes): consecutive threads take consecutive 16-byte vectors (or floats), so every
-// load instruction is coalesced. Contiguous (the draw): thread t owns [v0 + t kPer, + kPer), so
-// index order within a thread is preserved. Positions past v1 load as -inf, which every consumer
-// maps to zero mass; element indices are recomputed from the position, not stored.
+// A chunk [v0, v1) of a row is shared by the workgroup in the strided layout: consecutive
+// threads take consecutive 16-byte vectors (or floats), so every load instruction is coalesced
+// (a layout where each thread owns a contiguous run issues four times the memory requests and
+// measured slower in the draw). Positions past v1 load as -inf, which every consumer maps to zero
+// mass; element indices are recomputed from the position, not stored.
 template <bool VEC>
 __device__ __forceinline__ int strided_index(int v0, int i) {
     if constexpr (VEC) return v0 + ((i >> 2) * kT + (int)threadIdx.x) * 4 + (i & 3);
     else return v0 + i * kT + (int)threadIdx.x;
 }
 
-__device__ __forceinline__ int contig_index(int v0, int i) { return v0 + (int)threadIdx.x * kPer + i; }
 
 // Every load is issued unconditionally: a position past v1 reads the chunk's last vector (or
 // float) instead and is replaced by -inf afterwards (v0 < v1, and v1 is a multiple of 4 on the
@@ -166,29 +165,6 @@ __device__ __forceinline__ void load_buffer(const float* chunk, int bytes, float
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
             x[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)threadIdx.x * 4, i * kT * 4, POL));
-    }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void load_contig(const float* row, int v0, int v1, float (&x)[kPer]) {
-    if constexpr (VEC) {
-#pragma unroll
-        for (int it = 0; it < kPer / 4; ++it) {
-            const int v = contig_index(v0, it * 4);
-            const float4 f = *reinterpret_cast<const float4*>(row + min(v, v1 - 4));
-            const bool in = v < v1;
-            x[it * 4 + 0] = in ? f.x : kNegInf;
-            x[it * 4 + 1] = in ? f.y : kNegInf;
-            x[it * 4 + 2] = in ? f.z : kNegInf;
-            x[it * 4 + 3] = in ? f.w : kNegInf;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int v = contig_index(v0, i);
-            const float f = row[min(v, v1 - 1)];
-            x[i] = v < v1 ? f : kNegInf;
-        }
     }
 }
 
@@ -482,20 +458,35 @@ struct DrawShared {
     float rem;
     float wsum[4];
     float red[8];
+    float steps[4][kPer];  // per wave, per step of the located chunk: mass
 };
 
-// Inverse-CDF draw for sequence b from its chunk sums (a.csum; my_r / my_p are this thread's
-// run totals, loaded by the caller), run by a whole workgroup.
+// Largest run of chunk sums a thread of the draw keeps in registers (vocabularies up to
+// kT x kRunMax x kSpecChunk entries); longer runs are read from memory again in the walk.
+constexpr int kRunMax = 4;
+
+__device__ __forceinline__ int wave_max_int(int v) {
+    for (int m = 32; m >= 1; m >>= 1) v = max(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+// Inverse-CDF draw for sequence b from its chunk sums (a.csum; rv holds this thread's run of
+// them when it has at most kRunMax, and my_r / my_p are the run's totals, loaded by the caller),
+// run by a whole workgroup.
 // Locates the chunk holding u * total with a block scan of the chunk masses (thread t owns the
 // contiguous run [t * per, t * per + per), so the scan keeps index order), then walks that
-// chunk in index order and stores the token at out_tokens[b][pl.row].
+// chunk in index order and stores the token at out_tokens[b][pl.row]. Every cross-thread choice
+// (the first crossing, the last entry with mass) is settled within each wave by ballots and lane
+// reads before one thread per wave touches the shared word: 256 contending LDS atomics on one
+// address cost ~3.7 us here.
 template <bool VEC>
-__device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawShared& ds,
+__device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawShared& ds, const float2 (&rv)[kRunMax],
                            float my_r, float my_p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float2* cs = a.csum + (size_t)b * a.C;
     const int per = (a.C + kT - 1) / kT;
     const int c0 = threadIdx.x * per;
+    const int nrun = max(0, min(a.C, c0 + per) - c0);
     if (threadIdx.x == 0) {
         ds.chunk = 0x7fffffff;
         ds.last_chunk = -1;
@@ -519,32 +510,44 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
     __syncthreads();
     float ex = inc - mine;
     for (int w2 = 0; w2 < wave; ++w2) ex += ds.wsum[w2];
+    // Walk this thread's run in order: its first chunk where the running sum reaches the target
+    // (when the run's total does), and its last chunk with mass.
+    int my_chunk = 0x7fffffff, my_lastc = -1;
+    float my_rem = 0.f;
     if (mine > 0.f) {
-        if (ex + mine >= target) {
-            float cum = ex;  // walk this thread's run in order
-            for (int c = c0; c < min(a.C, c0 + per); ++c) {
-                const float w = use_res ? cs[c].x : cs[c].y;
-                if (w > 0.f && cum + w >= target) {
-                    atomicMin(&ds.chunk, c);
-                    break;
+        const bool reach = ex + mine >= target;
+        float cum = ex;
+        auto step = [&](int c, float w) {
+            if (w > 0.f) {
+                my_lastc = c;
+                if (reach && my_chunk == 0x7fffffff && cum + w >= target) {
+                    my_chunk = c;
+                    my_rem = target - cum;
                 }
-                cum += w;
             }
+            cum += w;
+        };
+        if (per <= kRunMax) {
+#pragma unroll
+            for (int i = 0; i < kRunMax; ++i)
+                if (i < nrun) step(c0 + i, use_res ? rv[i].x : rv[i].y);
+        } else {
+            for (int i = 0; i < nrun; ++i) step(c0 + i, use_res ? cs[c0 + i].x : cs[c0 + i].y);
         }
-        for (int c = min(a.C, c0 + per) - 1; c >= c0; --c)
-            if ((use_res ? cs[c].x : cs[c].y) > 0.f) {
-                atomicMax(&ds.last_chunk, c);
-                break;
-            }
+    }
+    // Runs ascend with the thread index: the wave's lowest crossing lane holds its first crossing.
+    const unsigned long long hit = __ballot(my_chunk != 0x7fffffff);
+    const int lastc = wave_max_int(my_lastc);
+    if (lane == 0) {
+        if (hit) atomicMin(&ds.chunk, __builtin_amdgcn_readlane(my_chunk, __ffsll((long long)hit) - 1));
+        if (lastc >= 0) atomicMax(&ds.last_chunk, lastc);
     }
     __syncthreads();
-    // The thread whose run holds the winning chunk derives the remainder from its scan prefix.
+    // The thread whose run holds the winning chunk publishes the remainder it computed.
     const int won = ds.chunk;
-    if (won != 0x7fffffff && won >= c0 && won < c0 + per) {
-        float cum = ex;
-        for (int c = c0; c < won; ++c) cum += use_res ? cs[c].x : cs[c].y;
-        ds.rem = target - cum;
-    } else if (won == 0x7fffffff && threadIdx.x == 0) {  // rounding left u * total past the end
+    if (won != 0x7fffffff) {
+        if (my_chunk == won) ds.rem = my_rem;
+    } else if (threadIdx.x == 0) {  // rounding left u * total past the end
         ds.chunk = ds.last_chunk < 0 ? a.C - 1 : ds.last_chunk;
         ds.rem = __builtin_huge_valf();
     }
@@ -553,39 +556,85 @@ __device__ void draw_token(const SpecArgs& a, int b, const SpecPlan& pl, DrawSha
     const float rem = ds.rem;
     const int v0 = chunk * a.chunk;
     const int v1 = min(a.V, v0 + a.chunk);
+    // The chunk in the streaming passes' strided layout (every load coalesced): step q of thread
+    // t covers entries EPS t .. EPS t + EPS - 1 of the step's EPS x kT consecutive entries, so the
+    // index order is (step, thread, entry). The walk locates the step from the step totals, then
+    // the thread from a block scan of that step, then the entry.
+    constexpr int EPS = VEC ? 4 : 1;
+    constexpr int NSTEP = kPer / EPS;
     float t[kPer], d[kPer], w[kPer];
-    load_contig<VEC>(target_row(a, b, pl.row), v0, v1, t);
-    if (use_res) load_contig<VEC>(draft_row(a, b, pl.row), v0, v1, d);
-    float ts = 0.f;
+    load_strided<VEC>(target_row(a, b, pl.row), v0, v1, t);
+    if (use_res) load_strided<VEC>(draft_row(a, b, pl.row), v0, v1, d);
+    float st[NSTEP];
     int my_last = -1;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        w[i] = draw_mass(pl, t[i], use_res ? d[i] : kNegInf, use_res);  // -inf past v1 -> 0
-        ts += w[i];
-        if (w[i] > 0.f) my_last = contig_index(v0, i);
-    }
-    // Exclusive scan of the per-thread sums in thread (= index) order.
-    const float inc2 = wave_incl_scan_f(ts);
-    if (lane == 63) ds.wsum[wave] = inc2;
-    __syncthreads();
-    float ex2 = inc2 - ts;
-    for (int w2 = 0; w2 < wave; ++w2) ex2 += ds.wsum[w2];
-    if (ex2 < rem && ex2 + ts >= rem) {
-        float cum = ex2;
-        int pick = my_last;
+    for (int q = 0; q < NSTEP; ++q) {
+        st[q] = 0.f;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            if (w[i] > 0.f) {
-                cum += w[i];
-                if (cum >= rem) {
-                    pick = contig_index(v0, i);
-                    break;
+        for (int e = 0; e < EPS; ++e) {
+            const int i = q * EPS + e;
+            w[i] = draw_mass(pl, t[i], use_res ? d[i] : kNegInf, use_res);  // -inf past v1 -> 0
+            st[q] += w[i];
+            if (w[i] > 0.f) my_last = strided_index<VEC>(v0, i);  // steps ascend: the last one wins
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NSTEP; ++q) {
+        const float x = wave_sum(st[q]);
+        if (lane == 0) ds.steps[wave][q] = x;
+    }
+    {
+        const int wl = wave_max_int(my_last);
+        if (lane == 0 && wl >= 0) atomicMax(&ds.last, wl);
+    }
+    __syncthreads();
+    // The step holding rem (uniform: every thread folds the same totals in the same order).
+    int sel = -1;
+    float rem2 = 0.f, cum = 0.f;
+#pragma unroll
+    for (int q = 0; q < NSTEP; ++q) {
+        const float x = (ds.steps[0][q] + ds.steps[1][q]) + (ds.steps[2][q] + ds.steps[3][q]);
+        if (sel < 0 && x > 0.f && cum + x >= rem) {
+            sel = q;
+            rem2 = rem - cum;
+        }
+        cum += x;
+    }
+    if (sel >= 0) {  // uniform
+        float mine = 0.f;
+#pragma unroll
+        for (int q = 0; q < NSTEP; ++q) mine = q == sel ? st[q] : mine;
+        const float inc2 = wave_incl_scan_f(mine);
+        if (lane == 63) ds.wsum[wave] = inc2;
+        __syncthreads();
+        float ex2 = inc2 - mine;
+        for (int w2 = 0; w2 < wave; ++w2) ex2 += ds.wsum[w2];
+        const bool cand = ex2 < rem2 && ex2 + mine >= rem2;
+        int pick = -1, last = -1;
+        if (cand) {
+            float c = ex2;
+#pragma unroll
+            for (int q = 0; q < NSTEP; ++q) {
+                if (q != sel) continue;
+#pragma unroll
+                for (int e = 0; e < EPS; ++e) {
+                    const int i = q * EPS + e;
+                    if (w[i] > 0.f) {
+                        last = strided_index<VEC>(v0, i);
+                        c += w[i];
+                        if (pick < 0 && c >= rem2) pick = last;
+                    }
                 }
             }
         }
-        atomicMin(&ds.pick, pick);
+        // Within step sel the entries ascend with the thread index: the wave's lowest candidate.
+        const unsigned long long cl = __ballot(cand);
+        if (cl) {
+            const int l = __ffsll((long long)cl) - 1;
+            const int v = __builtin_amdgcn_readlane(pick >= 0 ? pick : last, l);
+            if (lane == 0) atomicMin(&ds.pick, v);
+        }
     }
-    atomicMax(&ds.last, my_last);
     __syncthreads();
     if (threadIdx.x == 0) {
         int v = ds.pick != 0x7fffffff ? ds.pick : ds.last;
@@ -816,16 +865,30 @@ __global__ __launch_bounds__(kT) void spec_pick_kernel(SpecArgs a) {
     const float2* cs = a.csum + (size_t)b * a.C;
     const int per = (a.C + kT - 1) / kT;
     const int c0 = threadIdx.x * per;
+    const int nrun = max(0, min(a.C, c0 + per) - c0);
+    float2 rv[kRunMax];
     float my_r = 0.f, my_p = 0.f;
-    for (int c = c0; c < min(a.C, c0 + per); ++c) {
-        const float2 w = cs[c];
-        my_r += w.x;
-        my_p += w.y;
+    if (per <= kRunMax) {
+#pragma unroll
+        for (int i = 0; i < kRunMax; ++i) rv[i] = i < nrun ? cs[c0 + i] : make_float2(0.f, 0.f);
     }
     const SpecPlan p0 = a.plan[b], p1 = a.plan_tail[b];
+    if (per <= kRunMax) {
+#pragma unroll
+        for (int i = 0; i < kRunMax; ++i) {
+            my_r += rv[i].x;
+            my_p += rv[i].y;
+        }
+    } else {
+        for (int i = 0; i < nrun; ++i) {
+            const float2 w = cs[c0 + i];
+            my_r += w.x;
+            my_p += w.y;
+        }
+    }
     const SpecPlan pl = p0.mode == SPEC_PENDING ? p1 : p0;
     if (pl.mode == SPEC_DONE) return;
-    draw_token<VEC>(a, b, pl, ds, my_r, my_p);
+    draw_token<VEC>(a, b, pl, ds, rv, my_r, my_p);
 }
 
 }  // namespace
