@@ -106,9 +106,10 @@ int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, 
 
 /* ---------------------------------------------------------------- paged attention */
 
-/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (head_dim 128,
- * block_size 16; bf16 or f32 caches), whatever the number of query rows, and the vector kernel
- * otherwise (head_dim 64, other block sizes). */
+/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (block_size 16 and
+ * head_dim 128 with bf16 or f32 caches, or head_dim 64, 96 or 256 with bf16 caches), whatever the
+ * number of query rows, and the vector kernel otherwise (every other head_dim that is a multiple
+ * of 8 up to 256, other block sizes). */
 typedef enum kyro_attn_path {
     KYRO_ATTN_AUTO = 0,
     KYRO_ATTN_VECTOR = 1,
