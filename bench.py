@@ -514,11 +514,14 @@ def measure_config(name, warmup, steps, detailed=False, scratch=None):
     return line
 
 
-def head_dims_workload(warmup, steps):
-    """One JSON line: the attention at head dims 64, 80, 96, 128 and 256 on the Llama-3-8B verify
-    shape (GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV), AUTO (the MFMA kernel at 64,
-    96, 128 and 256, the vector kernel at 80) and the vector kernel, each on its algorithmic
-    bytes."""
+def shape_sweep_workload(kind, warmup, steps):
+    """One JSON line: the attention on the Llama-3-8B verify shape (GQA 32/8, batch 64, ctx 4096,
+    8 query rows, bf16 KV and out) at other head dims ("head-dims": 64, 80, 96, 128, 160, 192, 224
+    and 256 with 16-token blocks; AUTO takes the MFMA kernel at every multiple of 32, the vector
+    kernel at 80)
+    or other block sizes ("block-sizes": 8, 16, 32, 64 at head_dim 128; AUTO takes the MFMA
+    kernel at every multiple of 16, the vector kernel at 8), AUTO and the vector kernel, each on
+    its algorithmic bytes."""
     import torch
 
     import kyro_amd
@@ -526,15 +529,17 @@ def head_dims_workload(warmup, steps):
     from kyro_amd.attention import describe_attention
 
     dev = torch.device("cuda", 0)
-    res = {"workload": "head-dims", "shape": "GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV and out"}
-    for D in (64, 80, 96, 128, 256):
+    res = {"workload": kind, "shape": "GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV and out"}
+    points = ([(D, 16) for D in (64, 80, 96, 128, 160, 192, 224, 256)] if kind == "head-dims"
+              else [(128, bs) for bs in (8, 16, 32, 64)])
+    for D, bs in points:
         case = wl.make_attention_case(context_lens=[4096] * 64, q_lens=[8] * 64, num_heads=32, num_kv_heads=8,
-                                      head_dim=D, dtype="bf16", seed=D)
+                                      head_dim=D, block_size=bs, dtype="bf16", seed=D + bs)
         up = lambda x: torch.from_numpy(x).view(torch.bfloat16).to(dev)  # noqa: E731
         t = dict(q=up(case.query), kc=up(case.key_cache), vc=up(case.value_cache),
                  table=torch.from_numpy(case.block_table).to(dev), ctx=torch.from_numpy(case.context_lens).to(dev),
                  qs=torch.from_numpy(case.q_start_loc).to(dev))
-        attn = kyro_amd.PagedAttention(16, 32, D, 8)
+        attn = kyro_amd.PagedAttention(bs, 32, D, 8)
         out = torch.empty(t["q"].shape, dtype=torch.bfloat16, device=dev)
         nbytes = case.kv_bytes() + case.q_out_bytes(2)
         entry = {"algorithmic_bytes": nbytes}
@@ -544,9 +549,9 @@ def head_dims_workload(warmup, steps):
                 out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
             entry[path] = {"us": us, "GB_s": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / PEAK_HBM_GBS,
                            "launch": describe_attention(attn, batch=64, total_q=512, max_q_len=8,
-                                                        max_blocks_per_seq=256, num_blocks=case.key_cache.shape[0],
-                                                        path=path, device=0)}
-        res[f"d{D}"] = entry
+                                                        max_blocks_per_seq=case.block_table.shape[1],
+                                                        num_blocks=case.key_cache.shape[0], path=path, device=0)}
+        res[f"d{D}" if kind == "head-dims" else f"bs{bs}"] = entry
         del t, out
         torch.cuda.empty_cache()
     print(json.dumps(res), flush=True)
@@ -579,13 +584,14 @@ def main():
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
                              "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "ngram-draft",
-                             "head-dims", "others"],
+                             "head-dims", "block-sizes", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
         names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables",
-                  "decode-sample", "ngram-draft", "head-dims"] if args.workload == "others" else [args.workload])
+                  "decode-sample", "ngram-draft", "head-dims", "block-sizes"] if args.workload == "others"
+                 else [args.workload])
         for n in names:
             if n == "kv-append":
                 kv_append_workload(args.warmup, args.steps)
@@ -595,8 +601,8 @@ def main():
                 decode_sample_workload(args.warmup, args.steps)
             elif n == "ngram-draft":
                 ngram_draft_workload(args.warmup, args.steps)
-            elif n == "head-dims":
-                head_dims_workload(args.warmup, args.steps)
+            elif n in ("head-dims", "block-sizes"):
+                shape_sweep_workload(n, args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
         return

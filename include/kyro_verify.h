@@ -106,10 +106,10 @@ int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, 
 
 /* ---------------------------------------------------------------- paged attention */
 
-/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (block_size 16 and
- * head_dim 128 with bf16 or f32 caches, or head_dim 64, 96 or 256 with bf16 caches), whatever the
- * number of query rows, and the vector kernel otherwise (every other head_dim that is a multiple
- * of 8 up to 256, other block sizes). */
+/* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (a block_size that is a
+ * multiple of 16, and head_dim 128 with bf16 or f32 caches or any multiple of 32 from 64 to 256
+ * with bf16 caches), whatever the number of query rows, and the vector kernel otherwise (every
+ * other head_dim that is a multiple of 8 up to 256, block sizes that are not multiples of 16). */
 typedef enum kyro_attn_path {
     KYRO_ATTN_AUTO = 0,
     KYRO_ATTN_VECTOR = 1,
@@ -221,7 +221,8 @@ int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_param
  * sequence without rows). */
 typedef struct kyro_attention_plan {
     int32_t grid;          /* persistent workgroups */
-    int32_t chunk_blocks;  /* blocks per split of a sequence that splits */
+    int32_t chunk_blocks;  /* 16-token slots per split of a sequence that splits (the MFMA
+                              kernels walk a block of 16 m tokens as m slots) */
     int64_t items;         /* work items: sequence x kv head group x split x row group, one
                               partial-state slot each */
     int64_t slot_bound;    /* partial-state slots a launch with these params sizes; the device

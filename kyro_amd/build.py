@@ -20,7 +20,7 @@ OBJDIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libkyro_verify.so")
 STATIC_LIB = os.path.join(HERE, "libkyro_verify.a")
 SOURCES = ["runtime.cpp", "upload.hip", "blocks_abi.cpp", "block_manager.cpp", "sample_abi.cpp", "ngram_abi.cpp",
-           "paged_attention.hip", "paged_attention_hd.hip", "spec_verify.hip", "kv_append.hip", "sample.hip", "ngram.hip", "noalloc.hip"]
+           "paged_attention.hip", "paged_attention_hd.hip", "paged_attention_hd_wide.hip", "spec_verify.hip", "kv_append.hip", "sample.hip", "ngram.hip", "noalloc.hip"]
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -47,6 +47,11 @@ struct AttnArgs {
     float* ws_acc;   // [units, splits, rows_cap, D]
     int* err;        // device error word
     int B, H, Hkv, group, D, bs;
+    // Tokens per block slot the kernel walks (ubs) and slots per cache block (sub = bs / ubs):
+    // the vector kernel walks whole blocks (ubs = bs, sub = 1); the MFMA kernels walk 16-token
+    // slots, so a block of 16 m tokens is m slots. Slot s of block p, kv head h is the 16 x D
+    // slab at element ((p Hkv + h) bs + 16 s) D of a cache.
+    int ubs, sub;
     int max_blocks, num_blocks, total_q, max_q_len, rows_cap;
     int causal, out_bf16, dtype_bf16;
     float scale_log2;  // softmax scale * log2(e)
@@ -155,14 +160,17 @@ __host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16, int D) {
     return rows <= 16 ? 16 : (rows <= 32 || !bf16 || D != 128) ? 32 : kMfmaManyRows;
 }
 
-// Head dims the bf16 MFMA kernel is built for (block size 16); f32 caches take it at 128 only.
+// Head dims the bf16 MFMA kernel is built for (every multiple of 32 from 64 to 256); f32 caches
+// take it at 128 only.
 __host__ __device__ inline bool mfma_head_dim(int D, bool bf16) {
-    return D == 128 || (bf16 && (D == 64 || D == 96 || D == 256));
+    return D == 128 || (bf16 && D % 32 == 0 && D >= 64 && D <= 256);
 }
 
 hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
-// The bf16 MFMA kernel at head dims 64, 96 and 256 (its own translation unit).
+// The bf16 MFMA kernel at head dims 64, 96 and 256, and at 160, 192 and 224 (a translation unit
+// each).
 hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream);
+hipError_t launch_paged_attention_mfma_hd_wide(const AttnArgs& a, hipStream_t stream);
 
 // Per-sequence decision taken after the acceptance scan.
 struct SpecPlan {

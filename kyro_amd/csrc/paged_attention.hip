@@ -88,7 +88,7 @@ __device__ SeqInfo seq_info(const AttnArgs& a, int unit) {
     s.q0 = q0;
     s.q_len = s.ok ? q1 - q0 : 0;
     s.rows = s.q_len * a.group;
-    s.nblk = (s.ctx + a.bs - 1) / a.bs;
+    s.nblk = (s.ctx + a.ubs - 1) / a.ubs;
     return s;
 }
 
@@ -342,7 +342,7 @@ constexpr int kRawBufferWord3 = 0x00020000;
 template <int POL, int KM, int D>
 __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
-                                          size_t block_stride, size_t kv_off, int r, int g) {
+                                          size_t slot_stride, size_t kv_off, int r, int g) {
     static_assert(KM != kKDma || D == kMfmaD, "the LDS-staged K tiles hold 256-byte token rows");
     constexpr int kSlabBytes = kMfmaBS * D * 2;
     constexpr int T = D / 16;
@@ -352,7 +352,7 @@ __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, 
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
         const int blk = bi ? blk1 : blk0;
-        const size_t base = (size_t)(blk >= 0 ? blk : 0) * block_stride + kv_off;
+        const size_t base = (size_t)(blk >= 0 ? blk : 0) * slot_stride + kv_off;
         const uint16_t* kslab = blk >= 0 ? kp + base : kZeroSlab;
         const uint16_t* vslab = blk >= 0 ? vp + base : kZeroSlab;
         kr[bi] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kslab), (short)0, kSlabBytes, kRawBufferWord3);
@@ -379,34 +379,34 @@ __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, 
         }
     }
     // V: T consecutive bf16 of one token row per lane (16 bytes at D = 128, 8 at 64, 12 at 96,
-    // 32 at 256), in the widest loads that many bytes allow.
+    // 32 at 256; 20, 24 and 28 at 160, 192 and 224), in 16-byte loads and one narrower load for
+    // the rest (the offsets are 4-byte aligned, which buffer loads of several dwords accept).
+    constexpr int kVW = KVPair<D>::kVW;
+    constexpr int kV4 = kVW / 4 * 4;  // words loaded 16 bytes at a time
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             uint32_t* w = p.v[bi][e];
-            if constexpr (KVPair<D>::kVW % 4 == 0) {
 #pragma unroll
-                for (int q = 0; q < KVPair<D>::kVW; q += 4) {
-                    const auto x = __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 2 * D * e + 4 * q, POL);
-                    w[q] = x[0];
-                    w[q + 1] = x[1];
-                    w[q + 2] = x[2];
-                    w[q + 3] = x[3];
-                }
-            } else if constexpr (KVPair<D>::kVW == 3) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr[bi], voff, 2 * D * e, POL);
-                w[0] = x[0];
-                w[1] = x[1];
-                w[2] = x[2];
-            } else if constexpr (KVPair<D>::kVW == 2) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b64(vr[bi], voff, 2 * D * e, POL);
-                w[0] = x[0];
-                w[1] = x[1];
-            } else {
-#pragma unroll
-                for (int q = 0; q < KVPair<D>::kVW; ++q)
-                    w[q] = __builtin_amdgcn_raw_buffer_load_b32(vr[bi], voff, 2 * D * e + 4 * q, POL);
+            for (int q = 0; q < kV4; q += 4) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 2 * D * e + 4 * q, POL);
+                w[q] = x[0];
+                w[q + 1] = x[1];
+                w[q + 2] = x[2];
+                w[q + 3] = x[3];
+            }
+            if constexpr (kVW - kV4 == 3) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
+                w[kV4] = x[0];
+                w[kV4 + 1] = x[1];
+                w[kV4 + 2] = x[2];
+            } else if constexpr (kVW - kV4 == 2) {
+                const auto x = __builtin_amdgcn_raw_buffer_load_b64(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
+                w[kV4] = x[0];
+                w[kV4 + 1] = x[1];
+            } else if constexpr (kVW - kV4 == 1) {
+                w[kV4] = __builtin_amdgcn_raw_buffer_load_b32(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
             }
         }
 }
@@ -428,13 +428,17 @@ __device__ __forceinline__ void read_k_tile(KVPair<kMfmaD>& p, const uint4* __re
         for (int s = 0; s < 4; ++s) p.k[bi][s] = __builtin_bit_cast(bf16x8, tile[bi * 256 + r * 16 + ((4 * s + g) ^ r)]);
 }
 
-// Stages the block ids of the workgroup's split in LDS (validated once, -1 for a bad id), so the
-// streaming loop never waits on a table load before issuing K/V loads.
+// Stages the 16-token slots [blk_begin, blk_end) of the workgroup's split in LDS, validated once,
+// so the streaming loop never waits on a table load before issuing K/V loads. Slot i is slot
+// i % sub of block table[i / sub]; it is staged as p Hkv sub + i % sub (-1 for a bad id), the
+// index of its kv-head-0 slab in units of one 16 x D slab, so that the slab of kv head h starts
+// at element (id x 16 D + h bs D) of a cache.
 __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo& si, int blk_begin,
                                                 int blk_end, int* s_blk) {
     for (int i = blk_begin + (int)threadIdx.x; i < blk_end; i += kThreads) {
-        const int64_t blk = checked_block(a, si.b, i);
-        s_blk[i - blk_begin] = (int)blk;
+        const int q = i / a.sub;
+        const int64_t blk = checked_block(a, si.b, q);
+        s_blk[i - blk_begin] = blk < 0 ? -1 : (int)blk * a.Hkv * a.sub + (i - q * a.sub);
     }
     __syncthreads();
 }
@@ -604,7 +608,7 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
             const int ctx = ok ? (int)c : 0;
             const int ql = ok ? s1 - s0 : 0;
             const int r = (ql * a.group + RW - 1) / RW;
-            const int nb = (ctx + a.bs - 1) / a.bs;
+            const int nb = (ctx + a.ubs - 1) / a.ubs;
             P.ctx[sq] = ctx;
             P.q0[sq] = ok ? s0 : 0;
             P.qlen[sq] = ql;
@@ -639,7 +643,7 @@ __device__ void plan_build(const AttnArgs& a, PlanLds& P) {
     for (int j = 0; j < S; ++j) {
         const int sq = S * t + j;
         r[j] = sq < a.B ? P.r[sq] : 0;
-        const int nb = sq < a.B ? (P.ctx[sq] + a.bs - 1) / a.bs : 0;
+        const int nb = sq < a.B ? (P.ctx[sq] + a.ubs - 1) / a.ubs : 0;
         const int ql = sq < a.B ? P.qlen[sq] : 0;
         int n, ch;
         plan_split(nb, C, n, ch);
@@ -813,9 +817,8 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
     const uint16_t* __restrict__ qp = reinterpret_cast<const uint16_t*>(a.q);
     const uint16_t* __restrict__ kp = reinterpret_cast<const uint16_t*>(a.k);
     const uint16_t* __restrict__ vp = reinterpret_cast<const uint16_t*>(a.v);
-    const size_t head_stride = (size_t)kMfmaBS * D;               // one (block, kv head) slab
-    const size_t block_stride = (size_t)a.Hkv * head_stride;      // one block, all kv heads
-    const size_t kv_off = (size_t)si.kvh * head_stride;
+    const size_t slot_stride = (size_t)kMfmaBS * D;           // one (slot, kv head) slab
+    const size_t kv_off = (size_t)si.kvh * a.bs * D;           // kv head si.kvh within a block
     const float c = a.scale_log2;
     // Tokens below full_vis are visible to every query row of the sequence.
     const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
@@ -1061,14 +1064,14 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
                 constexpr int P = decltype(pol)::value;
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<P, KM, D>(bufB, ktB, kp, vp, b0, b1, block_stride, kv_off, r, g);
+                    load_pair<P, KM, D>(bufB, ktB, kp, vp, b0, b1, slot_stride, kv_off, r, g);
                     compute(bufA, ktA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, block_stride, kv_off, r, g);
+                    load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
                     compute(bufB, ktB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
@@ -1173,10 +1176,10 @@ struct KVBlockF32 {
 
 template <int POL>
 __device__ __forceinline__ void load_block_f32(KVBlockF32& kv, const float* __restrict__ kp,
-                                               const float* __restrict__ vp, int blk, size_t block_stride,
+                                               const float* __restrict__ vp, int blk, size_t slot_stride,
                                                size_t kv_off, int r, int g) {
     constexpr int kSlabBytes = kMfmaBS * kMfmaD * 4;
-    const size_t base = (size_t)(blk >= 0 ? blk : 0) * block_stride + kv_off;
+    const size_t base = (size_t)(blk >= 0 ? blk : 0) * slot_stride + kv_off;
     const float* kslab = blk >= 0 ? kp + base : kZeroSlabF32;
     const float* vslab = blk >= 0 ? vp + base : kZeroSlabF32;
     const __amdgpu_buffer_rsrc_t kr =
@@ -1219,9 +1222,8 @@ __device__ __forceinline__ void mfma_item_f32(const AttnArgs& a, Frame<NTW * 16,
     const float* __restrict__ qp = reinterpret_cast<const float*>(a.q);
     const float* __restrict__ kp = reinterpret_cast<const float*>(a.k);
     const float* __restrict__ vp = reinterpret_cast<const float*>(a.v);
-    const size_t head_stride = (size_t)kMfmaBS * D;
-    const size_t block_stride = (size_t)a.Hkv * head_stride;
-    const size_t kv_off = (size_t)si.kvh * head_stride;
+    const size_t slot_stride = (size_t)kMfmaBS * D;
+    const size_t kv_off = (size_t)si.kvh * a.bs * D;
     const float c = a.scale_log2;
     const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
 
@@ -1352,14 +1354,14 @@ __device__ __forceinline__ void mfma_item_f32(const AttnArgs& a, Frame<NTW * 16,
             if (nblk > 0) {
                 int j = 0;
                 int ia = block_id(0), ib;
-                load_block_f32<POL>(bufA, kp, vp, ia, block_stride, kv_off, r, g);
+                load_block_f32<POL>(bufA, kp, vp, ia, slot_stride, kv_off, r, g);
                 while (true) {
                     ib = next_id(j);
-                    load_block_f32<POL>(bufB, kp, vp, ib, block_stride, kv_off, r, g);
+                    load_block_f32<POL>(bufB, kp, vp, ib, slot_stride, kv_off, r, g);
                     compute(bufA, b0 + j * WPH, ia);
                     if (++j >= nblk) break;
                     ia = next_id(j);
-                    load_block_f32<POL>(bufA, kp, vp, ia, block_stride, kv_off, r, g);
+                    load_block_f32<POL>(bufA, kp, vp, ia, slot_stride, kv_off, r, g);
                     compute(bufB, b0 + j * WPH, ib);
                     if (++j >= nblk) break;
                 }
@@ -1460,7 +1462,7 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
             si.q0 = __builtin_amdgcn_readfirstlane(plan.q0[b]);
             si.q_len = __builtin_amdgcn_readfirstlane(plan.qlen[b]);
             si.rows = si.q_len * a.group;
-            si.nblk = (si.ctx + a.bs - 1) / a.bs;
+            si.nblk = (si.ctx + a.ubs - 1) / a.ubs;
             si.ok = true;
             const int nsplit = __builtin_amdgcn_readfirstlane(plan.ns[b]);
             const int blk_begin = chunk * C;
@@ -1777,10 +1779,11 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------ launcher
 
 #ifdef KYRO_ATTN_HD_UNIT
-// The bf16 MFMA kernel at head dims other than 128 (64, 96, 256), in a translation unit of its
-// own so that its instances compile in parallel with the rest: at most two row tiles per wave
-// (one at 256, whose K/V pairs and accumulators fill the register file), one or two kv heads per
-// workgroup, streaming or cached K/V loads, grid or balanced schedule.
+// The bf16 MFMA kernel at head dims other than 128 (64, 96 and 256 in one translation unit, 160,
+// 192 and 224 in another, so that their instances compile in parallel with the rest): at most two
+// row tiles per wave (one above 128, where the K/V pairs and accumulators fill the register
+// file), one or two kv heads per workgroup, streaming or cached K/V loads, grid or balanced
+// schedule.
 template <int D>
 hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream) {
     const dim3 block(kThreads);
@@ -1824,6 +1827,7 @@ hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream
 
 }  // namespace
 
+#if KYRO_ATTN_HD_UNIT == 1
 hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream) {
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
@@ -1834,6 +1838,18 @@ hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream)
         default: return hipErrorInvalidValue;
     }
 }
+#else
+hipError_t launch_paged_attention_mfma_hd_wide(const AttnArgs& a, hipStream_t stream) {
+    const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
+    if (grid.x == 0) return hipSuccess;
+    switch (a.D) {
+        case 160: return launch_mfma_hd<160>(a, grid, stream);
+        case 192: return launch_mfma_hd<192>(a, grid, stream);
+        case 224: return launch_mfma_hd<224>(a, grid, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+#endif
 
 #else  // KYRO_ATTN_HD_UNIT
 
@@ -1843,7 +1859,9 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     const dim3 block(kThreads);
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
-    if (path == ATTN_KERNEL_MFMA && a.D != kMfmaD) return launch_paged_attention_mfma_hd(a, stream);
+    if (path == ATTN_KERNEL_MFMA && a.D != kMfmaD)
+        return (a.D == 160 || a.D == 192 || a.D == 224) ? launch_paged_attention_mfma_hd_wide(a, stream)
+                                                         : launch_paged_attention_mfma_hd(a, stream);
     if (path == ATTN_KERNEL_MFMA) {
         const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
         const bool rows16 = rpg == 16;

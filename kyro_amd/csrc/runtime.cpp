@@ -202,12 +202,17 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (max_q_len <= 0) max_q_len = have_q_start ? p->total_q : 1;
     if (!have_q_start) max_q_len = 1;
 
-    const bool mfma_ok = p->block_size == 16 && kyro::mfma_head_dim(p->head_dim, p->dtype == KYRO_BF16);
+    // The MFMA kernels walk 16-token slots: any block size that is a multiple of 16, with every
+    // slot's index (block x kv heads x slots per block) in 31 bits.
+    const bool mfma_blocks = p->block_size % 16 == 0 &&
+                             (long long)p->num_blocks * p->num_kv_heads * (p->block_size / 16) < (1ll << 31);
+    const bool mfma_ok = mfma_blocks && kyro::mfma_head_dim(p->head_dim, p->dtype == KYRO_BF16);
     int kernel;
     if (p->path == KYRO_ATTN_MFMA) {
         if (!mfma_ok)
-            return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs block_size 16 and head_dim 128 "
-                        "(bf16 caches: 64, 96, 128 or 256)");
+            return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs a block_size that is a multiple of "
+                        "16 and head_dim 128 (bf16 caches: a multiple of 32 from 64 to 256); got block_size %d, head_dim %d",
+                        p->block_size, p->head_dim);
         kernel = kyro::ATTN_KERNEL_MFMA;
     } else if (p->path == KYRO_ATTN_VECTOR) {
         kernel = kyro::ATTN_KERNEL_VECTOR;
@@ -219,7 +224,7 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     }
     if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
         return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
-                    "(block_size 16; head_dim 128, or 64, 96, 256 with bf16 caches)");
+                    "(block_size a multiple of 16; head_dim 128, or a multiple of 32 from 64 to 256 with bf16 caches)");
 
     kyro::AttnArgs& a = s.a;
     a.B = p->batch_size;
@@ -228,6 +233,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     a.group = group;
     a.D = p->head_dim;
     a.bs = p->block_size;
+    a.ubs = kernel == kyro::ATTN_KERNEL_MFMA ? 16 : p->block_size;
+    a.sub = a.bs / a.ubs;
     a.max_blocks = p->max_blocks_per_seq;
     a.num_blocks = p->num_blocks;
     a.total_q = p->total_q;
@@ -260,8 +267,13 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups > 1 && rows_per_group == kyro::kMfmaManyRows)
         a.stream_kv = kyro::kKvPerUnit;
 
-    // Context splits: enough workgroups to cover the chip, chunks of whole block pairs.
-    const int mb = std::max(1, p->max_blocks_per_seq);
+    // Context splits: enough workgroups to cover the chip, chunks of whole slot pairs (a slot is
+    // a block of the vector kernel, 16 tokens of the MFMA kernels).
+    const long long mb_slots = (long long)std::max(1, p->max_blocks_per_seq) * a.sub;
+    if (mb_slots > (1ll << 30))
+        return fail(KYRO_EUNSUPPORTED, "paged_attention: max_blocks_per_seq %d x block_size %d tokens is too long",
+                    p->max_blocks_per_seq, p->block_size);
+    const int mb = (int)mb_slots;
     int splits = p->num_splits;
     if (splits <= 0) {
         // At most ~256 blocks (4096 tokens) per workgroup so a long context does not leave
@@ -739,7 +751,7 @@ int kyro_paged_attention_plan(const kyro_paged_attention_params* p, int num_cus,
                 return fail(KYRO_EINVAL, "paged_attention_plan: sequence %d: context length %lld or rows %d out of range",
                             b, c, ql);
             r[b] = (ql * a.group + a.plan_rw - 1) / a.plan_rw;
-            nb[b] = (int)((c + a.bs - 1) / a.bs);
+            nb[b] = (int)((c + a.ubs - 1) / a.ubs);
             T += (long long)U * r[b] * nb[b];
             if (r[b] > 0) maxnb = std::max(maxnb, nb[b]);
         }

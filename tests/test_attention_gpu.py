@@ -93,11 +93,11 @@ def test_small_parity(gpu, dtype, shape, path, splits):
 # Head dims of the reference's models (head_dim = hidden_size / num_attention_heads,
 # src/model/llama.rs:35, src/model/qwen.rs:31): every multiple of 8 up to 256 runs, including
 # ones that are not multiples of 16 (8 lanes per token row instead of 16).
-HEAD_DIMS = [8, 64, 72, 80, 96, 112, 128, 160, 192, 248, 256]
+HEAD_DIMS = [8, 64, 72, 80, 96, 112, 128, 160, 192, 224, 248, 256]
 
 
-# bf16 head dims the MFMA kernel takes besides 128 (block size 16)
-MFMA_HEAD_DIMS = (64, 96, 256)
+# bf16 head dims the MFMA kernel takes besides 128: every multiple of 32 from 64 to 256
+MFMA_HEAD_DIMS = (64, 96, 160, 192, 224, 256)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -230,6 +230,86 @@ def test_cache_slots_past_the_context_are_never_used(gpu, dtype):
                                t["context_lens"], q_start_loc=t["q_start_loc"], path=path,
                                num_splits=splits)
             h.assert_attention_close(out, case, exp, h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
+
+
+# Block sizes besides Kyro's 16 (its --block-size flag, src/config.rs:24-26): the MFMA kernels
+# walk a block of 16 m tokens as m 16-token slots; other sizes run on the vector kernel.
+BLOCK_SIZES = [8, 32, 48, 64, 256]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("D", [128, 64])
+@pytest.mark.parametrize("bs", BLOCK_SIZES)
+def test_block_sizes(gpu, dtype, D, bs):
+    """Every path at each block size against the oracle: AUTO, the vector kernel, and where the
+    MFMA kernel applies (block size a multiple of 16; f32 at head_dim 128 only) the MFMA kernel
+    on the grid with 1 and 3 splits and under the balanced schedule. Contexts end inside a
+    block's first, middle and last 16-token slot, and cover several blocks."""
+    ctx, ql = [70, 5, 33, 130, 600, 16], [5, 1, 3, 8, 2, 4]
+    case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=8, num_kv_heads=2, head_dim=D,
+                                  block_size=bs, dtype=dtype, seed=50 + bs + D)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(bs, 8, D, 2)
+    exp = h.oracle_attention(case)
+    runs = [dict(), dict(path="vector"), dict(path="vector", num_splits=3)]
+    mfma = bs % 16 == 0 and (D == 128 or dtype == "bf16")
+    if mfma:
+        runs += [dict(path="mfma", num_splits=1), dict(path="mfma", num_splits=3), dict(schedule="balanced")]
+    else:
+        with pytest.raises(kyro_amd.KyroError, match="block_size"):
+            attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                         q_start_loc=t["q_start_loc"], path="mfma")
+    for kw in runs:
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                           q_start_loc=t["q_start_loc"], **kw)
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16 if dtype == "bf16" else h.ATOL_F32)
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_block_sizes_nan_past_the_context_and_long(gpu, bs):
+    """At 32- and 64-token blocks: NaN in every slot past each context (inside the last block's
+    16-token slots too) and in unreferenced blocks, and contexts of 9000 and 20000 tokens under
+    both schedules, against the oracle (bf16 KV, GQA 32/8, 8 query rows)."""
+    ctx = [17, 40, 33, 100, 1, 48]
+    case = wl.make_attention_case(context_lens=ctx, q_lens=[1, 5, 8, 3, 1, 4], num_heads=8, num_kv_heads=2,
+                                  block_size=bs, dtype="bf16", seed=60 + bs, num_blocks=64)
+    nan = np.uint16(0x7FC0)
+    used = set()
+    for b, c in enumerate(ctx):
+        nb = -(-c // bs)
+        used.update(int(x) for x in case.block_table[b, :nb])
+        last, tail = int(case.block_table[b, nb - 1]), c - (nb - 1) * bs
+        case.key_cache[last, :, tail:, :] = nan
+        case.value_cache[last, :, tail:, :] = nan
+    unused = [i for i in range(case.key_cache.shape[0]) if i not in used]
+    case.key_cache[unused] = nan
+    case.value_cache[unused] = nan
+    t = h.attention_tensors(case, gpu)
+    exp = h.oracle_attention(case)
+    attn = make_attention(bs, 8, 128, 2)
+    for kw in (dict(path="mfma"), dict(path="mfma", num_splits=2), dict(schedule="balanced")):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                           q_start_loc=t["q_start_loc"], **kw)
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16)
+    case = wl.make_attention_case(context_lens=[9000, 20000, 700], q_lens=[8, 8, 8], num_heads=32, num_kv_heads=8,
+                                  block_size=bs, dtype="bf16", seed=70 + bs)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(bs, 32, 128, 8)
+    exp = h.oracle_attention(case)
+    for kw in (dict(schedule="grid"), dict(schedule="balanced")):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                           q_start_loc=t["q_start_loc"], out_dtype=torch.bfloat16, **kw)
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16)
+    # GQA 64/8 with up to 64 rows per kv head: the four-tile kernel
+    case = wl.make_attention_case(context_lens=[3000, 700, 50], q_lens=[8, 5, 1], num_heads=64, num_kv_heads=8,
+                                  block_size=bs, dtype="bf16", seed=80 + bs)
+    t = h.attention_tensors(case, gpu)
+    attn = make_attention(bs, 64, 128, 8)
+    exp = h.oracle_attention(case)
+    for kw in (dict(schedule="grid"), dict(schedule="balanced")):
+        out = attn.forward(t["query"], t["key_cache"], t["value_cache"], t["block_table"], t["context_lens"],
+                           q_start_loc=t["q_start_loc"], **kw)
+        h.assert_attention_close(out, case, exp, h.ATOL_BF16)
 
 
 def test_long_context_in_one_split(gpu):
