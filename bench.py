@@ -516,9 +516,8 @@ def measure_config(name, warmup, steps, detailed=False, scratch=None):
 
 def shape_sweep_workload(kind, warmup, steps):
     """One JSON line: the attention on the Llama-3-8B verify shape (GQA 32/8, batch 64, ctx 4096,
-    8 query rows, bf16 KV and out) at other head dims ("head-dims": 64, 80, 96, 128, 160, 192, 224
-    and 256 with 16-token blocks; AUTO takes the MFMA kernel at every multiple of 32, the vector
-    kernel at 80)
+    8 query rows, bf16 KV and out) at other head dims ("head-dims": 64, 80, 96, 112, 128, 160, 192,
+    224 and 256 with 16-token blocks; AUTO takes the MFMA kernel at each of them)
     or other block sizes ("block-sizes": 8, 16, 32, 64 at head_dim 128; AUTO takes the MFMA
     kernel at every multiple of 16, the vector kernel at 8), AUTO and the vector kernel, each on
     its algorithmic bytes."""
@@ -530,7 +529,7 @@ def shape_sweep_workload(kind, warmup, steps):
 
     dev = torch.device("cuda", 0)
     res = {"workload": kind, "shape": "GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV and out"}
-    points = ([(D, 16) for D in (64, 80, 96, 128, 160, 192, 224, 256)] if kind == "head-dims"
+    points = ([(D, 16) for D in (64, 80, 96, 112, 128, 160, 192, 224, 256)] if kind == "head-dims"
               else [(128, bs) for bs in (8, 16, 32, 64)])
     for D, bs in points:
         case = wl.make_attention_case(context_lens=[4096] * 64, q_lens=[8] * 64, num_heads=32, num_kv_heads=8,

@@ -107,9 +107,10 @@ int kyro_buf_download(kyro_ctx ctx, void* dst, kyro_buf src, size_t src_offset, 
 /* ---------------------------------------------------------------- paged attention */
 
 /* Attention-kernel choice. AUTO picks the MFMA kernel whenever it applies (a block_size that is a
- * multiple of 16, and head_dim 128 with bf16 or f32 caches or any multiple of 32 from 64 to 256
- * with bf16 caches), whatever the number of query rows, and the vector kernel otherwise (every
- * other head_dim that is a multiple of 8 up to 256, block sizes that are not multiples of 16). */
+ * multiple of 16, and head_dim 128 with bf16 or f32 caches, or with bf16 caches head_dim 80, 112
+ * or any multiple of 32 from 64 to 256), whatever the number of query rows, and the vector kernel
+ * otherwise (every other head_dim that is a multiple of 8 up to 256, block sizes that are not
+ * multiples of 16). */
 typedef enum kyro_attn_path {
     KYRO_ATTN_AUTO = 0,
     KYRO_ATTN_VECTOR = 1,

@@ -160,15 +160,15 @@ __host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16, int D) {
     return rows <= 16 ? 16 : (rows <= 32 || !bf16 || D != 128) ? 32 : kMfmaManyRows;
 }
 
-// Head dims the bf16 MFMA kernel is built for (every multiple of 32 from 64 to 256); f32 caches
-// take it at 128 only.
+// Head dims the bf16 MFMA kernel is built for: every multiple of 32 from 64 to 256, and 80 and 112
+// in the operand layouts of 96 and 128; f32 caches take it at 128 only.
 __host__ __device__ inline bool mfma_head_dim(int D, bool bf16) {
-    return D == 128 || (bf16 && D % 32 == 0 && D >= 64 && D <= 256);
+    return D == 128 || (bf16 && ((D % 32 == 0 && D >= 64 && D <= 256) || D == 80 || D == 112));
 }
 
 hipError_t launch_paged_attention(const AttnArgs& a, int kernel, hipStream_t stream);
-// The bf16 MFMA kernel at head dims 64, 96 and 256, and at 160, 192 and 224 (a translation unit
-// each).
+// The bf16 MFMA kernel at head dims 64, 80, 96 and 256, and at 112, 160, 192 and 224 (a
+// translation unit each).
 hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream);
 hipError_t launch_paged_attention_mfma_hd_wide(const AttnArgs& a, hipStream_t stream);
 

@@ -140,11 +140,11 @@ struct Frame {
 
 // After every wave has added its rescaled accumulator: either normalise and store the rows
 // (single split) or park the split's partial state in the workspace, local row n at workspace
-// row pbase + n.
-template <int R, int D>
+// row pbase + n. The frame holds D columns; rows in memory (out, workspace) hold the first DR.
+template <int R, int D, int DR = D>
 __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int nsplit, int row0, int nrows,
                             Frame<R, D>& f, int nslots, size_t pbase) {
-    constexpr int Q = D / 4;
+    constexpr int Q = DR / 4;
     if (nsplit == 1) {
         for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
             const int n = idx / Q, d = (idx - n * Q) * 4;
@@ -152,8 +152,8 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int nsplit, in
             for (int w = 0; w < nslots; ++w) L += f.l[w][n];
             const float inv = L > 0.f ? 1.f / L : 0.f;
             const float* src = &f.acc[n * Frame<R, D>::kStride + d];
-            store_row4<D>(a, out_row(a, si, row0 + n), d, src[0] * inv, src[1] * inv, src[2] * inv,
-                          src[3] * inv);
+            store_row4<DR>(a, out_row(a, si, row0 + n), d, src[0] * inv, src[1] * inv, src[2] * inv,
+                           src[3] * inv);
         }
         return;
     }
@@ -166,7 +166,7 @@ __device__ void frame_flush(const AttnArgs& a, const SeqInfo& si, int nsplit, in
     for (int idx = threadIdx.x; idx < nrows * Q; idx += kThreads) {
         const int n = idx / Q, d = (idx - n * Q) * 4;
         const float* src = &f.acc[n * Frame<R, D>::kStride + d];
-        *reinterpret_cast<float4*>(a.ws_acc + (pbase + n) * D + d) = make_float4(src[0], src[1], src[2], src[3]);
+        *reinterpret_cast<float4*>(a.ws_acc + (pbase + n) * DR + d) = make_float4(src[0], src[1], src[2], src[3]);
     }
 }
 
@@ -339,15 +339,22 @@ constexpr int kRawBufferWord3 = 0x00020000;
 // buffer resource with fixed per-lane offsets, and a missing block reads the zero slab: the
 // addresses are scalar and the loads are issued without a branch, so the loop's waits can leave
 // a prefetched pair in flight. POL is the loads' cache policy (kLoadCached or kLoadStream).
-template <int POL, int KM, int D>
+//
+// D is the operand layout (a multiple of 32) and DR the head dim of the cache rows (DR <= D, a
+// multiple of 8): with DR < D the layout's last head-dim slots are padding. K slots past DR read
+// as zeros (an offset beyond the slab, which the range check answers with zeros), so padded dims
+// add nothing to S = K Q^T whatever the slab holds; V loads there read the next token's row or
+// zeros, which only reach the padded output dims, never stored.
+template <int POL, int KM, int D, int DR = D>
 __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, const uint16_t* __restrict__ kp,
                                           const uint16_t* __restrict__ vp, int blk0, int blk1,
                                           size_t slot_stride, size_t kv_off, int r, int g) {
-    static_assert(KM != kKDma || D == kMfmaD, "the LDS-staged K tiles hold 256-byte token rows");
-    constexpr int kSlabBytes = kMfmaBS * D * 2;
+    static_assert(KM != kKDma || (D == kMfmaD && DR == D), "the LDS-staged K tiles hold 256-byte token rows");
+    constexpr int kSlabBytes = kMfmaBS * DR * 2;
     constexpr int T = D / 16;
-    const int koff = (r * D + 8 * g) * 2;        // bytes; + 64 s for head-dim slot s
-    const int voff = (4 * g * D + T * r) * 2;    // bytes; + 2 D e for token 4 g + e
+    const int koff = (r * DR + 8 * g) * 2;       // bytes; + 64 s for head-dim slot s
+    const int voff = (4 * g * DR + T * r) * 2;   // bytes; + 2 DR e for token 4 g + e
+    constexpr int kPastSlab = 1 << 28;           // any offset at or past kSlabBytes reads zeros
     __amdgpu_buffer_rsrc_t kr[2], vr[2];
 #pragma unroll
     for (int bi = 0; bi < 2; ++bi) {
@@ -374,8 +381,10 @@ __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, 
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < KVPair<D>::kSteps; ++s)
-                p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], koff, 64 * s, POL));
+            for (int s = 0; s < KVPair<D>::kSteps; ++s) {
+                const int off = (DR < D && 32 * s + 8 * g >= DR) ? kPastSlab : koff;
+                p.k[bi][s] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(kr[bi], off, 64 * s, POL));
+            }
         }
     }
     // V: T consecutive bf16 of one token row per lane (16 bytes at D = 128, 8 at 64, 12 at 96,
@@ -390,23 +399,23 @@ __device__ __forceinline__ void load_pair(KVPair<D>& p, uint4* __restrict__ kt, 
             uint32_t* w = p.v[bi][e];
 #pragma unroll
             for (int q = 0; q < kV4; q += 4) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 2 * D * e + 4 * q, POL);
+                const auto x = __builtin_amdgcn_raw_buffer_load_b128(vr[bi], voff, 2 * DR * e + 4 * q, POL);
                 w[q] = x[0];
                 w[q + 1] = x[1];
                 w[q + 2] = x[2];
                 w[q + 3] = x[3];
             }
             if constexpr (kVW - kV4 == 3) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
+                const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr[bi], voff, 2 * DR * e + 4 * kV4, POL);
                 w[kV4] = x[0];
                 w[kV4 + 1] = x[1];
                 w[kV4 + 2] = x[2];
             } else if constexpr (kVW - kV4 == 2) {
-                const auto x = __builtin_amdgcn_raw_buffer_load_b64(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
+                const auto x = __builtin_amdgcn_raw_buffer_load_b64(vr[bi], voff, 2 * DR * e + 4 * kV4, POL);
                 w[kV4] = x[0];
                 w[kV4 + 1] = x[1];
             } else if constexpr (kVW - kV4 == 1) {
-                w[kV4] = __builtin_amdgcn_raw_buffer_load_b32(vr[bi], voff, 2 * D * e + 4 * kV4, POL);
+                w[kV4] = __builtin_amdgcn_raw_buffer_load_b32(vr[bi], voff, 2 * DR * e + 4 * kV4, POL);
             }
         }
 }
@@ -792,12 +801,14 @@ __device__ __forceinline__ bool plan_item(const AttnArgs& a, const PlanLds& P, i
 //
 // mfma_item runs one work item: kv head group ug of sequence si.b (si describes this wave's kv
 // head), row group rg, blocks [blk_begin, blk_end) of nsplit; partial states (nsplit > 1) go to
-// workspace rows pb0 + h * pbstep + n for head h of the group.
-template <int NTW, int HP, int POL, int KM, int D>
+// workspace rows pb0 + h * pbstep + n for head h of the group. D is the operand layout and DR
+// the head dim of query, cache and output rows (load_pair).
+template <int NTW, int HP, int POL, int KM, int D, int DR = D>
 __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> (&frame)[HP], int* s_blk,
                                           uint4* kstA, uint4* kstB, uint4* sq, const SeqInfo& si, int ug, int rg,
                                           int blk_begin, int blk_end, int nsplit, size_t pb0, size_t pbstep) {
-    static_assert(D % 32 == 0 && D <= kMaxHeadDim, "the bf16 MFMA kernel takes head dims that are multiples of 32");
+    static_assert(D % 32 == 0 && D <= kMaxHeadDim, "the bf16 MFMA kernel's operand layout is a multiple of 32");
+    static_assert(DR % 8 == 0 && DR <= D && DR > D - 32, "cache rows fill the layout's last 32-dim step in part");
     constexpr int RW = NTW * 16;      // rows of one wave (one tile group)
     constexpr int KS = D / 32;        // head-dim steps of S^T = K Q^T
     constexpr int T = D / 16;         // d-tiles of O^T (lane row r <-> head dims T r + dt)
@@ -805,7 +816,8 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
     // More than two tiles: Q is read from LDS per tile (sq, staged once per item) and only the
     // tiles that hold rows of this unit are computed.
     constexpr bool QL = NTW > 2;
-    static_assert(!QL || (HP == 1 && KM == kKDma && D == kMfmaD), "the many-tile form needs one kv head and K in LDS");
+    static_assert(!QL || (HP == 1 && KM == kKDma && D == kMfmaD && DR == D),
+                  "the many-tile form needs one kv head and K in LDS");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform by construction
     const int hw = wave / WPH;  // this wave's kv head within the group
     const int wp = wave % WPH;  // and its place among that head's waves
@@ -817,8 +829,8 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
     const uint16_t* __restrict__ qp = reinterpret_cast<const uint16_t*>(a.q);
     const uint16_t* __restrict__ kp = reinterpret_cast<const uint16_t*>(a.k);
     const uint16_t* __restrict__ vp = reinterpret_cast<const uint16_t*>(a.v);
-    const size_t slot_stride = (size_t)kMfmaBS * D;           // one (slot, kv head) slab
-    const size_t kv_off = (size_t)si.kvh * a.bs * D;           // kv head si.kvh within a block
+    const size_t slot_stride = (size_t)kMfmaBS * DR;          // one (slot, kv head) slab
+    const size_t kv_off = (size_t)si.kvh * a.bs * DR;          // kv head si.kvh within a block
     const float c = a.scale_log2;
     // Tokens below full_vis are visible to every query row of the sequence.
     const int full_vis = a.causal ? si.ctx - si.q_len + 1 : si.ctx;
@@ -851,7 +863,9 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
                     const size_t qrow = out_row(a, si, n);
 #pragma unroll
                     for (int s = 0; s < KS; ++s)
-                        qB[nt][s] = __builtin_bit_cast(bf16x8, load16(qp + qrow * D + 32 * s + 8 * g));
+                        qB[nt][s] = __builtin_bit_cast(bf16x8, (DR < D && 32 * s + 8 * g >= DR)
+                                                                   ? make_uint4(0, 0, 0, 0)
+                                                                   : load16(qp + qrow * DR + 32 * s + 8 * g));
                 }
                 vis[nt] = a.causal ? si.ctx - si.q_len + j + 1 : si.ctx;
             } else {
@@ -1064,14 +1078,14 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
                 constexpr int P = decltype(pol)::value;
                 int j = 0, a0, a1, b0, b1;
                 pair_ids(0, a0, a1);
-                load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
+                load_pair<P, KM, D, DR>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
                 while (true) {
                     next_ids(j, b0, b1);
-                    load_pair<P, KM, D>(bufB, ktB, kp, vp, b0, b1, slot_stride, kv_off, r, g);
+                    load_pair<P, KM, D, DR>(bufB, ktB, kp, vp, b0, b1, slot_stride, kv_off, r, g);
                     compute(bufA, ktA, pb0 + j * step, a0, a1);
                     if (++j >= npairs) break;
                     next_ids(j, a0, a1);
-                    load_pair<P, KM, D>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
+                    load_pair<P, KM, D, DR>(bufA, ktA, kp, vp, a0, a1, slot_stride, kv_off, r, g);
                     compute(bufB, ktB, pb0 + j * step, b0, b1);
                     if (++j >= npairs) break;
                 }
@@ -1145,7 +1159,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
         for (int h = 0; h < HP; ++h) {  // the whole workgroup stores each head's rows
             SeqInfo sh = si;
             sh.kvh = (ug * HP + h) % a.Hkv;
-            frame_flush<RW, D>(a, sh, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH, pb0 + h * pbstep);
+            frame_flush<RW, D, DR>(a, sh, nsplit, row0, nrows > 0 ? nrows : 0, frame[h], WPH, pb0 + h * pbstep);
         }
     }
 }
@@ -1512,13 +1526,13 @@ struct FrameLds<NTW, HP, true, D> {};
 // bf16 caches. Head dims other than 128 load K straight into operand layout and take at most
 // two row tiles per wave (the LDS-staged K tiles and the many-tile form are built for 256-byte
 // token rows).
-template <int NTW, int HP, int POL, bool PLAN, int D = kMfmaD>
+template <int NTW, int HP, int POL, bool PLAN, int D = kMfmaD, int DR = D>
 __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     using Fr = Frame<NTW * 16, D>;
     constexpr bool QL = NTW > 2;
     __shared__ FrameLds<NTW, HP, QL, D> s_fr;
     __shared__ int s_blk[kMaxChunkBlocks];
-    constexpr int KM = D == kMfmaD ? kKModeFor<NTW, PLAN> : kKDirect;
+    constexpr int KM = (D == kMfmaD && DR == D) ? kKModeFor<NTW, PLAN> : kKDirect;
     // Two separate arrays, so that the compiler's wait for one tile's loads does not also wait
     // for the other's (it tells LDS DMA destinations apart by the object written). The
     // many-tile kernel keeps its merge frame in the first (the frame is used only after the
@@ -1534,7 +1548,7 @@ __global__ __launch_bounds__(kThreads) void attn_mfma_kernel(AttnArgs a) {
     Fr (&frame)[HP] = *reinterpret_cast<Fr(*)[HP]>(fp);
     mfma_schedule<NTW, HP, PLAN>(a, [&](const SeqInfo& si, int ug, int rg, int bb, int be, int ns, size_t pb0,
                                         size_t pbs) {
-        mfma_item<NTW, HP, POL, KM, D>(a, frame, s_blk, s_kstA, s_kstB, s_q, si, ug, rg, bb, be, ns, pb0, pbs);
+        mfma_item<NTW, HP, POL, KM, D, DR>(a, frame, s_blk, s_kstA, s_kstB, s_q, si, ug, rg, bb, be, ns, pb0, pbs);
     });
 }
 
@@ -1779,19 +1793,20 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------ launcher
 
 #ifdef KYRO_ATTN_HD_UNIT
-// The bf16 MFMA kernel at head dims other than 128 (64, 96 and 256 in one translation unit, 160,
-// 192 and 224 in another, so that their instances compile in parallel with the rest): at most two
-// row tiles per wave (one above 128, where the K/V pairs and accumulators fill the register
-// file), one or two kv heads per workgroup, streaming or cached K/V loads, grid or balanced
-// schedule.
-template <int D>
+// The bf16 MFMA kernel at head dims other than 128 (64, 80, 96 and 256 in one translation unit,
+// 112, 160, 192 and 224 in another, so that their instances compile in parallel with the rest):
+// at most two row tiles per wave (one above 128, where the K/V pairs and accumulators fill the
+// register file), one or two kv heads per workgroup, streaming or cached K/V loads, grid or
+// balanced schedule. D is the operand layout, DR the head dim (80 runs in the layout of 96, 112
+// in that of 128).
+template <int D, int DR = D>
 hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream) {
     const dim3 block(kThreads);
-    const int rpg = mfma_rows_per_group(a.rows_cap, true, D);
-#define KYRO_HD_LAUNCH(NT, POL, PLAN)                                                       \
-    {                                                                                       \
-        if (a.hpw == 2) attn_mfma_kernel<NT, 2, POL, PLAN, D><<<grid, block, 0, stream>>>(a); \
-        else attn_mfma_kernel<NT, 1, POL, PLAN, D><<<grid, block, 0, stream>>>(a);          \
+    const int rpg = mfma_rows_per_group(a.rows_cap, true, DR);
+#define KYRO_HD_LAUNCH(NT, POL, PLAN)                                                           \
+    {                                                                                           \
+        if (a.hpw == 2) attn_mfma_kernel<NT, 2, POL, PLAN, D, DR><<<grid, block, 0, stream>>>(a); \
+        else attn_mfma_kernel<NT, 1, POL, PLAN, D, DR><<<grid, block, 0, stream>>>(a);          \
     }
 #define KYRO_HD_POL(NT, PLAN)                                                               \
     {                                                                                       \
@@ -1815,12 +1830,12 @@ hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream
     if (a.plan) {
         constexpr long long kCombineMaxGrid = 2048;
         const long long units = (long long)a.units * ((a.rows_cap + kCombineRows - 1) / kCombineRows);
-        attn_combine_plan_kernel<D><<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0,
-                                       stream>>>(a);
+        attn_combine_plan_kernel<DR><<<dim3((unsigned)(units < kCombineMaxGrid ? units : kCombineMaxGrid)), block, 0,
+                                        stream>>>(a);
     } else if (a.splits > 1) {
-        const int rpw = kThreads / (D / 4);
+        const int rpw = kThreads / (DR / 4);
         const dim3 cgrid((unsigned)a.units, (unsigned)((a.rows_cap + rpw - 1) / rpw));
-        attn_combine_kernel<D><<<cgrid, block, 0, stream>>>(a);
+        attn_combine_kernel<DR><<<cgrid, block, 0, stream>>>(a);
     }
     return hipGetLastError();
 }
@@ -1833,6 +1848,7 @@ hipError_t launch_paged_attention_mfma_hd(const AttnArgs& a, hipStream_t stream)
     if (grid.x == 0) return hipSuccess;
     switch (a.D) {
         case 64: return launch_mfma_hd<64>(a, grid, stream);
+        case 80: return launch_mfma_hd<96, 80>(a, grid, stream);
         case 96: return launch_mfma_hd<96>(a, grid, stream);
         case 256: return launch_mfma_hd<256>(a, grid, stream);
         default: return hipErrorInvalidValue;
@@ -1843,6 +1859,7 @@ hipError_t launch_paged_attention_mfma_hd_wide(const AttnArgs& a, hipStream_t st
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     switch (a.D) {
+        case 112: return launch_mfma_hd<128, 112>(a, grid, stream);
         case 160: return launch_mfma_hd<160>(a, grid, stream);
         case 192: return launch_mfma_hd<192>(a, grid, stream);
         case 224: return launch_mfma_hd<224>(a, grid, stream);
@@ -1860,8 +1877,8 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
     const dim3 grid((unsigned)(a.plan ? a.plan_grid : a.ugroups_padded * a.splits * a.row_groups));
     if (grid.x == 0) return hipSuccess;
     if (path == ATTN_KERNEL_MFMA && a.D != kMfmaD)
-        return (a.D == 160 || a.D == 192 || a.D == 224) ? launch_paged_attention_mfma_hd_wide(a, stream)
-                                                         : launch_paged_attention_mfma_hd(a, stream);
+        return (a.D == 112 || a.D == 160 || a.D == 192 || a.D == 224) ? launch_paged_attention_mfma_hd_wide(a, stream)
+                                                                       : launch_paged_attention_mfma_hd(a, stream);
     if (path == ATTN_KERNEL_MFMA) {
         const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
         const bool rows16 = rpg == 16;

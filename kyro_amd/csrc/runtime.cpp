@@ -211,7 +211,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     if (p->path == KYRO_ATTN_MFMA) {
         if (!mfma_ok)
             return fail(KYRO_EUNSUPPORTED, "paged_attention: the MFMA kernel needs a block_size that is a multiple of "
-                        "16 and head_dim 128 (bf16 caches: a multiple of 32 from 64 to 256); got block_size %d, head_dim %d",
+                        "16 and head_dim 128 (bf16 caches: 80, 112 or a multiple of 32 from 64 to 256); got block_size %d, "
+                        "head_dim %d",
                         p->block_size, p->head_dim);
         kernel = kyro::ATTN_KERNEL_MFMA;
     } else if (p->path == KYRO_ATTN_VECTOR) {
@@ -224,7 +225,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     }
     if (p->schedule == KYRO_ATTN_SCHEDULE_BALANCED && kernel != kyro::ATTN_KERNEL_MFMA)
         return fail(KYRO_EUNSUPPORTED, "paged_attention: the balanced schedule runs on the MFMA kernel "
-                    "(block_size a multiple of 16; head_dim 128, or a multiple of 32 from 64 to 256 with bf16 caches)");
+                    "(block_size a multiple of 16; head_dim 128, or 80, 112 or a multiple of 32 from 64 to 256 with "
+                    "bf16 caches)");
 
     kyro::AttnArgs& a = s.a;
     a.B = p->batch_size;
