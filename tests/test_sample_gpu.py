@@ -54,6 +54,30 @@ def test_matches_oracle(gpu, V, mode):
     run_both(x, T, u, gpu, **kw)
 
 
+@pytest.mark.parametrize("V", [8, 2052, 4096, 6148, 128256, 1000004])
+def test_plain_and_greedy_rows_mixed(gpu, V):
+    """Greedy and sampled rows mixed in one batch without processors, top-k or top-p, from one
+    short chunk to 245 chunks, with a short last chunk (2052, 6148), a row of -inf but one entry,
+    and a row of -inf (the last index when sampled, index 0 at T 0), u = 0 and u just below 1,
+    against the oracle."""
+    rng = np.random.default_rng(V + 3)
+    B = 20
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    x[4, :] = -np.inf
+    x[4, V // 3] = 1.0
+    x[5, :] = -np.inf
+    x[6, :] = -np.inf
+    T = np.where(np.arange(B) % 3 == 0, 0.0, 0.8).astype(np.float32)
+    T[5] = 1.0
+    T[6] = 0.0
+    T[7] = 1.7
+    u = rng.random(B).astype(np.float32)
+    u[8] = 0.0
+    u[9] = np.float32(1.0 - 2 ** -24)
+    got = run_both(x, T, u, gpu)
+    assert got[4] == V // 3 and got[5] == V - 1 and got[6] == 0
+
+
 def test_ties_follow_the_index(gpu):
     """Small integer logits: many equal values, so top-k boundaries and the descending order
     depend on the tie rule (lower index first)."""
