@@ -715,12 +715,11 @@ int kyro_spec_verify_describe(const kyro_spec_verify_params* p, char* buf, size_
         const std::string first = tail ? "window of " + std::to_string(a.win) + " of " + std::to_string(a.kmax) +
                                              " draft positions"
                                        : "every row in the first pass";
-        const std::string tail_k =
-            tail ? ", spec_stats_tail_kernel on " + std::to_string(a.tail_wgs) + " workgroups" : "";
-        std::snprintf(t, sizeof t,
-                      "%s; chunks of %d entries, %d per row; spec_stats_kernel, spec_decide_kernel%s, "
-                      "spec_resample_kernel, spec_pick_kernel",
-                      first.c_str(), a.chunk, a.C, tail_k.c_str());
+        const std::string mid = tail ? "spec_decide_kernel, spec_stats_tail_kernel on " + std::to_string(a.tail_wgs) +
+                                           " workgroups, spec_resample_kernel"
+                                     : "spec_resample_kernel with the acceptance scan";
+        std::snprintf(t, sizeof t, "%s; chunks of %d entries, %d per row; spec_stats_kernel, %s, spec_pick_kernel",
+                      first.c_str(), a.chunk, a.C, mid.c_str());
         return put_text(t, buf, len, needed);
     });
 }

@@ -378,7 +378,7 @@ __device__ void accept_sequence(const SpecArgs& a, int b, int avail, bool writer
                 float bs = 0.f;
 #pragma unroll
                 for (int i = 0; i < kChunkGroup; ++i)
-                    if (y[i].x != kNegInf) bs += y[i].y * fast_exp2((y[i].x - bm) * c2);
+                    if (y[i].x != kNegInf) bs = __builtin_fmaf(y[i].y, fast_exp2((y[i].x - bm) * c2), bs);
                 const float2 f = fold_stats(make_float2(m, z), make_float2(bm, bs), c2);
                 m = f.x;
                 z = f.y;
@@ -823,16 +823,23 @@ __global__ __launch_bounds__(kT) void spec_stats_tail_kernel(SpecArgs a) {
 // Residual (and p) mass of one chunk of the row to resample. The plan comes from the window's
 // scan; a sequence that was pending repeats the scan over all its rows here (wave 0, in every
 // chunk workgroup; the chunk-0 workgroup stores the outputs).
-template <bool VEC>
+// EAGER: every row was read by the statistics pass and no decide pass ran; every workgroup runs
+// the whole acceptance scan itself (one round of loads, as the decide pass would), the chunk-0
+// one stores the outputs and the plan in plan[b], which no other workgroup of this launch reads.
+template <bool VEC, bool EAGER>
 __global__ __launch_bounds__(kT) void spec_resample_kernel(SpecArgs a) {
     __shared__ AcceptShared acc;
     __shared__ float sh[4];
     const int c = blockIdx.x % a.C, b = blockIdx.x / a.C;
     if (threadIdx.x < 64) {
-        const SpecPlan pl = a.plan[b];
-        // plan[b] is only read here; the full scan's plan goes to plan_tail.
-        if (pl.mode == SPEC_PENDING) accept_sequence(a, b, a.kmax + 1, c == 0, a.plan_tail, acc);
-        else if (threadIdx.x == 0) acc.plan = pl;
+        if constexpr (EAGER) {
+            accept_sequence(a, b, a.kmax + 1, c == 0, a.plan, acc);
+        } else {
+            const SpecPlan pl = a.plan[b];
+            // plan[b] is only read here; the full scan's plan goes to plan_tail.
+            if (pl.mode == SPEC_PENDING) accept_sequence(a, b, a.kmax + 1, c == 0, a.plan_tail, acc);
+            else if (threadIdx.x == 0) acc.plan = pl;
+        }
     }
     __syncthreads();
     const SpecPlan pl = acc.plan;
@@ -897,20 +904,23 @@ hipError_t launch_spec_verify(const SpecArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
     // Window rows: target rows 0 .. min(win, kmax + 1) - 1, draft rows 0 .. min(win, kmax) - 1.
     const dim3 wgrid(a.C * a.B, min(a.win, a.kmax + 1) + min(a.win, a.kmax));
-    const bool tail = a.kmax >= a.win;  // otherwise every sequence is decided by the window
-    if (a.vec4) {
-        spec_stats_kernel<true><<<wgrid, kT, 0, stream>>>(a);
-        spec_decide_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
-        if (tail) spec_stats_tail_kernel<true><<<dim3(a.tail_wgs), kT, 0, stream>>>(a);
-        spec_resample_kernel<true><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
-        spec_pick_kernel<true><<<dim3(a.B), kT, 0, stream>>>(a);
-    } else {
-        spec_stats_kernel<false><<<wgrid, kT, 0, stream>>>(a);
-        spec_decide_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
-        if (tail) spec_stats_tail_kernel<false><<<dim3(a.tail_wgs), kT, 0, stream>>>(a);
-        spec_resample_kernel<false><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
-        spec_pick_kernel<false><<<dim3(a.B), kT, 0, stream>>>(a);
-    }
+    // Every row in the first pass (the window covers the drafts and the bonus row): no decide
+    // pass; the resample pass runs the acceptance scan in each workgroup (four launches to three).
+    const bool eager = a.win > a.kmax;
+    auto run = [&](auto vec) {
+        constexpr bool V4 = decltype(vec)::value;
+        spec_stats_kernel<V4><<<wgrid, kT, 0, stream>>>(a);
+        if (eager) {
+            spec_resample_kernel<V4, true><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
+        } else {
+            spec_decide_kernel<<<dim3(a.B), 64, 0, stream>>>(a);
+            spec_stats_tail_kernel<V4><<<dim3(a.tail_wgs), kT, 0, stream>>>(a);
+            spec_resample_kernel<V4, false><<<dim3(a.C * a.B), kT, 0, stream>>>(a);
+        }
+        spec_pick_kernel<V4><<<dim3(a.B), kT, 0, stream>>>(a);
+    };
+    if (a.vec4) run(std::true_type{});
+    else run(std::false_type{});
     return hipGetLastError();
 }
 

@@ -97,6 +97,24 @@ def test_window_does_not_change_outputs(gpu, window):
     assert torch.equal(torch.nan_to_num(res.p_draft, -1.0), torch.nan_to_num(ref.p_draft, -1.0))
 
 
+@pytest.mark.parametrize("vocab", [4096, 5000, 20000, 32768])
+def test_eager_passes_match_the_lazy_passes(gpu, vocab):
+    """Every row read at once (window 64: statistics, then resample with the acceptance scan in
+    every workgroup, then the draw) against the lazy windows (statistics of the window, decide,
+    tail, resample, draw): one chunk, a partial second chunk, five and eight chunks; greedy and
+    sampled sequences with 0 to 8 drafts: the outputs are the same bits, and the oracle's."""
+    k = wl.rng(vocab, wl.S_KSEQ).integers(0, 9, size=24)
+    case = wl.verify_mixed(k, vocab=vocab, seed=vocab)
+    t = h.verify_tensors(case, gpu)
+    eager = kyro_amd.verify_drafts(**t, return_probs=True, window=64)
+    h.assert_verify_parity(eager, case, h.oracle_verify(case), max_exempt=1)
+    for window in (1, 3):
+        lazy = kyro_amd.verify_drafts(**t, return_probs=True, window=window)
+        assert torch.equal(eager.accepted, lazy.accepted) and torch.equal(eager.tokens, lazy.tokens)
+        assert torch.equal(torch.nan_to_num(eager.p_draft, -1.0), torch.nan_to_num(lazy.p_draft, -1.0))
+        assert torch.equal(torch.nan_to_num(eager.q_draft, -1.0), torch.nan_to_num(lazy.q_draft, -1.0))
+
+
 def test_tail_pass_with_more_items_than_the_default_grid_holds(gpu):
     """600 sequences that accept every draft (draft logits equal the target's): after a window of
     1 there are 600 x 29 rows x 8 chunks = 139,200 tail items, more than 2048 workgroups x 64 items,
