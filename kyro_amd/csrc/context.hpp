@@ -23,6 +23,8 @@ struct kyro_ctx_s {
     int* err = nullptr;     // device error word
     int* sched = nullptr;   // kyro::kSchedWords device counters of the balanced attention schedule
                             // (zero between launches: the last workgroup of a launch resets them)
+    int* row_cnt = nullptr; // kyro::kSampleRowCounters per-row counters of the one-launch decode
+                            // pass (zero between launches, reset by each row's last workgroup)
     // Host staging for small uploads (hipHostMalloc): kStageSlots slots used in turn, each with
     // an event recorded after the copies out of it.
     void* pinned = nullptr;

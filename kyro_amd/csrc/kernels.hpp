@@ -292,7 +292,27 @@ struct SampleArgs {
     int* err;
     int B, V, num_masks, mask_words;
     int vec4;                   // rows (logits and workspace) are 16-byte aligned
+    // Rows without processors, top-k or top-p: workgroups per row of the one-launch pass (0: the
+    // chunked passes), its per-segment statistics [B, ceil(V / 2048)] and the per-row counters
+    // (zero between launches).
+    int row_wgs;
+    float2* segs;
+    int* row_cnt;
 };
+
+// Rows per launch the one-launch decode pass counts with the context's counters.
+constexpr int kSampleRowCounters = 16384;
+// The one-launch decode pass: entries per segment (one wave reduces a segment), segments per
+// workgroup (one per wave of its 1024 threads) and workgroups per row at most.
+#ifndef KYRO_SAMPLE_SEG
+#define KYRO_SAMPLE_SEG 2048
+#endif
+#ifndef KYRO_SAMPLE_ROW_WGS
+#define KYRO_SAMPLE_ROW_WGS 8
+#endif
+constexpr int kSampleSeg = KYRO_SAMPLE_SEG;
+constexpr int kSampleSegsPerWg = 16;
+constexpr int kSampleRowWgsMax = KYRO_SAMPLE_ROW_WGS;
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
 

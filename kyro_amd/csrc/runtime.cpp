@@ -474,6 +474,8 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         if (e == hipSuccess) e = hipMemset(ctx->err, 0, sizeof(int));
         if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->sched), kyro::kSchedWords * sizeof(int));
         if (e == hipSuccess) e = hipMemset(ctx->sched, 0, kyro::kSchedWords * sizeof(int));
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->row_cnt), kyro::kSampleRowCounters * sizeof(int));
+        if (e == hipSuccess) e = hipMemset(ctx->row_cnt, 0, kyro::kSampleRowCounters * sizeof(int));
         if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, device);
         if (e == hipSuccess && ctx->num_cus <= 0) e = hipErrorInvalidDevice;
         // Set-up of kyro_spec_verify_noalloc: the static scratch array's address on this device.
@@ -487,6 +489,7 @@ int kyro_ctx_create(int device, kyro_ctx* out) {
         if (e != hipSuccess) {
             if (ctx->err) (void)hipFree(ctx->err);
             if (ctx->sched) (void)hipFree(ctx->sched);
+            if (ctx->row_cnt) (void)hipFree(ctx->row_cnt);
             if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
             delete ctx;
             return fail(KYRO_EHIP, "kyro_ctx_create: %s", hipGetErrorString(e));
@@ -506,6 +509,7 @@ int kyro_ctx_destroy(kyro_ctx ctx) {
         if (ctx->arena) (void)hipFree(ctx->arena);
         if (ctx->err) (void)hipFree(ctx->err);
         if (ctx->sched) (void)hipFree(ctx->sched);
+        if (ctx->row_cnt) (void)hipFree(ctx->row_cnt);
         for (hipEvent_t& e : ctx->pinned_done)
             if (e) (void)hipEventSynchronize(e);
         if (ctx->pinned) (void)hipHostFree(ctx->pinned);

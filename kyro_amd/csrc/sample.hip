@@ -1426,10 +1426,223 @@ __global__ __launch_bounds__(kRT) void sample_select_kernel(SampleArgs a) {
     finish_row(a, b, sh, covered ? n : -1, M, Z, kmin, T, k, tp, u, cp_bits, cp);
 }
 
+// ------------------------------------------------------- plain and greedy rows in one launch
+//
+// A batch without processors, top-k or top-p needs only each row's first maximum (T <= 0) or its
+// softmax normaliser and one inverse-CDF walk, so one launch settles it. S = a.row_wgs
+// workgroups of 1024 threads share a row (one workgroup alone streams at ~54 GB/s when 64 stream
+// at once, so a row of 128256 entries takes four to put every CU to work). Wave w of a
+// workgroup reduces segments of kSeg entries (eight 16-byte loads a lane, the next segment's
+// issued before the current one is reduced) to {max z, sum exp(z - max)} or {max y, first
+// index}. The segment statistics are published with device-scope stores and counted on the
+// row's counter (a.row_cnt, zero between launches); the workgroup that counts last reads them
+// all back with device-scope loads, combines them, finds the segment where the running mass in
+// index order reaches u Z, walks it, and resets the counter. No workgroup waits for another:
+// the others exit after counting. Masses are grouped by segment instead of by chunk, so a token
+// can differ from the chunked passes' only where rounding decides the walk.
+constexpr int kSeg = kSampleSeg;          // entries per segment
+constexpr int kSegVec = kSeg / (4 * 64);  // 16-byte loads per lane per segment
+constexpr int kRawWord3 = 0x00020000;     // raw buffer resource, 32-bit format, no swizzle
+
+struct PlainShared {
+    float fred[kRW];
+    int ired[kRW];
+    int last;
+    int found;
+    float rem;
+};
+
+__device__ __forceinline__ void store_coherent(float2* p, float2 v) {
+    __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), __builtin_bit_cast(unsigned long long, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent(const float2* p) {
+    return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__global__ __launch_bounds__(kRT) void sample_plain_kernel(SampleArgs a) {
+    __shared__ PlainShared sh;
+    const int b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the segment loop is scalar
+    const int S = a.row_wgs;
+    const float T = a.temperature[b];
+    const float u = a.u[b];
+    const float* y = a.logits + (size_t)b * a.V;
+    const int n4 = a.V >> 2;  // the row is 16-byte aligned and V a multiple of 4
+    const int nseg = (a.V + kSeg - 1) / kSeg;
+    const int spw = (nseg + S - 1) / S;  // segments of each workgroup
+    const int s0 = (int)blockIdx.x * spw, s1 = min(nseg, s0 + spw);
+    const bool greedy = !(T > 0.f);
+    const float sc = greedy ? 0.f : (float)(1.0 / (double)T);
+    const float ninf = -__builtin_huge_valf();
+    float2* segs = a.segs + (size_t)b * nseg;
+    // Segment sg's loads for this lane: vectors sg kSeg / 4 + lane + 64 i, through a resource that
+    // starts at the segment and ends at the row's end (scalar base and size, fixed lane offsets:
+    // no vector address arithmetic between loads); past the row the loads read zeros, which the
+    // reduction drops. An index past the workgroup's segments reads nothing.
+    auto load_seg = [&](int sg, float4 (&x)[kSegVec]) {
+        const int v0 = min(min(sg, s1) * kSeg, a.V);
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(y + v0), (short)0, sg < s1 ? (a.V - v0) * 4 : 0, kRawWord3);
+#pragma unroll
+        for (int i = 0; i < kSegVec; ++i)
+            x[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16 + 1024 * i, 0, 0));
+    };
+    auto reduce_seg = [&](int sg, const float4 (&x)[kSegVec]) {
+        const int f0 = sg * (kSeg / 4) + lane;
+        float2 st;
+        if (greedy) {  // first maximum of y: a lane's entries ascend in index
+            float bv = ninf;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < kSegVec; ++i) {
+                const int f = f0 + 64 * i;
+                const float e[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (f < n4 && e[j] > bv) {
+                        bv = e[j];
+                        bi = 4 * f + j;
+                    }
+            }
+            wave_argmax(bv, bi);
+            st = make_float2(bv, __int_as_float(bi));
+        } else {
+            float m = ninf;
+#pragma unroll
+            for (int i = 0; i < kSegVec; ++i) {
+                if (f0 + 64 * i < n4)
+                    m = fmaxf(fmaxf(m, fmaxf(x[i].x * sc + 0.0f, x[i].y * sc + 0.0f)),
+                              fmaxf(x[i].z * sc + 0.0f, x[i].w * sc + 0.0f));
+            }
+            m = wave_max(m);
+            float sum = 0.f;
+            if (m != ninf) {
+#pragma unroll
+                for (int i = 0; i < kSegVec; ++i) {
+                    if (f0 + 64 * i < n4) {
+                        sum += fast_exp2((x[i].x * sc + 0.0f - m) * kLog2e);
+                        sum += fast_exp2((x[i].y * sc + 0.0f - m) * kLog2e);
+                        sum += fast_exp2((x[i].z * sc + 0.0f - m) * kLog2e);
+                        sum += fast_exp2((x[i].w * sc + 0.0f - m) * kLog2e);
+                    }
+                }
+            }
+            st = make_float2(m, wave_sum(sum));
+        }
+        if (lane == 0) store_coherent(segs + sg, st);
+    };
+    if (s0 + wave < s1) {
+        float4 xa[kSegVec], xb[kSegVec];
+        int sg = s0 + wave;
+        load_seg(sg, xa);
+        while (true) {
+            load_seg(sg + kRW, xb);
+            reduce_seg(sg, xa);
+            sg += kRW;
+            if (sg >= s1) break;
+            load_seg(sg + kRW, xa);
+            reduce_seg(sg, xb);
+            sg += kRW;
+            if (sg >= s1) break;
+        }
+    }
+    if (S > 1) {
+        // Every wave's stores have reached the device-coherent level before the workgroup counts
+        // itself; the last to count sees every other workgroup's stores.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) sh.last = atomicAdd(&a.row_cnt[b], 1) == S - 1;
+        __syncthreads();
+        if (!sh.last) return;
+        if (tid == 0) __hip_atomic_store(&a.row_cnt[b], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+    // The last workgroup: thread t holds segment t (nseg <= kRT).
+    const float2 st = tid < nseg ? load_coherent(segs + tid) : make_float2(ninf, __int_as_float(0x7fffffff));
+    if (greedy) {
+        float bv = st.x;
+        int bi = __float_as_int(st.y);
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+            sh.fred[wave] = bv;
+            sh.ired[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            bv = sh.fred[0];
+            bi = sh.ired[0];
+            for (int w = 1; w < kRW; ++w)
+                if (sh.fred[w] > bv || (sh.fred[w] == bv && sh.ired[w] < bi)) {
+                    bv = sh.fred[w];
+                    bi = sh.ired[w];
+                }
+            a.out[b] = (uint32_t)(bi == 0x7fffffff ? 0 : bi);
+        }
+        return;
+    }
+    float M = wave_max(st.x);
+    if (lane == 0) sh.fred[wave] = M;
+    __syncthreads();
+    M = sh.fred[0];
+    for (int w = 1; w < kRW; ++w) M = fmaxf(M, sh.fred[w]);
+    __syncthreads();
+    if (M == ninf) {  // no finite logit
+        if (tid == 0) a.out[b] = (uint32_t)(a.V - 1);
+        return;
+    }
+    // Segment masses exp(z - M) in index order; a block scan gives Z and the crossing segment.
+    const float w = (tid < nseg && st.x != ninf) ? st.y * fast_exp2((st.x - M) * kLog2e) : 0.f;
+    const float winc = wave_incl_scan_f(w);
+    if (lane == 63) sh.fred[wave] = winc;
+    if (tid == 0) sh.found = 0x7fffffff;
+    __syncthreads();
+    float cbase = 0.f, Z = 0.f;
+    for (int q = 0; q < kRW; ++q) {
+        if (q < wave) cbase += sh.fred[q];
+        Z += sh.fred[q];
+    }
+    const float cum = cbase + winc;  // running mass through segment tid
+    const float rr = u * Z;
+    if (tid < nseg && cum >= rr && (tid == 0 || cum - w < rr)) atomicMin(&sh.found, tid);
+    __syncthreads();
+    const int cs = sh.found == 0x7fffffff ? nseg - 1 : sh.found;
+    if (tid == cs) sh.rem = rr - (cum - w);  // r less the mass before the crossing segment
+    __syncthreads();
+    const float rem = sh.rem;
+    if (tid == 0) sh.found = 0x7fffffff;
+    // Walk segment cs in index order: thread t owns the 2 consecutive entries 2t, 2t + 1.
+    const int v0 = cs * kSeg, v1 = min(a.V, v0 + kSeg);
+    const int v = v0 + 2 * tid;
+    const float2 q = v < v1 ? *reinterpret_cast<const float2*>(y + v) : make_float2(0.f, 0.f);
+    const float e0 = v < v1 ? fast_exp2((q.x * sc + 0.0f - M) * kLog2e) : 0.f;
+    const float e1 = v < v1 ? fast_exp2((q.y * sc + 0.0f - M) * kLog2e) : 0.f;
+    const float mine = e0 + e1;
+    const float inc = wave_incl_scan_f(mine);
+    if (lane == 63) sh.fred[wave] = inc;
+    __syncthreads();
+    float base = inc - mine;
+    for (int q2 = 0; q2 < wave; ++q2) base += sh.fred[q2];
+    if (v < v1 && base < rem && base + mine >= rem) {  // this thread's two hold the crossing
+        atomicMin(&sh.found, base + e0 >= rem ? v : v + 1);  // rounding can make two threads claim it
+    } else if (tid == 0 && rem <= 0.f) {
+        atomicMin(&sh.found, v0);
+    }
+    __syncthreads();
+    if (tid == 0) a.out[b] = (uint32_t)(sh.found != 0x7fffffff ? sh.found : a.V - 1);
+}
+
 }  // namespace
 
 hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
     if (a.B == 0) return hipSuccess;
+    if (a.row_wgs > 0) {  // no processor, top-k or top-p: one launch
+        sample_plain_kernel<<<dim3((unsigned)a.row_wgs, (unsigned)a.B), kRT, 0, stream>>>(a);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)a.C, (unsigned)a.B);
     if (a.bias_off || a.pen_off || a.mask_row) sample_prepare_kernel<<<grid, kCT, 0, stream>>>(a);
     sample_stats_kernel<<<grid, kCT, 0, stream>>>(a);

@@ -58,7 +58,16 @@ int kyro_sample_tokens(kyro_ctx ctx, const kyro_sample_params* p, const float* l
         // Arena: processed rows (when a processor is given), chunk statistics, and for top-k /
         // top-p the chunks' thresholds, counts and candidate lists.
         const bool filtered = top_p || top_k;
-        const size_t ws_b = (bias_offsets || penalty_offsets || mask_row) ? align_up((size_t)a.B * a.V * sizeof(float), 256) : 0;
+        const bool processed = bias_offsets || penalty_offsets || mask_row;
+        // Rows without processors, top-k or top-p take the one-launch pass: segments of
+        // kSampleSeg entries, kSampleSegsPerWg per workgroup (one a wave) while the row allows,
+        // at most kSampleRowWgsMax workgroups a row.
+        const int nseg = (a.V + kyro::kSampleSeg - 1) / kyro::kSampleSeg;
+        if (!filtered && !processed && a.vec4 && a.B <= kyro::kSampleRowCounters && nseg <= 1024)
+            a.row_wgs = std::min(kyro::kSampleRowWgsMax,
+                                 std::max(1, (nseg + kyro::kSampleSegsPerWg - 1) / kyro::kSampleSegsPerWg));
+        const size_t seg_b = a.row_wgs ? align_up((size_t)a.B * nseg * sizeof(float2), 256) : 0;
+        const size_t ws_b = processed ? align_up((size_t)a.B * a.V * sizeof(float), 256) : 0;
         const size_t cstat_b = align_up((size_t)a.B * a.C * sizeof(float2), 256);
         const size_t thr_b = filtered ? align_up((size_t)a.B * a.C * sizeof(float), 256) : 0;
         const size_t cnt_b = filtered ? align_up((size_t)a.B * a.C * sizeof(int), 256) : 0;
@@ -70,7 +79,7 @@ int kyro_sample_tokens(kyro_ctx ctx, const kyro_sample_params* p, const float* l
             return fail(KYRO_EUNSUPPORTED, "sample_tokens: %d chunks leave too few copy threads", a.C);
         DeviceGuard dg(ctx->device);
         KYRO_HIP(dg.status);
-        if (int rc = ensure_arena(ctx, ws_b + cstat_b + thr_b + cnt_b + cand_b)) return rc;
+        if (int rc = ensure_arena(ctx, ws_b + cstat_b + thr_b + cnt_b + cand_b + seg_b)) return rc;
         char* base = static_cast<char*>(ctx->arena);
         a.ws = ws_b ? reinterpret_cast<float*>(base) : nullptr;
         base += ws_b;
@@ -81,6 +90,9 @@ int kyro_sample_tokens(kyro_ctx ctx, const kyro_sample_params* p, const float* l
         a.ccount = cnt_b ? reinterpret_cast<int*>(base) : nullptr;
         base += cnt_b;
         a.cand = cand_b ? reinterpret_cast<unsigned long long*>(base) : nullptr;
+        base += cand_b;
+        a.segs = seg_b ? reinterpret_cast<float2*>(base) : nullptr;
+        a.row_cnt = ctx->row_cnt;
         a.err = ctx->err;
         KYRO_HIP(kyro::launch_sample(a, ctx->stream));
         return KYRO_OK;

@@ -78,6 +78,21 @@ def test_plain_and_greedy_rows_mixed(gpu, V):
     assert got[4] == V // 3 and got[5] == V - 1 and got[6] == 0
 
 
+def test_one_launch_rows_repeat_and_change_shape(gpu):
+    """Batches without processors, top-k or top-p run in one launch whose workgroups count
+    themselves on per-row counters that the last one resets: calls back to back give the same
+    tokens, and batches of other sizes and vocabularies (4, 1 and 8 workgroups a row) that
+    follow them still match the oracle."""
+    rng = np.random.default_rng(23)
+    for B, V in ((64, 128256), (64, 128256), (3, 128256), (40, 32000), (17, 300004), (64, 128256)):
+        x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+        T = np.where(np.arange(B) % 4 == 0, 0.0, 0.8).astype(np.float32)
+        u = rng.random(B).astype(np.float32)
+        got = run_both(x, T, u, gpu)
+        again = kyro_amd.sample_tokens(torch.from_numpy(x).to(gpu), T, u).cpu().numpy().astype(np.uint32)
+        assert np.array_equal(got, again)
+
+
 def test_ties_follow_the_index(gpu):
     """Small integer logits: many equal values, so top-k boundaries and the descending order
     depend on the tie rule (lower index first)."""
