@@ -17,7 +17,10 @@
 //               after top-p, the least probable kept token after top-k alone, the last index
 //               otherwise (worker.rs:340-360).
 //
-// The row is split into 4096-entry chunks so that a batch of a few rows still fills the chip:
+// A batch with no processor, top-k or top-p takes one launch, sample_plain_kernel (below: a few
+// workgroups a row, the last to finish combining the row's segment statistics and walking it).
+// Otherwise the row is split into 4096-entry chunks so that a batch of a few rows still fills
+// the chip:
 //   sample_prepare_kernel  (rows with a processor; grid chunk x row) copies the row into the
 //                          workspace with the mask, then the bias, then the penalty applied.
 //   sample_stats_kernel    (grid chunk x row) per chunk: {max z, sum exp(z - max z)}, or the first
