@@ -360,8 +360,8 @@ def ngram_draft_workload(warmup, steps):
     print(json.dumps({"workload": "ngram-draft", "corpus_tokens": int(sum(c.size for c in corpus)),
                       "table_entries": len(table), "host_build_ms": build_s * 1e3, "draft_us": us,
                       "mean_drafts": float(nd.float().mean().item()),
-                      "roofline": {"bound": "latency", "note": "one lane per sequence, 7 dependent "
-                                   "table probes of a few bytes each"},
+                      "roofline": {"bound": "latency", "note": "one wave per sequence, 7 dependent "
+                                   "lookups of one round of loads each (64 probe slots at once)"},
                       "cpu_baseline": {"value": sec * 1e6, "unit": "us per batch", "cores": 1,
                                        "kind": "port", "sample": "the same 64 contexts, Python dict "
                                        "table of the oracle"}}), flush=True)
