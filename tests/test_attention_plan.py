@@ -63,9 +63,9 @@ def test_slot_bound_holds_over_random_batches(chunk_quarters, num_cus):
         worst = max(worst, info["items"] / info["slot_bound"])
         # Items are sequence x kv head group x split x row group, with the row groups of the
         # launch's row-group size (16, 32 or 64 rows per group for the bf16 MFMA kernels; the
-        # 64-row kernel takes one kv head per workgroup).
+        # 64-row kernel, and the 16-row one under MHA, take one kv head per workgroup).
         rw = _rows_per_group(group * max(1, int(ql.max())))
-        hp = 2 if hkv % 2 == 0 and rw <= 32 else 1
+        hp = 2 if hkv % 2 == 0 and rw <= 32 and not (rw <= 16 and group == 1) else 1
         r = _ceil(ql.astype(np.int64) * group, rw)
         assert info["items"] == int(np.sum((hkv // hp) * splits.astype(np.int64) * r))
         # Splits: one for a sequence within the chunk; otherwise chunks of C blocks from the start,
@@ -90,12 +90,12 @@ def test_a_uniform_batch_keeps_one_item_per_kv_head_group():
 
 
 def test_a_bound_for_another_chunk_length_is_exceeded():
-    """The Llama-2-7B batch (MHA 32/32, B 16, ctx 512-2048, 5 rows) planned with chunks of L/2
-    needs more slots than a bound derived for the library's 3L/2 allows: the check above has the
-    power to catch a plan/bound mismatch (one once wrote past the workspace), and the shared chunk
-    constant keeps them consistent."""
+    """The Llama-2-7B batch's context lengths (B 16, ctx 512-2048, 5 rows) under GQA 32/8, planned
+    with chunks of L/2, need more slots than a bound derived for the library's 3L/2 allows: the
+    check above has the power to catch a plan/bound mismatch (one once wrote past the workspace),
+    and the shared chunk constant keeps them consistent."""
     ctx = wl.rng(0, wl.S_CTX).integers(512, 2049, size=16)
-    attn = PagedAttention(16, 32, 128, 32)
+    attn = PagedAttention(16, 32, 128, 8)
     half, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128, chunk_quarters=2)
     lib, _ = attention_plan(attn, ctx, [5] * 16, max_blocks_per_seq=128)
     assert lib["items"] <= lib["slot_bound"]
