@@ -256,12 +256,13 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
     // waves per head): the workgroup then reads both heads' slabs of each block together, and
     // the Llama-3-8B step fits the chip in one round of workgroups. The 64-row kernel takes one
-    // kv head per workgroup (its four waves and its LDS are that head's), and so does the bf16
+    // kv head per workgroup (its four waves and its LDS are that head's), and so does the
     // one-tile kernel under MHA (one query head per kv head): twice the workgroups, two a CU,
     // each streaming half the bytes, which evens out ragged context lengths (MHA Llama-2-7B
-    // batch, ctx 512-2048: 61.7 -> 57.3 us; uniform MHA shapes 0.5-1.5% faster). GQA batches
-    // keep head pairs (ragged GQA 32/8 decode measured 107 -> 111 us with one head).
-    const bool one_head = rows_per_group <= 16 && group == 1 && p->dtype == KYRO_BF16;
+    // batch, ctx 512-2048: bf16 61.7 -> 57.3 us, f32 131.5 -> 121.7 us; uniform MHA shapes
+    // 0.5-1.5% faster in bf16, 2-2.5% slower in f32). GQA batches keep head pairs (ragged GQA
+    // 32/8 decode measured 107 -> 111 us with one head).
+    const bool one_head = rows_per_group <= 16 && group == 1;
     a.hpw = (kernel == kyro::ATTN_KERNEL_MFMA && p->num_kv_heads % 2 == 0 && rows_per_group <= 32 && !one_head)
                 ? 2 : 1;
     a.ugroups = a.units / a.hpw;
