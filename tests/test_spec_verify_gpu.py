@@ -97,12 +97,13 @@ def test_window_does_not_change_outputs(gpu, window):
     assert torch.equal(torch.nan_to_num(res.p_draft, -1.0), torch.nan_to_num(ref.p_draft, -1.0))
 
 
-@pytest.mark.parametrize("vocab", [4096, 5000, 20000, 32768])
+@pytest.mark.parametrize("vocab", [4096, 4097, 5000, 20000, 32768, 50000])
 def test_eager_passes_match_the_lazy_passes(gpu, vocab):
     """Every row read at once (window 64: statistics, then resample with the acceptance scan in
     every workgroup, then the draw) against the lazy windows (statistics of the window, decide,
-    tail, resample, draw): one chunk, a partial second chunk, five and eight chunks; greedy and
-    sampled sequences with 0 to 8 drafts: the outputs are the same bits, and the oracle's."""
+    tail, resample, draw): one chunk, a partial second chunk (4097 also takes the scalar-load
+    path), five, eight and thirteen chunks; greedy and sampled sequences with 0 to 8 drafts:
+    the outputs are the same bits, and the oracle's."""
     k = wl.rng(vocab, wl.S_KSEQ).integers(0, 9, size=24)
     case = wl.verify_mixed(k, vocab=vocab, seed=vocab)
     t = h.verify_tensors(case, gpu)
