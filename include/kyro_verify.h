@@ -216,7 +216,7 @@ int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_param
  * query rows (q_lens NULL: one row each). For analysis and tests; no counterpart in the
  * reference. num_cus 0 means 256; chunk_quarters 0 means the library's chunk length (a sequence
  * longer than the per-workgroup share L of the work splits into chunks of about
- * L x chunk_quarters / 4 blocks, 3L/2 by default; other values model other chunk lengths, the
+ * L x chunk_quarters / 4 blocks, 5L/4 by default; other values model other chunk lengths, the
  * slot bound included). Fails with KYRO_EINVAL when the params
  * would run on the grid schedule. out_splits [B] (may be NULL): splits per sequence (0 for a
  * sequence without rows). */

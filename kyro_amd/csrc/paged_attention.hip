@@ -1460,7 +1460,8 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
         const int x = (int)blockIdx.x & 7;
         const int len = plan.len;
         const int C = plan.C;
-        for (int k = (int)blockIdx.x >> 3; k < len;) {
+        const int nw = G / 8, pw = (int)blockIdx.x >> 3;  // workgroups of the lane, this one's place
+        for (int k = pw; k < len;) {
             PlanItem it = {0, 0, 0, 0, 0};
             const bool has = plan_item<HP>(a, plan, k, it);
             // Plan values come from LDS: make them scalar for the addressing that follows.
@@ -1483,13 +1484,22 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
             const int blk_end = min(si.nblk, blk_begin + C);
             if (__builtin_amdgcn_readfirstlane(has ? 1 : 0))
                 item(si, si.b * U + hp, rg, blk_begin, blk_end, nsplit, (size_t)slot * HP * RW, (size_t)RW);
-            // Claimed after the item: an atomic issued before it would sit at the head of the
-            // in-order load counter and hold up the item's first waits (measured: 437 -> 474 us
-            // on the mixed GQA 64/8 batch).
-            if (threadIdx.x == 0) s_claim = G / 8 + atomicAdd(&a.sched[x], 1);
-            __syncthreads();
-            k = s_claim;
-            __syncthreads();  // s_claim is written again after the next item
+            if (len <= 2 * nw) {
+                // At most one item per workgroup beyond its first: no claims. Item nw + i goes
+                // to workgroup nw - 1 - i, so the largest of the rest join the smallest first
+                // items (skewed prefix, chunks of 5L/4: 146.2 -> 143.0 us). With more items per
+                // workgroup the claims adapt to the rates each one sees and measured better
+                // (mixed GQA 64/8: 391 against 406 us for the same rule continued as a snake).
+                k = k < nw ? 2 * nw - 1 - pw : len;
+            } else {
+                // Claimed after the item: an atomic issued before it would sit at the head of
+                // the in-order load counter and hold up the item's first waits (measured: 437
+                // -> 474 us on the mixed GQA 64/8 batch).
+                if (threadIdx.x == 0) s_claim = nw + atomicAdd(&a.sched[x], 1);
+                __syncthreads();
+                k = s_claim;
+                __syncthreads();  // s_claim is written again after the next item
+            }
         }
         // The last workgroup out resets the counters for the next launch: every other workgroup
         // has had its last claim answered before it counts itself done.

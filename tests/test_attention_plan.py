@@ -91,7 +91,7 @@ def test_a_uniform_batch_keeps_one_item_per_kv_head_group():
 
 def test_a_bound_for_another_chunk_length_is_exceeded():
     """The Llama-2-7B batch's context lengths (B 16, ctx 512-2048, 5 rows) under GQA 32/8, planned
-    with chunks of L/2, need more slots than a bound derived for the library's 3L/2 allows: the
+    with chunks of L/2, need more slots than a bound derived for the library's 5L/4 allows: the
     check above has the power to catch a plan/bound mismatch (one once wrote past the workspace),
     and the shared chunk constant keeps them consistent."""
     ctx = wl.rng(0, wl.S_CTX).integers(512, 2049, size=16)
