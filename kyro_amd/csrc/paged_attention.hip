@@ -459,7 +459,7 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //  * work of sequence b: W_b = kv head groups x row groups x blocks; per-workgroup share
 //    L = ceil(sum W / grid);
 //  * chunk C = L when no sequence is longer than L (nothing splits, so a uniform batch keeps one
-//    item per (sequence, kv head group)), else ceil(L x kPlanChunkQuarters / 4) (3L / 2), within
+//    item per (sequence, kv head group)), else ceil(L x kPlanChunkQuarters / 4) (5L / 4), within
 //    [kPlanMinChunk, max chunk];
 //  * a longer sequence splits into chunks of C blocks from its start, the last one shorter;
 //  * item groups (sequence, chunk, kv head group) come in two phases: first every chunk but the
@@ -471,9 +471,11 @@ __device__ __forceinline__ void stage_block_ids(const AttnArgs& a, const SeqInfo
 //  * item groups are dealt to 8 lanes, one per XCD, in a snake (lanes 0..7, then 7..0), which
 //    keeps the lanes' totals even; the row groups of an item group take consecutive positions of
 //    one lane, so they run together on one XCD and share its L2;
-//  * a workgroup takes one item of its XCD's lane at a time, the next unclaimed one (a counter
-//    per lane), so the workgroups of an XCD share its lane's items greedily, largest first. Each
-//    workgroup keeps only its own lane's item counts.
+//  * a workgroup takes one item of its XCD's lane at a time: first item w / 8; then, when the
+//    lane has at most two items per workgroup, item 2 nw - 1 - w / 8 (nw workgroups a lane: the
+//    largest of the rest go to the smallest first items, no claims); otherwise the next
+//    unclaimed one (a counter per lane), so the workgroups of an XCD share its lane's items
+//    greedily, largest first. Each workgroup keeps only its own lane's item counts.
 struct PlanLds {
     alignas(16) uint32_t key[kPlanMaxSeqs];  // by sequence: (last chunk << 16) | (0xffff - b); larger first
     // By sequence:
@@ -1453,9 +1455,10 @@ __device__ __forceinline__ void mfma_schedule(const AttnArgs& a, Item&& item) {
         const int G = a.plan_grid;  // a multiple of 8
         const int U = a.Hkv / HP;
         // Workgroup w works on lane x = w % 8, the items dealt to its XCD: first the lane's item
-        // k = w / 8, then whichever item of the lane is next unclaimed when it becomes free. The
-        // G / 8 workgroups of an XCD thus take the lane's items largest first, greedily, and the
-        // row groups of one item group (consecutive on the lane) run together and share its L2.
+        // k = w / 8, then (below) one assigned item or whichever item of the lane is next
+        // unclaimed when it becomes free. The G / 8 workgroups of an XCD thus take the lane's
+        // items largest first, and the row groups of one item group (consecutive on the lane)
+        // run together and share its L2.
         __shared__ int s_claim;
         const int x = (int)blockIdx.x & 7;
         const int len = plan.len;
