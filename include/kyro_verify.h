@@ -84,8 +84,9 @@ int kyro_ctx_set_stream(kyro_ctx ctx, void* hip_stream);
  * and allocates a larger one; kernels captured into a HIP graph before that point would then
  * address freed memory. A caller that captures calls into a graph should reserve the largest
  * arena those calls need first (or re-capture after a growth). The balanced attention schedule
- * also keeps small counters in the context that every launch returns to zero, so its launches
- * replay from a graph as they run eagerly. */
+ * and the one-launch decode sampler (kyro_sample_tokens without processors, top-k or top-p) also
+ * keep small counters in the context that every launch returns to zero, so their launches replay
+ * from a graph as they run eagerly. */
 int kyro_ctx_reserve(kyro_ctx ctx, size_t bytes);
 
 /* Waits for all work queued on the context's stream, then reports latched device errors. */
