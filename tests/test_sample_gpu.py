@@ -93,6 +93,44 @@ def test_one_launch_rows_repeat_and_change_shape(gpu):
         assert np.array_equal(got, again)
 
 
+def test_one_launch_pass_replays_from_a_graph(gpu):
+    """The one-launch pass captured in a HIP graph after an eager call on the same stream (the
+    arena already large enough): its per-row counters return to zero in every launch, so each
+    replay, with eager calls of another shape and synchronisations in between, gives the eager
+    tokens, which match the oracle."""
+    rng = np.random.default_rng(41)
+    B, V = 64, 128256
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    T = np.where(np.arange(B) % 4 == 0, 0.0, 0.8).astype(np.float32)
+    u = rng.random(B).astype(np.float32)
+    x2 = (rng.standard_normal((5, 32000)) * 3).astype(np.float32)
+    T2, u2 = np.full(5, 0.7, np.float32), rng.random(5).astype(np.float32)
+    exp = run_both(x, T, u, gpu)
+    dx, dT, du = torch.from_numpy(x).to(gpu), torch.from_numpy(T).to(gpu), torch.from_numpy(u).to(gpu)
+    dx2, dT2, du2 = torch.from_numpy(x2).to(gpu), torch.from_numpy(T2).to(gpu), torch.from_numpy(u2).to(gpu)
+    procs = kyro_amd.sampling.Processors(B, V, gpu)
+    procs2 = kyro_amd.sampling.Processors(5, 32000, gpu)
+    s = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(s):
+        eager = kyro_amd.sample_tokens_async(dx, dT, du, processors=procs).clone()
+        eager2 = kyro_amd.sample_tokens_async(dx2, dT2, du2, processors=procs2).clone()
+        out = torch.empty(B, dtype=torch.int32, device=gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(eager.cpu().numpy().astype(np.uint32), exp)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        kyro_amd.sample_tokens_async(dx, dT, du, processors=procs, out=out)
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        with torch.cuda.stream(s):
+            again = kyro_amd.sample_tokens_async(dx2, dT2, du2, processors=procs2)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager2)
+
+
 def test_ties_follow_the_index(gpu):
     """Small integer logits: many equal values, so top-k boundaries and the descending order
     depend on the tie rule (lower index first)."""
