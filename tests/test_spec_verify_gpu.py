@@ -226,3 +226,51 @@ def test_rejection_only_b8_matches_golden_fixture(gpu):
         "q_draft": np.array([[np.nan if v is None else v for v in r] for r in g["q_draft"]]),
     }
     h.assert_verify_parity(res, case, fixture)
+
+
+def test_verify_step_replays_from_a_graph(gpu):
+    """One verify step (attention on the grid schedule, then acceptance with a window of 2 so
+    that the decide and tail passes run) captured in a HIP graph after eager calls on the same
+    stream: every replay, with an eager step of another shape and synchronisations in between,
+    gives the eager outputs bit for bit, and those match the oracle."""
+    acase = wl.make_attention_case(context_lens=[1500, 300, 2048, 977, 64, 1024, 1800, 512], q_lens=[8] * 8,
+                                   num_heads=32, num_kv_heads=8, dtype="bf16", seed=51)
+    vcase = wl.make_verify_case(batch=8, kmax=7, vocab=32000, target_sigma=2.5, noise_sigma=0.4,
+                                temperature=0.8, num_draft=np.array([7, 7, 3, 0, 7, 5, 7, 7]), seed=52)
+    other_v = wl.make_verify_case(batch=3, kmax=4, vocab=5000, target_sigma=2.0, noise_sigma=0.8,
+                                  temperature=1.0, num_draft=np.array([4, 2, 4]), seed=53)
+    ta = h.attention_tensors(acase, gpu)
+    tv = h.verify_tensors(vcase, gpu)
+    to = h.verify_tensors(other_v, gpu)
+    attn = kyro_amd.PagedAttention(16, 32, 128, 8)
+    aargs = (ta["query"], ta["key_cache"], ta["value_cache"], ta["block_table"], ta["context_lens"])
+
+    def step(att_out, vout):
+        attn.forward_async(*aargs, q_start_loc=ta["q_start_loc"], max_q_len=8, out=att_out)
+        return kyro_amd.speculative.verify_drafts_async(**tv, window=2, out=vout)
+
+    s = torch.cuda.Stream(gpu)
+    with torch.cuda.stream(s):
+        att_e = torch.empty(ta["query"].shape, dtype=torch.float32, device=gpu)
+        v_e = step(att_e, None)
+        other_e = kyro_amd.speculative.verify_drafts_async(**to, window=1)
+        att_g = torch.empty_like(att_e)
+        v_out = (torch.empty_like(v_e.accepted), torch.empty_like(v_e.tokens))
+    torch.cuda.synchronize()
+    h.assert_attention_close(att_e, acase, h.oracle_attention(acase), h.ATOL_BF16)
+    h.assert_verify_parity(v_e, vcase, h.oracle_verify(vcase), max_exempt=1)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        step(att_g, v_out)
+    for _ in range(3):
+        att_g.zero_()
+        v_out[0].zero_()
+        v_out[1].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(att_g, att_e)
+        assert torch.equal(v_out[0], v_e.accepted) and torch.equal(v_out[1], v_e.tokens)
+        with torch.cuda.stream(s):
+            again = kyro_amd.speculative.verify_drafts_async(**to, window=1)
+        torch.cuda.synchronize()
+        assert torch.equal(again.accepted, other_e.accepted) and torch.equal(again.tokens, other_e.tokens)
