@@ -124,9 +124,10 @@ typedef enum kyro_attn_path {
  * same kv head, or by another sequence whose table holds the same block) then comes from HBM
  * again instead of L2.
  *   AUTO:   streaming when each slab is read by one workgroup, i.e. a kv head's query rows
- *           (GQA group x max_q_len) fit one row group (16, 32, or 64 rows for bf16 caches);
- *           cached otherwise. With 64-row groups the choice is made per sequence: those whose
- *           rows fit one group stream. Right when no two sequences of the batch share a block.
+ *           (GQA group x max_q_len) fit one row group (16, 32, 64 or 80 rows for bf16
+ *           caches); cached otherwise. With 64- and 80-row groups the choice is made per
+ *           sequence: those whose rows fit one group stream. Right when no two sequences of the
+ *           batch share a block.
  *   SHARED: cached loads; for tables that share blocks between sequences (prefix caching;
  *           kyro_bm_write_tables reports it).
  *   STREAM: streaming loads regardless. */

@@ -33,6 +33,18 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // Cross-lane moves. xor 16 / xor 32 swap the 16-lane rows of a wave64.
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// Max over the four 16-lane rows of a wave64 (lanes l, l ^ 16, l ^ 32 and l ^ 48), in every lane.
+// permlane16_swap(v, v) returns {v of lane l with rows 1 and 3 replaced by rows 0 and 2, v with
+// rows 0 and 2 replaced by rows 1 and 3}, so the max of the pair is the max over rows 2i, 2i + 1;
+// permlane32_swap does the same for the halves. Two VALU swaps where __shfl_xor makes two round
+// trips through the LDS unit.
+__device__ __forceinline__ float max_over_rows(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Sum over each 16-lane row with DPP; every lane of the row gets the row total.
 __device__ __forceinline__ float row16_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]

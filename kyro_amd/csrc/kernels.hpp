@@ -27,7 +27,7 @@ constexpr int kLoadCached = 0;
 constexpr int kLoadStream = 2;
 // Not a hardware policy: the kernel picks kLoadStream or kLoadCached per unit.
 constexpr int kLoadPerUnit = -1;
-// AttnArgs::stream_kv value that selects kLoadPerUnit (four-tile kernel only).
+// AttnArgs::stream_kv value that selects kLoadPerUnit (four- and five-tile kernels only).
 constexpr int kKvPerUnit = 2;
 
 // Upper bound on the blocks one attention workgroup streams (its split); the block ids of a
@@ -60,6 +60,7 @@ struct AttnArgs {
     int ugroups;       // units / hpw
     int ugroups_padded;  // ugroups rounded up to a multiple of 8 (the XCD count)
     int row_groups;    // workgroups per (unit group, split), each covering rows_per_group rows
+    int rows_per_group;  // query rows of a row group (MFMA: 16, 32, 64 or 80; vector: 8)
     int stream_kv;     // MFMA kernel: K/V loads with kLoadStream (1), kLoadCached (0) or per unit (kKvPerUnit)
     // Balanced schedule (MFMA kernel, automatic splits): a persistent grid of plan_grid
     // workgroups computes per-sequence splits from the context lengths and walks the work items
@@ -151,14 +152,27 @@ constexpr int kMaxHeadDim = 256;
 constexpr int kVectorRowsPerGroup = 8;
 // MFMA kernels: one 16-row tile, two (32 rows), or for bf16 units of more than 32 rows four
 // (kMfmaManyRows: one kv head per workgroup, Q read from LDS, only the unit's tiles computed),
-// so that a unit of up to 64 rows streams its K/V once instead of once per 32-row group. (Five
-// tiles need more than the 512 registers a wave can hold.)
+// so that a unit of up to 64 rows streams its K/V once instead of once per 32-row group.
+// Five tiles (kMfmaWideRows) where they take fewer row groups than four and the batch's
+// average unit (total_rows / seqs rows per kv head) fills more than half of what the last
+// 64-row group would hold: GQA 64/8 with 8 drafts on every sequence (72 rows a unit) then
+// streams each unit's K/V once instead of twice (B 64, ctx 4096: 331 -> 235 us). The five-tile
+// kernel copies about 1.7x as many values through AGPRs per block pair as the four-tile one (both
+// hold more than the 256 VGPRs a wave can address), so a batch with few such units keeps four
+// (mixed GQA 64/8, 0-8 drafts: 385 us with four, 396 with five).
 // Head dims other than 128 take at most two tiles (one at 256: its K/V pairs and accumulators
 // fill the register file).
 constexpr int kMfmaManyRows = 64;
-__host__ __device__ inline int mfma_rows_per_group(int rows, bool bf16, int D) {
+constexpr int kMfmaWideRows = 80;
+inline int mfma_rows_per_group(int rows, bool bf16, int D, long long total_rows, int seqs) {
     if (D > 128) return 16;
-    return rows <= 16 ? 16 : (rows <= 32 || !bf16 || D != 128) ? 32 : kMfmaManyRows;
+    if (rows <= 16) return 16;
+    if (rows <= 32 || !bf16 || D != 128) return 32;
+    const int groups4 = (rows + kMfmaManyRows - 1) / kMfmaManyRows;
+    const int groups5 = (rows + kMfmaWideRows - 1) / kMfmaWideRows;
+    const long long lo = (long long)kMfmaManyRows * (groups4 - 1);  // rows before the last 64-row group
+    const bool wide = groups5 < groups4 && 2 * total_rows > (long long)seqs * (rows + lo);
+    return wide ? kMfmaWideRows : kMfmaManyRows;
 }
 
 // Head dims the bf16 MFMA kernel is built for: every multiple of 32 from 64 to 256, and 80 and 112

@@ -913,8 +913,7 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
             float mx = sv[0];
 #pragma unroll
             for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sv[i]);
-            mx = fmaxf(mx, shfl_xor_f(mx, 16));
-            mx = fmaxf(mx, shfl_xor_f(mx, 32));
+            mx = max_over_rows(mx);
             const float m_new = fmaxf(m[nt], mx * c);
             const float mref = (m_new == kNegInf) ? 0.f : m_new;
             const float alpha = fast_exp2(m[nt] - mref);
@@ -1311,8 +1310,7 @@ __device__ __forceinline__ void mfma_item_f32(const AttnArgs& a, Frame<NTW * 16,
                     }
                 }
                 float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-                mx = fmaxf(mx, shfl_xor_f(mx, 16));
-                mx = fmaxf(mx, shfl_xor_f(mx, 32));
+                mx = max_over_rows(mx);
                 const float m_new = fmaxf(m[nt], mx * c);
                 const float mref = (m_new == kNegInf) ? 0.f : m_new;
                 const float alpha = fast_exp2(m[nt] - mref);
@@ -1815,7 +1813,7 @@ __global__ __launch_bounds__(kThreads) void attn_vector_kernel(AttnArgs a) {
 template <int D, int DR = D>
 hipError_t launch_mfma_hd(const AttnArgs& a, const dim3 grid, hipStream_t stream) {
     const dim3 block(kThreads);
-    const int rpg = mfma_rows_per_group(a.rows_cap, true, DR);
+    const int rpg = a.rows_per_group;
 #define KYRO_HD_LAUNCH(NT, POL, PLAN)                                                           \
     {                                                                                           \
         if (a.hpw == 2) attn_mfma_kernel<NT, 2, POL, PLAN, D, DR><<<grid, block, 0, stream>>>(a); \
@@ -1893,7 +1891,7 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
         return (a.D == 112 || a.D == 160 || a.D == 192 || a.D == 224) ? launch_paged_attention_mfma_hd_wide(a, stream)
                                                                        : launch_paged_attention_mfma_hd(a, stream);
     if (path == ATTN_KERNEL_MFMA) {
-        const int rpg = mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
+        const int rpg = a.rows_per_group;
         const bool rows16 = rpg == 16;
 #define KYRO_MFMA_LAUNCH2(K, POL, PLAN)                                                     \
         if (a.hpw == 2) {                                                                   \
@@ -1905,14 +1903,21 @@ hipError_t launch_paged_attention(const AttnArgs& a, int path, hipStream_t strea
         }
 #define KYRO_MFMA_LAUNCH(POL, PLAN)                                                         \
         if (a.dtype_bf16) {                                                                 \
-            if (rpg == kMfmaManyRows) attn_mfma_kernel<kMfmaManyRows / 16, 1, POL, PLAN><<<grid, block, 0, stream>>>(a); \
+            if (rpg == kMfmaWideRows) attn_mfma_kernel<kMfmaWideRows / 16, 1, POL, PLAN><<<grid, block, 0, stream>>>(a); \
+            else if (rpg == kMfmaManyRows) attn_mfma_kernel<kMfmaManyRows / 16, 1, POL, PLAN><<<grid, block, 0, stream>>>(a); \
             else { KYRO_MFMA_LAUNCH2(attn_mfma_kernel, POL, PLAN) }                         \
         } else {                                                                            \
             KYRO_MFMA_LAUNCH2(attn_mfma_f32_kernel, POL, PLAN)                              \
         }
-        if (a.stream_kv == kKvPerUnit) {  // four-tile kernel only (the host decides)
-            if (a.plan) attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, true><<<grid, block, 0, stream>>>(a);
-            else attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, false><<<grid, block, 0, stream>>>(a);
+        if (a.stream_kv == kKvPerUnit) {  // four- and five-tile kernels only (the host decides)
+            if (rpg == kMfmaWideRows) {
+                if (a.plan) attn_mfma_kernel<kMfmaWideRows / 16, 1, kLoadPerUnit, true><<<grid, block, 0, stream>>>(a);
+                else attn_mfma_kernel<kMfmaWideRows / 16, 1, kLoadPerUnit, false><<<grid, block, 0, stream>>>(a);
+            } else if (a.plan) {
+                attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, true><<<grid, block, 0, stream>>>(a);
+            } else {
+                attn_mfma_kernel<kMfmaManyRows / 16, 1, kLoadPerUnit, false><<<grid, block, 0, stream>>>(a);
+            }
         } else if (a.plan) {
             if (a.stream_kv) {
                 KYRO_MFMA_LAUNCH(kLoadStream, true)

@@ -251,7 +251,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
     // (vector) or 16 / 32 / 64 (MFMA) rows that stream the same K/V.
     const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA
-                                   ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16, p->head_dim)
+                                   ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16, p->head_dim,
+                                                               (long long)p->total_q * group, p->batch_size)
                                    : kyro::kVectorRowsPerGroup;
     // The MFMA kernel gives one workgroup two adjacent kv heads of a sequence when it can (two
     // waves per head): the workgroup then reads both heads' slabs of each block together, and
@@ -268,12 +269,13 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     a.ugroups = a.units / a.hpw;
     a.ugroups_padded = (a.ugroups + 7) / 8 * 8;
     a.row_groups = std::max(1, (a.rows_cap + rows_per_group - 1) / rows_per_group);
+    a.rows_per_group = rows_per_group;
     // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
     // of a kv head, or (as the caller says) other sequences holding the same blocks. The
     // four-tile kernel decides per unit under AUTO: on a ragged batch only the units with more
     // than 64 rows have a second row group.
     a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
-    if (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups > 1 && rows_per_group == kyro::kMfmaManyRows)
+    if (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups > 1 && rows_per_group >= kyro::kMfmaManyRows)
         a.stream_kv = kyro::kKvPerUnit;
 
     // Context splits: enough workgroups to cover the chip, chunks of whole slot pairs (a slot is
@@ -694,7 +696,7 @@ int kyro_paged_attention_describe(kyro_ctx ctx, const kyro_paged_attention_param
         const kyro::AttnArgs& a = s.a;
         char t[512];
         if (s.kernel == kyro::ATTN_KERNEL_MFMA) {
-            const int rpg = kyro::mfma_rows_per_group(a.rows_cap, a.dtype_bf16 != 0, a.D);
+            const int rpg = a.rows_per_group;
             const char* pol = a.stream_kv == kyro::kKvPerUnit ? "per-unit" : a.stream_kv ? "stream" : "cached";
             std::snprintf(t, sizeof t,
                           "%s<row tiles %d, kv heads per workgroup %d, K/V loads %s> schedule %s, "

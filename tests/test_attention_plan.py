@@ -12,16 +12,25 @@ import numpy as np
 import pytest
 
 from kyro_amd import workloads as wl
-from kyro_amd.attention import PagedAttention, attention_plan
+from kyro_amd.attention import PagedAttention, attention_plan, describe_attention
 
 
 def _ceil(a, b):
     return -(-a // b)
 
 
-def _rows_per_group(rows_cap):
-    """Rows per MFMA row group for bf16: one tile, two, or the four-tile kernel's 64."""
-    return 16 if rows_cap <= 16 else 32 if rows_cap <= 32 else 64
+def _rows_per_group(rows_cap, total_rows, seqs):
+    """Rows per MFMA row group for bf16 at head_dim 128: one tile, two, the four-tile kernel's
+    64, or the five-tile kernel's 80 where that takes fewer row groups (65-80, 129-160 rows) and
+    the average unit (total_rows / seqs) holds more than half of what the last 64-row group
+    would."""
+    if rows_cap <= 16:
+        return 16
+    if rows_cap <= 32:
+        return 32
+    lo = 64 * (_ceil(rows_cap, 64) - 1)
+    wide = _ceil(rows_cap, 80) < _ceil(rows_cap, 64) and 2 * total_rows > seqs * (rows_cap + lo)
+    return 80 if wide else 64
 
 
 def _random_batch(g):
@@ -62,9 +71,10 @@ def test_slot_bound_holds_over_random_batches(chunk_quarters, num_cus):
         assert info["items"] <= info["slot_bound"], (info, ctx.tolist(), ql.tolist(), hkv, group)
         worst = max(worst, info["items"] / info["slot_bound"])
         # Items are sequence x kv head group x split x row group, with the row groups of the
-        # launch's row-group size (16, 32 or 64 rows per group for the bf16 MFMA kernels; the
-        # 64-row kernel, and the 16-row one under MHA, take one kv head per workgroup).
-        rw = _rows_per_group(group * max(1, int(ql.max())))
+        # launch's row-group size (16, 32, 64 or 80 rows per group for the bf16 MFMA kernels;
+        # the 64- and 80-row kernels, and the 16-row one under MHA, take one kv head per
+        # workgroup).
+        rw = _rows_per_group(group * max(1, int(ql.max())), group * int(ql.sum()), len(ctx))
         hp = 2 if hkv % 2 == 0 and rw <= 32 and not (rw <= 16 and group == 1) else 1
         r = _ceil(ql.astype(np.int64) * group, rw)
         assert info["items"] == int(np.sum((hkv // hp) * splits.astype(np.int64) * r))
@@ -81,6 +91,23 @@ def test_slot_bound_holds_over_random_batches(chunk_quarters, num_cus):
             else:
                 assert splits[b] == _ceil(nb[b], C) and (splits[b] - 1) * C < nb[b] <= splits[b] * C
     assert worst > 0.0
+
+
+@pytest.mark.parametrize("heads,max_q_len,total_q,tiles,row_groups", [
+    ((32, 8), 8, 32, 2, 1), ((64, 8), 8, 32, 4, 1), ((64, 8), 9, 36, 5, 1), ((64, 8), 9, 35, 5, 1),
+    ((64, 8), 9, 34, 4, 2), ((64, 8), 9, 20, 4, 2), ((16, 2), 12, 48, 4, 2), ((32, 2), 9, 36, 5, 2),
+    ((32, 2), 10, 40, 5, 2), ((32, 2), 10, 36, 4, 3), ((32, 2), 11, 44, 4, 3), ((64, 8), 16, 64, 4, 2)])
+def test_row_group_size_follows_the_rows_per_kv_head(heads, max_q_len, total_q, tiles, row_groups):
+    """bf16, head_dim 128, a batch of 4: 16-row tiles per row group for GQA group x max_q_len
+    rows per kv head and total_q query rows. Five tiles where they need fewer row groups than
+    four (72, 144 and 160 rows) and the average unit holds more than half of the last 64-row
+    group's rows (GQA 64/8, max_q_len 9: 35 of 36 rows in all take five tiles, 34 four); four
+    otherwise above 32 rows. As the library reports for a launch."""
+    H, Hkv = heads
+    text = describe_attention(PagedAttention(16, H, 128, Hkv), batch=4, total_q=total_q,
+                              max_q_len=max_q_len, max_blocks_per_seq=64, num_blocks=256)
+    assert f"row tiles {tiles}," in text and f"row groups {row_groups}," in text, text
+    assert _rows_per_group(H // Hkv * max_q_len, H // Hkv * total_q, 4) == 16 * tiles
 
 
 def test_a_uniform_batch_keeps_one_item_per_kv_head_group():
