@@ -989,8 +989,8 @@ __device__ __forceinline__ void mfma_item(const AttnArgs& a, Frame<NTW * 16, D> 
                             S2[bi] = acc;
                         }
                         const bf16x8 pB = softmax_tile(nt, S2[0], S2[1], full, pb, blk0, blk1);
-                        // The V^T operands are rebuilt per tile (32 v_perm): holding all eight
-                        // across the tiles costs 32 registers the accumulators need.
+                        // The V^T operands are written per tile; the compiler builds the eight once
+                        // per block pair and keeps them for the other tiles (32 registers).
 #pragma unroll
                         for (int dt = 0; dt < T; ++dt)
                             O[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_operand(kv, dt), pB, O[dt][nt], 0, 0, 0);
