@@ -320,23 +320,24 @@ def test_block_sizes_nan_past_the_context_and_long(gpu, bs):
         h.assert_attention_close(out, case, exp, h.ATOL_BF16)
 
 
+@pytest.mark.parametrize("bs", [16, 64])
 @pytest.mark.parametrize("schedule,splits", [("grid", 1), ("grid", 3), ("auto", 0), ("balanced", 0)])
-def test_five_tile_row_groups(gpu, schedule, splits):
+def test_five_tile_row_groups(gpu, schedule, splits, bs):
     """Units of 65-80 query rows per kv head (GQA 64/8 with 8 drafts: 72 rows) take one five-tile
     row group, and units of 129-160 rows (GQA 32/2 with 9 or 10 query rows) two, when most units
     of the batch are that long; the shorter units of the same launches fill part of a group or
     none of the second. Every cache policy, on the grid with and without splits and under the
-    balanced schedule, against the oracle."""
+    balanced schedule, in 16- and 64-token blocks, against the oracle."""
     for (H, Hkv), ctx, ql in (((64, 8), [3000, 700, 50, 1200, 0, 4100, 33, 260, 1500, 17, 800, 2047, 129],
                                [9, 9, 9, 9, 9, 9, 9, 9, 9, 9, 9, 9, 3]),
                               ((32, 2), [2500, 300, 47, 900, 1, 1200], [10, 10, 9, 10, 10, 6])):
-        text = describe_attention(make_attention(16, H, 128, Hkv), batch=len(ctx), total_q=sum(ql),
+        text = describe_attention(make_attention(bs, H, 128, Hkv), batch=len(ctx), total_q=sum(ql),
                                   max_q_len=max(ql), max_blocks_per_seq=512, num_blocks=4096)
         assert "row tiles 5," in text, text
         case = wl.make_attention_case(context_lens=ctx, q_lens=ql, num_heads=H, num_kv_heads=Hkv,
-                                      dtype="bf16", seed=90 + H)
+                                      block_size=bs, dtype="bf16", seed=90 + H + bs)
         t = h.attention_tensors(case, gpu)
-        attn = make_attention(16, H, 128, Hkv)
+        attn = make_attention(bs, H, 128, Hkv)
         exp = h.oracle_attention(case)
         for reuse in ("auto", "shared", "stream"):
             for out_dtype in (torch.float32, torch.bfloat16):
