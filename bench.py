@@ -520,7 +520,9 @@ def shape_sweep_workload(kind, warmup, steps):
     224 and 256 with 16-token blocks; AUTO takes the MFMA kernel at each of them)
     or other block sizes ("block-sizes": 8, 16, 32, 64 at head_dim 128; AUTO takes the MFMA
     kernel at every multiple of 16, the vector kernel at 8), AUTO and the vector kernel, each on
-    its algorithmic bytes."""
+    its algorithmic bytes; or ("row-tiles") GQA 64/8 at head_dim 128 with 1, 2, 4, 8 and 9 query
+    rows per sequence (8 to 72 rows per kv head: the one-, two-, four- and five-tile MFMA
+    kernels), AUTO only."""
     import torch
 
     import kyro_amd
@@ -528,29 +530,35 @@ def shape_sweep_workload(kind, warmup, steps):
     from kyro_amd.attention import describe_attention
 
     dev = torch.device("cuda", 0)
-    res = {"workload": kind, "shape": "GQA 32/8, batch 64, ctx 4096, 8 query rows, bf16 KV and out"}
-    points = ([(D, 16) for D in (64, 80, 96, 112, 128, 160, 192, 224, 256)] if kind == "head-dims"
-              else [(128, bs) for bs in (8, 16, 32, 64)])
-    for D, bs in points:
-        case = wl.make_attention_case(context_lens=[4096] * 64, q_lens=[8] * 64, num_heads=32, num_kv_heads=8,
-                                      head_dim=D, block_size=bs, dtype="bf16", seed=D + bs)
+    H = 64 if kind == "row-tiles" else 32
+    res = {"workload": kind, "shape": f"GQA {H}/8, batch 64, ctx 4096, "
+           + ("1-9" if kind == "row-tiles" else "8") + " query rows, bf16 KV and out"}
+    if kind == "head-dims":
+        points = [(D, 16, 8) for D in (64, 80, 96, 112, 128, 160, 192, 224, 256)]
+    elif kind == "block-sizes":
+        points = [(128, bs, 8) for bs in (8, 16, 32, 64)]
+    else:
+        points = [(128, 16, q) for q in (1, 2, 4, 8, 9)]
+    for D, bs, ql in points:
+        case = wl.make_attention_case(context_lens=[4096] * 64, q_lens=[ql] * 64, num_heads=H, num_kv_heads=8,
+                                      head_dim=D, block_size=bs, dtype="bf16", seed=D + bs + ql)
         up = lambda x: torch.from_numpy(x).view(torch.bfloat16).to(dev)  # noqa: E731
         t = dict(q=up(case.query), kc=up(case.key_cache), vc=up(case.value_cache),
                  table=torch.from_numpy(case.block_table).to(dev), ctx=torch.from_numpy(case.context_lens).to(dev),
                  qs=torch.from_numpy(case.q_start_loc).to(dev))
-        attn = kyro_amd.PagedAttention(bs, 32, D, 8)
+        attn = kyro_amd.PagedAttention(bs, H, D, 8)
         out = torch.empty(t["q"].shape, dtype=torch.bfloat16, device=dev)
         nbytes = case.kv_bytes() + case.q_out_bytes(2)
         entry = {"algorithmic_bytes": nbytes}
-        for path in ("auto", "vector"):
+        for path in (("auto",) if kind == "row-tiles" else ("auto", "vector")):
             us = _median_us(lambda: attn.forward_async(
-                t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"], max_q_len=8,
+                t["q"], t["kc"], t["vc"], t["table"], t["ctx"], q_start_loc=t["qs"], max_q_len=ql,
                 out_dtype=torch.bfloat16, out=out, path=path), warmup, steps)
             entry[path] = {"us": us, "GB_s": nbytes / us / 1e3, "frac": nbytes / us / 1e3 / PEAK_HBM_GBS,
-                           "launch": describe_attention(attn, batch=64, total_q=512, max_q_len=8,
+                           "launch": describe_attention(attn, batch=64, total_q=64 * ql, max_q_len=ql,
                                                         max_blocks_per_seq=case.block_table.shape[1],
                                                         num_blocks=case.key_cache.shape[0], path=path, device=0)}
-        res[f"d{D}" if kind == "head-dims" else f"bs{bs}"] = entry
+        res[{"head-dims": f"d{D}", "block-sizes": f"bs{bs}"}.get(kind, f"q{ql}")] = entry
         del t, out
         torch.cuda.empty_cache()
     print(json.dumps(res), flush=True)
@@ -583,13 +591,13 @@ def main():
     ap.add_argument("--workload", default="llama3-8b",
                     choices=["llama3-8b", "mha-llama2-7b", "rejection-b8", "skewed-prefix",
                              "mixed-llama3-70b", "kv-append", "block-tables", "decode-sample", "ngram-draft",
-                             "head-dims", "block-sizes", "others"],
+                             "head-dims", "block-sizes", "row-tiles", "others"],
                     help="llama3-8b (default) prints the benchmark line; the others print one "
                          "informational line each (attention and sampler on their algorithmic bytes)")
     args = ap.parse_args()
     if args.workload != "llama3-8b":
         names = (["mha-llama2-7b", "rejection-b8", "skewed-prefix", "mixed-llama3-70b", "kv-append", "block-tables",
-                  "decode-sample", "ngram-draft", "head-dims", "block-sizes"] if args.workload == "others"
+                  "decode-sample", "ngram-draft", "head-dims", "block-sizes", "row-tiles"] if args.workload == "others"
                  else [args.workload])
         for n in names:
             if n == "kv-append":
@@ -600,7 +608,7 @@ def main():
                 decode_sample_workload(args.warmup, args.steps)
             elif n == "ngram-draft":
                 ngram_draft_workload(args.warmup, args.steps)
-            elif n in ("head-dims", "block-sizes"):
+            elif n in ("head-dims", "block-sizes", "row-tiles"):
                 shape_sweep_workload(n, args.warmup, args.steps)
             else:
                 other_workload(n, args.warmup, args.steps)
