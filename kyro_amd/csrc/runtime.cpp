@@ -249,7 +249,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     a.scale_log2 = (float)(scale * 1.4426950408889634);
     a.units = p->batch_size * p->num_kv_heads;
     // Row groups: a unit's group * max_q_len query rows are spread over workgroups of 8
-    // (vector) or 16 / 32 / 64 (MFMA) rows that stream the same K/V.
+    // (vector) or 16 / 32 / 64 / 80 (MFMA) rows that stream the same K/V. The five-tile choice
+    // reads the average rows per kv head from total_q (an upper bound when q has padding rows).
     const int rows_per_group = kernel == kyro::ATTN_KERNEL_MFMA
                                    ? kyro::mfma_rows_per_group(a.rows_cap, p->dtype == KYRO_BF16, p->head_dim,
                                                                (long long)p->total_q * group, p->batch_size)
@@ -272,8 +273,8 @@ int attention_setup(const kyro_paged_attention_params* p, bool have_q_start, int
     a.rows_per_group = rows_per_group;
     // Streaming K/V loads unless another workgroup reads the same slabs: the other row groups
     // of a kv head, or (as the caller says) other sequences holding the same blocks. The
-    // four-tile kernel decides per unit under AUTO: on a ragged batch only the units with more
-    // than 64 rows have a second row group.
+    // four- and five-tile kernels decide per unit under AUTO: on a ragged batch only the units
+    // with more rows than a group holds have a second row group.
     a.stream_kv = p->kv_reuse == KYRO_KV_REUSE_STREAM || (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups == 1);
     if (p->kv_reuse == KYRO_KV_REUSE_AUTO && a.row_groups > 1 && rows_per_group >= kyro::kMfmaManyRows)
         a.stream_kv = kyro::kKvPerUnit;
