@@ -448,14 +448,14 @@ def test_balanced_schedule_large_batches(gpu, batch):
     h.assert_attention_close(out2, case2, h.oracle_attention(case2, [0, 1023, 1024]), h.ATOL_BF16)
 
 
-@pytest.mark.parametrize("H", [32, 64])
-def test_balanced_schedule_replays_from_a_graph(gpu, H):
+@pytest.mark.parametrize("H,ql", [(32, (8, 8, 3, 1, 5, 8)), (64, (8, 8, 3, 1, 5, 8)), (64, (9, 9, 9, 9, 9, 8))])
+def test_balanced_schedule_replays_from_a_graph(gpu, H, ql):
     """A balanced launch (plan, per-lane claim counters, combine pass) captured in a HIP graph
     after an eager call on the same stream (so the arena is already large enough): every replay,
     with eager launches of another shape and synchronisations in between, equals the eager
     result bit for bit. GQA 32/8 runs the two-tile kernel, GQA 64/8 (up to 64 rows per kv head)
-    the four-tile one."""
-    case = wl.make_attention_case(context_lens=[3000, 17, 0, 900, 5000, 33], q_lens=[8, 8, 3, 1, 5, 8],
+    the four-tile one, and GQA 64/8 with 72 rows on most sequences the five-tile one."""
+    case = wl.make_attention_case(context_lens=[3000, 17, 0, 900, 5000, 33], q_lens=list(ql),
                                   num_heads=H, num_kv_heads=8, dtype="bf16", seed=23)
     other = wl.make_attention_case(context_lens=[700, 2100], q_lens=[2, 3], num_heads=H, num_kv_heads=8,
                                    dtype="bf16", seed=24)
@@ -473,7 +473,7 @@ def test_balanced_schedule_replays_from_a_graph(gpu, H):
     h.assert_attention_close(eager, case, h.oracle_attention(case), h.ATOL_BF16)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", out=out, max_q_len=8)
+        attn.forward_async(*args, q_start_loc=t["q_start_loc"], schedule="balanced", out=out, max_q_len=max(ql))
     for _ in range(4):
         out.zero_()
         g.replay()
